@@ -1,0 +1,62 @@
+// Device helpers shared by the kernels: fp16 decode, wavefront reductions, argmax keys.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace tfk {
+
+// IEEE half bits -> float (v_cvt_f32_f16: exact for every half value).
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    _Float16 v;
+    const uint16_t b = (uint16_t)bits16;
+    __builtin_memcpy(&v, &b, 2);
+    return (float)v;
+}
+
+// Unsigned byte n of a dword as float (v_cvt_f32_ubyte{0..3}).
+__device__ __forceinline__ float ub0(uint32_t w) { return (float)(w & 0xFFu); }
+__device__ __forceinline__ float ub1(uint32_t w) { return (float)((w >> 8) & 0xFFu); }
+__device__ __forceinline__ float ub2(uint32_t w) { return (float)((w >> 16) & 0xFFu); }
+__device__ __forceinline__ float ub3(uint32_t w) { return (float)(w >> 24); }
+
+// Butterfly sums: partners add the same two values, so every lane ends with the
+// bit-identical total and the result does not depend on scheduling.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long w = __shfl_xor(v, o);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// Argmax key: unsigned order of the key follows the float order of the value (with
+// -0 folded onto +0, as `>` treats them equal) and, for equal values, the lower index
+// (sample_greedy keeps the first maximum, sampler.cpp:8-13).
+__device__ __forceinline__ unsigned long long argmax_key(float v, int64_t idx) {
+    uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)b << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+}  // namespace tfk

@@ -1,0 +1,985 @@
+// libtf_hip: the C ABI of include/tf_hip.h over the gfx950 kernels.
+//
+// A context owns the weights (repacked into the DevMat layout), the fp32 KV cache,
+// the activations and one captured hipGraph for a decode step. The graph reads the
+// token and position from the device control block (Ctl), so the same graph serves
+// decode (token staged in the token history), prefill (all prompt tokens staged,
+// replayed once per token with attention limited to the prompt, as attn_prefill
+// does) and the greedy loop (token = previous argmax, no host round trip).
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "formats.hpp"
+#include "tf_internal.hpp"
+
+using namespace tfk;
+
+namespace {
+
+constexpr int kNumClasses = 7;  // embed, qkv, attention, wo, gate/up, down, lm_head
+const char* const kClassNames[kNumClasses] = {"embed", "qkv_gemv", "attention", "wo_gemv",
+                                              "gateup_gemv", "down_gemv", "lmhead_gemv"};
+
+struct Prof {
+    std::vector<hipEvent_t> ev;  // pairs per launch
+    std::vector<int> cls;
+    std::vector<double> bytes;
+};
+
+}  // namespace
+
+struct tf_hip_ctx {
+    int device = 0;
+    hipStream_t st = nullptr;
+    tf_hip_hparams hp{};
+    int H = 0, KVd = 0;  // n_head*head_dim, n_kv_head*head_dim
+    std::vector<DevMat> mats;
+    std::vector<float*> vecs;
+    std::vector<int64_t> vec_len;
+    std::vector<void*> allocs;
+    float* kc = nullptr;
+    float* vc = nullptr;
+    size_t kv_layer = 0;  // floats per layer
+    float* rope_cos = nullptr;
+    float* rope_sin = nullptr;
+    bool rope_set = false;
+    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr;
+    float *logits = nullptr, *taps = nullptr, *part_o = nullptr, *part_ml = nullptr;
+    unsigned* counters = nullptr;
+    Ctl* ctl = nullptr;
+    Ctl* ctl_host = nullptr;      // pinned staging
+    int32_t* hist = nullptr;      // device token per position
+    int32_t* tok_host = nullptr;  // pinned staging [max_seq]
+    int S = 1;                    // attention splits per kv head
+    int pos = 0;
+    bool have_logits = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    float last_ms = 0;
+    int last_steps = 0;
+    std::string err;
+};
+
+namespace {
+
+int fail(tf_hip_ctx* c, int code, const std::string& msg) {
+    if (c) c->err = msg;
+    return code;
+}
+
+#define HIPCHK(ctx, call)                                                                      \
+    do {                                                                                       \
+        hipError_t e_ = (call);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return fail(ctx, e_ == hipErrorOutOfMemory ? TF_HIP_ENOMEM : TF_HIP_EDEVICE,      \
+                        std::string(#call) + ": " + hipGetErrorString(e_));                    \
+    } while (0)
+
+template <typename T>
+int dalloc(tf_hip_ctx* c, T** p, size_t bytes) {
+    void* d = nullptr;
+    const hipError_t e = hipMalloc(&d, bytes ? bytes : 16);
+    if (e != hipSuccess)
+        return fail(c, TF_HIP_ENOMEM, "hipMalloc(" + std::to_string(bytes) + "): " + hipGetErrorString(e));
+    c->allocs.push_back(d);
+    *p = (T*)d;
+    return 0;
+}
+
+size_t blck_bytes(int t) {
+    switch (t) {
+        case TF_HIP_TYPE_F32: return 4;
+        case TF_HIP_TYPE_F16: return 2;
+        case TF_HIP_TYPE_Q4_0: return 18;
+        case TF_HIP_TYPE_Q4_1: return 20;
+        case TF_HIP_TYPE_Q8_0: return 34;
+        case TF_HIP_TYPE_Q6_K: return 210;
+    }
+    return 0;
+}
+int blck_elems(int t) {
+    switch (t) {
+        case TF_HIP_TYPE_Q4_0:
+        case TF_HIP_TYPE_Q4_1:
+        case TF_HIP_TYPE_Q8_0: return 32;
+        case TF_HIP_TYPE_Q6_K: return 256;
+        case TF_HIP_TYPE_F32:
+        case TF_HIP_TYPE_F16: return 1;
+    }
+    return 0;
+}
+
+// Row length constraints of the backend layout (16-byte lane steps).
+bool row_ok(int t, int64_t K) {
+    if (blck_elems(t) == 0 || K <= 0) return false;
+    switch (t) {
+        case TF_HIP_TYPE_F32: return K % 4 == 0;
+        case TF_HIP_TYPE_F16: return K % 8 == 0;
+        case TF_HIP_TYPE_Q6_K: return K % 256 == 0;
+        default: return K % 32 == 0;
+    }
+}
+
+size_t gguf_nbytes(int t, int64_t K, int64_t N) { return (size_t)N * (size_t)(K / blck_elems(t)) * blck_bytes(t); }
+
+// Allocates the streams of m and converts the GGUF bytes (already on the device) into them.
+hipError_t make_devmat(int t, int64_t K, int64_t N, const uint8_t* d_raw, DevMat& m, std::vector<void*>& owned,
+                       hipStream_t st) {
+    m.type = t;
+    m.K = K;
+    m.N = N;
+    m.gguf_bytes = gguf_nbytes(t, K, N);
+    auto al = [&](uint8_t** p, size_t n) -> hipError_t {
+        void* d = nullptr;
+        hipError_t e = hipMalloc(&d, n ? n : 16);
+        if (e == hipSuccess) owned.push_back(d);
+        *p = (uint8_t*)d;
+        return e;
+    };
+    hipError_t e = hipSuccess;
+    switch (t) {
+        case TF_HIP_TYPE_F32:
+        case TF_HIP_TYPE_F16:
+            if ((e = al(&m.q, m.gguf_bytes)) != hipSuccess) return e;
+            return hipMemcpyAsync(m.q, d_raw, m.gguf_bytes, hipMemcpyDeviceToDevice, st);
+        case TF_HIP_TYPE_Q8_0:
+            if ((e = al(&m.q, (size_t)N * K)) != hipSuccess) return e;
+            if ((e = al(&m.s, (size_t)N * (K / 32) * 2)) != hipSuccess) return e;
+            break;
+        case TF_HIP_TYPE_Q4_0:
+            if ((e = al(&m.q, (size_t)N * K / 2)) != hipSuccess) return e;
+            if ((e = al(&m.s, (size_t)N * (K / 32) * 2)) != hipSuccess) return e;
+            break;
+        case TF_HIP_TYPE_Q4_1:
+            if ((e = al(&m.q, (size_t)N * K / 2)) != hipSuccess) return e;
+            if ((e = al(&m.s, (size_t)N * (K / 32) * 4)) != hipSuccess) return e;
+            break;
+        case TF_HIP_TYPE_Q6_K:
+            if ((e = al(&m.q, (size_t)N * K / 2)) != hipSuccess) return e;
+            if ((e = al(&m.q2, (size_t)N * K / 4)) != hipSuccess) return e;
+            if ((e = al(&m.s, (size_t)N * (K / 16))) != hipSuccess) return e;
+            if ((e = al(&m.s2, (size_t)N * (K / 256) * 2)) != hipSuccess) return e;
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return launch_repack(t, d_raw, K, N, m, st);
+}
+
+// Rows per wavefront: as many as keep at least two workgroups per CU busy.
+int pick_rows(int64_t n_rows) {
+    const int64_t want = 2LL * device_cu_count() * kWavesPerBlock;
+    if (n_rows >= 4 * want) return 4;
+    if (n_rows >= 2 * want) return 2;
+    return 1;
+}
+
+void add_seg(GemvArgs& a, const DevMat& m, float* y, const float* bias, float* tap, int R) {
+    GemvSeg& s = a.seg[a.n_seg++];
+    s.a = m;
+    s.y = y;
+    s.bias = bias;
+    s.tap = tap;
+    s.groups = gemv_groups(m.N, R);
+    a.total_groups += s.groups;
+}
+
+const DevMat& mat(const tf_hip_ctx* c, int slot) { return c->mats[(size_t)slot]; }
+const float* vec(const tf_hip_ctx* c, int slot) { return c->vecs[(size_t)slot]; }
+
+const DevMat& output_mat(const tf_hip_ctx* c) {
+    return mat(c, TF_HIP_SLOT_OUTPUT).valid() ? mat(c, TF_HIP_SLOT_OUTPUT) : mat(c, TF_HIP_SLOT_TOKEN_EMBD);
+}
+
+int check_ready(tf_hip_ctx* c) {
+    auto need_m = [&](int slot, const char* what) -> bool {
+        if (!mat(c, slot).valid()) {
+            c->err = std::string("tensor not uploaded: ") + what;
+            return false;
+        }
+        return true;
+    };
+    auto need_v = [&](int slot, const char* what) -> bool {
+        if (!vec(c, slot)) {
+            c->err = std::string("tensor not uploaded: ") + what;
+            return false;
+        }
+        return true;
+    };
+    if (!need_m(TF_HIP_SLOT_TOKEN_EMBD, "token_embd.weight") || !need_v(TF_HIP_SLOT_OUTPUT_NORM, "output_norm.weight"))
+        return TF_HIP_ESTATE;
+    for (int l = 0; l < c->hp.n_layer; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        if (!need_v(TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_ATTN_NORM), (p + "attn_norm").c_str()) ||
+            !need_m(TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_Q), (p + "attn_q").c_str()) ||
+            !need_m(TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_K), (p + "attn_k").c_str()) ||
+            !need_m(TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_V), (p + "attn_v").c_str()) ||
+            !need_m(TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_O), (p + "attn_output").c_str()) ||
+            !need_v(TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_FFN_NORM), (p + "ffn_norm").c_str()) ||
+            !need_m(TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_GATE), (p + "ffn_gate").c_str()) ||
+            !need_m(TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_UP), (p + "ffn_up").c_str()) ||
+            !need_m(TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_DOWN), (p + "ffn_down").c_str()))
+            return TF_HIP_ESTATE;
+    }
+    if (!c->rope_set) {
+        c->err = "RoPE table not set";
+        return TF_HIP_ESTATE;
+    }
+    return 0;
+}
+
+// Launch one kernel, bracketed by events when profiling.
+struct Launcher {
+    tf_hip_ctx* c;
+    Prof* prof;
+    hipError_t err = hipSuccess;
+    template <typename Fn>
+    void run(int cls, double bytes, Fn fn) {
+        if (err != hipSuccess) return;
+        hipEvent_t a = nullptr, b = nullptr;
+        if (prof) {
+            (void)hipEventCreate(&a);
+            (void)hipEventCreate(&b);
+            (void)hipEventRecord(a, c->st);
+        }
+        err = fn();
+        if (prof) {
+            (void)hipEventRecord(b, c->st);
+            prof->ev.push_back(a);
+            prof->ev.push_back(b);
+            prof->cls.push_back(cls);
+            prof->bytes.push_back(bytes);
+        }
+    }
+};
+
+// One decode step (model.cpp:197-208) on the context stream.
+hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof) {
+    const tf_hip_hparams& hp = c->hp;
+    const int D = hp.n_embd, F = hp.n_ff;
+    Launcher L{c, prof};
+    const DevMat& emb = mat(c, TF_HIP_SLOT_TOKEN_EMBD);
+    L.run(0, (double)emb.gguf_bytes / emb.N, [&] { return launch_embed(emb, c->x, c->ctl, c->hist, D, c->st); });
+    for (int l = 0; l < hp.n_layer; ++l) {
+        auto M = [&](int kind) -> const DevMat& { return mat(c, TF_HIP_SLOT_LAYER(l, kind)); };
+        auto V = [&](int kind) { return vec(c, TF_HIP_SLOT_LAYER(l, kind)); };
+        // Q, K, V (+bias): one launch when the three share a format
+        {
+            const DevMat& wq = M(TF_HIP_LAYER_Q);
+            const DevMat& wk = M(TF_HIP_LAYER_K);
+            const DevMat& wv = M(TF_HIP_LAYER_V);
+            const int R = pick_rows(wq.N + wk.N + wv.N);
+            const DevMat* ms[3] = {&wq, &wk, &wv};
+            float* ys[3] = {c->q, c->k, c->v};
+            const float* bs[3] = {V(TF_HIP_LAYER_BQ), V(TF_HIP_LAYER_BK), V(TF_HIP_LAYER_BV)};
+            int i = 0;
+            while (i < 3) {
+                GemvArgs a;
+                a.type = ms[i]->type;
+                a.K = D;
+                a.mode = GEMV_STORE;
+                a.x = c->x;
+                a.norm_w = V(TF_HIP_LAYER_ATTN_NORM);
+                a.eps = hp.rms_eps;
+                double bytes = 0;
+                while (i < 3 && ms[i]->type == a.type) {
+                    add_seg(a, *ms[i], ys[i], bs[i], nullptr, R);
+                    bytes += (double)ms[i]->gguf_bytes;
+                    ++i;
+                }
+                L.run(1, bytes, [&] { return launch_gemv(a, R, c->st); });
+            }
+        }
+        {
+            AttnArgs a{};
+            a.q = c->q;
+            a.knew = c->k;
+            a.vnew = c->v;
+            a.kc = c->kc + (size_t)l * c->kv_layer;
+            a.vc = c->vc + (size_t)l * c->kv_layer;
+            a.rope_cos = c->rope_cos;
+            a.rope_sin = c->rope_sin;
+            a.part_o = c->part_o;
+            a.part_ml = c->part_ml;
+            a.counter = c->counters + (size_t)l * hp.n_kv_head;
+            a.out = c->att;
+            a.ctl = c->ctl;
+            a.H = hp.n_head;
+            a.G = hp.n_kv_head;
+            a.hd = hp.head_dim;
+            a.max_seq = hp.max_seq;
+            a.layout = hp.kv_layout;
+            a.S = c->S;
+            a.rope = 1;
+            a.store_kv = 1;
+            a.fixed_pos = -1;
+            a.fixed_start = 0;
+            L.run(2, 0.0, [&] { return launch_attn_decode(a, c->st); });
+        }
+        {
+            const DevMat& wo = M(TF_HIP_LAYER_O);
+            const int R = pick_rows(wo.N);
+            GemvArgs a;
+            a.type = wo.type;
+            a.K = c->H;
+            a.mode = GEMV_RESID;
+            a.x = c->att;
+            add_seg(a, wo, c->x, nullptr, nullptr, R);
+            L.run(3, (double)wo.gguf_bytes, [&] { return launch_gemv(a, R, c->st); });
+        }
+        {
+            const DevMat& wg = M(TF_HIP_LAYER_GATE);
+            const DevMat& wu = M(TF_HIP_LAYER_UP);
+            if (wg.type == wu.type) {
+                const int R = pick_rows(2 * wg.N) > 1 ? 2 : 1;
+                GemvArgs a;
+                a.type = wg.type;
+                a.K = D;
+                a.mode = GEMV_SILU;
+                a.x = c->x;
+                a.norm_w = V(TF_HIP_LAYER_FFN_NORM);
+                a.eps = hp.rms_eps;
+                add_seg(a, wg, c->h, nullptr, nullptr, R);
+                a.seg[0].b = wu;
+                L.run(4, (double)(wg.gguf_bytes + wu.gguf_bytes), [&] { return launch_gemv(a, R, c->st); });
+            } else {
+                L.err = hipErrorInvalidValue;  // rejected at upload; unreachable
+            }
+        }
+        {
+            const DevMat& wd = M(TF_HIP_LAYER_DOWN);
+            const int R = pick_rows(wd.N);
+            GemvArgs a;
+            a.type = wd.type;
+            a.K = F;
+            a.mode = GEMV_RESID;
+            a.x = c->h;
+            add_seg(a, wd, c->x, nullptr, c->taps + (size_t)l * D, R);
+            L.run(5, (double)wd.gguf_bytes, [&] { return launch_gemv(a, R, c->st); });
+        }
+    }
+    {
+        const DevMat& wout = output_mat(c);
+        const int R = pick_rows(wout.N);
+        GemvArgs a;
+        a.type = wout.type;
+        a.K = D;
+        a.mode = GEMV_LOGITS;
+        a.x = c->x;
+        a.norm_w = vec(c, TF_HIP_SLOT_OUTPUT_NORM);
+        a.eps = hp.rms_eps;
+        a.norm_out = c->taps + (size_t)hp.n_layer * D;
+        a.ctl = c->ctl;
+        a.bump_pos = 1;
+        add_seg(a, wout, c->logits, nullptr, nullptr, R);
+        L.run(6, (double)wout.gguf_bytes, [&] { return launch_gemv(a, R, c->st); });
+    }
+    return L.err;
+}
+
+int ensure_graph(tf_hip_ctx* c) {
+    if (c->gexec) return 0;
+    int rc = check_ready(c);
+    if (rc) return rc;
+    HIPCHK(c, hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+    const hipError_t e = enqueue_step(c, nullptr);
+    hipGraph_t g = nullptr;
+    const hipError_t e2 = hipStreamEndCapture(c->st, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return fail(c, TF_HIP_EDEVICE, std::string("decode step launch: ") + hipGetErrorString(e));
+    }
+    if (e2 != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(e2));
+    c->graph = g;
+    HIPCHK(c, hipGraphInstantiate(&c->gexec, c->graph, nullptr, nullptr, 0));
+    return 0;
+}
+
+// Writes att_start and mode of the device control block.
+int set_ctl(tf_hip_ctx* c, int att_start, int mode) {
+    c->ctl_host->att_start = att_start;
+    c->ctl_host->mode = mode;
+    HIPCHK(c, hipMemcpyAsync((char*)c->ctl + offsetof(Ctl, att_start), (char*)c->ctl_host + offsetof(Ctl, att_start),
+                             2 * sizeof(int32_t), hipMemcpyHostToDevice, c->st));
+    return 0;
+}
+
+int finish_step_outputs(tf_hip_ctx* c, float* logits, int32_t* argmax) {
+    if (logits)
+        HIPCHK(c, hipMemcpyAsync(logits, c->logits, (size_t)c->hp.n_vocab * 4, hipMemcpyDeviceToHost, c->st));
+    HIPCHK(c, hipMemcpyAsync(c->ctl_host, c->ctl, sizeof(Ctl), hipMemcpyDeviceToHost, c->st));
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    if (c->ctl_host->err) return fail(c, TF_HIP_EDEVICE, "device reported an invalid token");
+    if (c->ctl_host->pos != c->pos) return fail(c, TF_HIP_EDEVICE, "device position out of step");
+    if (argmax) *argmax = key_to_index(c->ctl_host->key);
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tf_hip_last_error(const tf_hip_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out) {
+    if (!hp || !out) return TF_HIP_EINVAL;
+    *out = nullptr;
+    const tf_hip_hparams& p = *hp;
+    if (p.n_vocab <= 0 || p.n_embd <= 0 || p.n_ff <= 0 || p.n_layer <= 0 || p.n_head <= 0 || p.n_kv_head <= 0 ||
+        p.max_seq <= 0)
+        return TF_HIP_EINVAL;
+    if (p.n_head % p.n_kv_head != 0 || p.n_head / p.n_kv_head > 8) return TF_HIP_EINVAL;
+    if (p.head_dim != p.n_embd / p.n_head || p.head_dim % 8 != 0 || p.head_dim > 256) return TF_HIP_EINVAL;
+    if (p.kv_layout != TF_HIP_KV_SEQ_MAJOR && p.kv_layout != TF_HIP_KV_HEAD_MAJOR) return TF_HIP_EINVAL;
+    if (p.n_embd % 32 != 0 || p.n_ff % 32 != 0) return TF_HIP_EINVAL;
+
+    tf_hip_ctx* c = new tf_hip_ctx();
+    c->device = device;
+    c->hp = p;
+    c->H = p.n_head * p.head_dim;
+    c->KVd = p.n_kv_head * p.head_dim;
+    auto bail = [&](int rc) {
+        tf_hip_destroy(c);
+        return rc;
+    };
+    if (hipSetDevice(device) != hipSuccess) return bail(TF_HIP_EDEVICE);
+    if (hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking) != hipSuccess) return bail(TF_HIP_EDEVICE);
+    const int n_slots = TF_HIP_SLOT_LAYER(p.n_layer, 0);
+    c->mats.resize((size_t)n_slots);
+    c->vecs.assign((size_t)n_slots, nullptr);
+    c->vec_len.assign((size_t)n_slots, 0);
+
+    // split count: enough workgroups per kv head to stream long caches, at most 64
+    int S = (p.max_seq + 63) / 64;
+    S = std::max(1, std::min(S, 64));
+    c->S = S;
+    c->kv_layer = (size_t)p.n_kv_head * p.max_seq * p.head_dim;
+    const size_t D = (size_t)p.n_embd;
+    int rc = 0;
+    if ((rc = dalloc(c, &c->kc, c->kv_layer * p.n_layer * 4)) || (rc = dalloc(c, &c->vc, c->kv_layer * p.n_layer * 4)) ||
+        (rc = dalloc(c, &c->x, D * 4)) || (rc = dalloc(c, &c->q, (size_t)c->H * 4)) ||
+        (rc = dalloc(c, &c->k, (size_t)c->KVd * 4)) || (rc = dalloc(c, &c->v, (size_t)c->KVd * 4)) ||
+        (rc = dalloc(c, &c->att, (size_t)c->H * 4)) || (rc = dalloc(c, &c->h, (size_t)p.n_ff * 4)) ||
+        (rc = dalloc(c, &c->logits, (size_t)p.n_vocab * 4)) ||
+        (rc = dalloc(c, &c->taps, (size_t)(p.n_layer + 1) * D * 4)) ||
+        (rc = dalloc(c, &c->part_o, (size_t)p.n_head * S * p.head_dim * 4)) ||
+        (rc = dalloc(c, &c->part_ml, (size_t)p.n_head * S * 2 * 4)) ||
+        (rc = dalloc(c, &c->counters, (size_t)p.n_layer * p.n_kv_head * 4)) || (rc = dalloc(c, &c->ctl, sizeof(Ctl))) ||
+        (rc = dalloc(c, &c->hist, (size_t)p.max_seq * 4)) ||
+        (rc = dalloc(c, &c->rope_cos, (size_t)p.max_seq * (p.head_dim / 2) * 4)) ||
+        (rc = dalloc(c, &c->rope_sin, (size_t)p.max_seq * (p.head_dim / 2) * 4)))
+        return bail(rc);
+    if (hipHostMalloc((void**)&c->ctl_host, sizeof(Ctl), 0) != hipSuccess) return bail(TF_HIP_ENOMEM);
+    if (hipHostMalloc((void**)&c->tok_host, (size_t)p.max_seq * 4, 0) != hipSuccess) return bail(TF_HIP_ENOMEM);
+    std::memset(c->ctl_host, 0, sizeof(Ctl));
+    if (hipMemset(c->counters, 0, (size_t)p.n_layer * p.n_kv_head * 4) != hipSuccess ||
+        hipMemset(c->ctl, 0, sizeof(Ctl)) != hipSuccess || hipMemset(c->kc, 0, c->kv_layer * p.n_layer * 4) != hipSuccess ||
+        hipMemset(c->vc, 0, c->kv_layer * p.n_layer * 4) != hipSuccess ||
+        hipMemset(c->taps, 0, (size_t)(p.n_layer + 1) * D * 4) != hipSuccess)
+        return bail(TF_HIP_EDEVICE);
+    if (hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess) return bail(TF_HIP_EDEVICE);
+    *out = c;
+    return 0;
+}
+
+int tf_hip_destroy(tf_hip_ctx* c) {
+    if (!c) return 0;
+    (void)hipSetDevice(c->device);
+    if (c->st) (void)hipStreamSynchronize(c->st);
+    if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    for (void* p : c->allocs) (void)hipFree(p);
+    if (c->ctl_host) (void)hipHostFree(c->ctl_host);
+    if (c->tok_host) (void)hipHostFree(c->tok_host);
+    if (c->ev0) (void)hipEventDestroy(c->ev0);
+    if (c->ev1) (void)hipEventDestroy(c->ev1);
+    if (c->st) (void)hipStreamDestroy(c->st);
+    delete c;
+    return 0;
+}
+
+int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne1, const void* host, size_t nbytes) {
+    if (!c) return TF_HIP_EINVAL;
+    const tf_hip_hparams& p = c->hp;
+    if (slot < 0 || slot >= (int)c->mats.size() || (slot > 2 && slot < 16) || !host)
+        return fail(c, TF_HIP_EINVAL, "bad tensor slot " + std::to_string(slot));
+    if (blck_elems(t) == 0) return fail(c, TF_HIP_EINVAL, "unsupported ggml type " + std::to_string(t));
+    if (ne0 <= 0 || ne1 <= 0 || ne0 % blck_elems(t) != 0)
+        return fail(c, TF_HIP_EINVAL, "row length not divisible by block size");
+    if (nbytes != gguf_nbytes(t, ne0, ne1)) return fail(c, TF_HIP_EINVAL, "tensor byte size does not match its shape");
+    if (c->gexec) {
+        (void)hipGraphExecDestroy(c->gexec);
+        (void)hipGraphDestroy(c->graph);
+        c->gexec = nullptr;
+        c->graph = nullptr;
+    }
+    HIPCHK(c, hipSetDevice(c->device));
+    // vectors: norms and biases are read as raw F32 by the reference (model.cpp:87, layers.cpp:11)
+    int kind = -1;
+    if (slot >= 16) kind = (slot - 16) % TF_HIP_LAYER_COUNT;
+    const bool is_vec = slot == TF_HIP_SLOT_OUTPUT_NORM || kind == TF_HIP_LAYER_ATTN_NORM ||
+                        kind == TF_HIP_LAYER_FFN_NORM || kind == TF_HIP_LAYER_BQ || kind == TF_HIP_LAYER_BK ||
+                        kind == TF_HIP_LAYER_BV;
+    if (is_vec) {
+        int64_t want = p.n_embd;
+        if (kind == TF_HIP_LAYER_BQ) want = c->H;
+        if (kind == TF_HIP_LAYER_BK || kind == TF_HIP_LAYER_BV) want = c->KVd;
+        if (t != TF_HIP_TYPE_F32 || ne0 * ne1 != want)
+            return fail(c, TF_HIP_EINVAL, "vector tensor must be F32 of length " + std::to_string(want));
+        float* d = c->vecs[(size_t)slot];
+        if (!d) {
+            int rc = dalloc(c, &d, (size_t)want * 4);
+            if (rc) return rc;
+            c->vecs[(size_t)slot] = d;
+        }
+        c->vec_len[(size_t)slot] = want;
+        HIPCHK(c, hipMemcpy(d, host, (size_t)want * 4, hipMemcpyHostToDevice));
+        return 0;
+    }
+    // matrices: expected [ne0 x ne1]
+    int64_t K = 0, N = 0;
+    if (slot == TF_HIP_SLOT_TOKEN_EMBD || slot == TF_HIP_SLOT_OUTPUT) {
+        K = p.n_embd;
+        N = p.n_vocab;
+    } else {
+        switch (kind) {
+            case TF_HIP_LAYER_Q: K = p.n_embd; N = c->H; break;
+            case TF_HIP_LAYER_K:
+            case TF_HIP_LAYER_V: K = p.n_embd; N = c->KVd; break;
+            case TF_HIP_LAYER_O: K = c->H; N = p.n_embd; break;
+            case TF_HIP_LAYER_GATE:
+            case TF_HIP_LAYER_UP: K = p.n_embd; N = p.n_ff; break;
+            case TF_HIP_LAYER_DOWN: K = p.n_ff; N = p.n_embd; break;
+        }
+    }
+    if (slot == TF_HIP_SLOT_TOKEN_EMBD && ne0 == K && ne1 >= N) N = ne1;  // embedding may hold extra rows
+    if (ne0 != K || ne1 != N)
+        return fail(c, TF_HIP_EINVAL, "tensor shape [" + std::to_string(ne0) + " x " + std::to_string(ne1) +
+                                           "] does not match the model, want [" + std::to_string(K) + " x " +
+                                           std::to_string(N) + "]");
+    if (!row_ok(t, K)) return fail(c, TF_HIP_EINVAL, "row length unsupported for this format");
+    if (kind == TF_HIP_LAYER_UP || kind == TF_HIP_LAYER_GATE) {
+        const int other = slot + (kind == TF_HIP_LAYER_UP ? -1 : 1);
+        const DevMat& o = c->mats[(size_t)other];
+        if (o.valid() && o.type != t) return fail(c, TF_HIP_EINVAL, "ffn_gate and ffn_up must share a format");
+    }
+    uint8_t* raw = nullptr;
+    HIPCHK(c, hipMalloc(&raw, nbytes));
+    hipError_t e = hipMemcpy(raw, host, nbytes, hipMemcpyHostToDevice);
+    DevMat m;
+    std::vector<void*> owned;
+    if (e == hipSuccess) e = make_devmat(t, K, N, raw, m, owned, c->st);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->st);
+    (void)hipFree(raw);
+    if (e != hipSuccess) {
+        for (void* q : owned) (void)hipFree(q);
+        return fail(c, e == hipErrorOutOfMemory ? TF_HIP_ENOMEM : TF_HIP_EDEVICE,
+                    std::string("upload: ") + hipGetErrorString(e));
+    }
+    c->allocs.insert(c->allocs.end(), owned.begin(), owned.end());
+    c->mats[(size_t)slot] = m;  // a re-upload leaves the old streams allocated until destroy
+    return 0;
+}
+
+int tf_hip_set_rope_table(tf_hip_ctx* c, const float* cos_tab, const float* sin_tab, int32_t n_pos, int32_t half) {
+    if (!c || !cos_tab || !sin_tab) return TF_HIP_EINVAL;
+    if (half != c->hp.head_dim / 2 || n_pos < c->hp.max_seq)
+        return fail(c, TF_HIP_EINVAL, "RoPE table must be [>= max_seq][head_dim/2]");
+    const size_t n = (size_t)c->hp.max_seq * half * 4;
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipMemcpy(c->rope_cos, cos_tab, n, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(c->rope_sin, sin_tab, n, hipMemcpyHostToDevice));
+    c->rope_set = true;
+    return 0;
+}
+
+int tf_hip_reset(tf_hip_ctx* c) {
+    if (!c) return TF_HIP_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    c->pos = 0;
+    c->have_logits = false;
+    std::memset(c->ctl_host, 0, sizeof(Ctl));
+    HIPCHK(c, hipMemcpyAsync(c->ctl, c->ctl_host, sizeof(Ctl), hipMemcpyHostToDevice, c->st));
+    HIPCHK(c, hipMemsetAsync(c->kc, 0, c->kv_layer * c->hp.n_layer * 4, c->st));
+    HIPCHK(c, hipMemsetAsync(c->vc, 0, c->kv_layer * c->hp.n_layer * 4, c->st));
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    return 0;
+}
+
+int tf_hip_get_pos(const tf_hip_ctx* c) { return c ? c->pos : TF_HIP_EINVAL; }
+
+int tf_hip_decode(tf_hip_ctx* c, int32_t token, float* logits, int32_t* argmax) {
+    if (!c) return TF_HIP_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    if (c->pos + 1 > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
+    if (token < 0 || token >= mat(c, TF_HIP_SLOT_TOKEN_EMBD).N)
+        return fail(c, TF_HIP_ERANGE, "token " + std::to_string(token) + " out of range");
+    int rc = ensure_graph(c);
+    if (rc) return rc;
+    c->tok_host[0] = token;
+    HIPCHK(c, hipMemcpyAsync(c->hist + c->pos, c->tok_host, 4, hipMemcpyHostToDevice, c->st));
+    if ((rc = set_ctl(c, 0, 0))) return rc;
+    HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    c->pos += 1;
+    rc = finish_step_outputs(c, logits, argmax);
+    if (rc) return rc;
+    c->have_logits = true;
+    return 0;
+}
+
+int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logits, int32_t* argmax) {
+    if (!c || (n > 0 && !tokens)) return TF_HIP_EINVAL;
+    if (n <= 0) return 0;
+    HIPCHK(c, hipSetDevice(c->device));
+    if (c->pos + n > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "prefill exceeds max_seq");
+    const int64_t V = mat(c, TF_HIP_SLOT_TOKEN_EMBD).N;
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= V)
+            return fail(c, TF_HIP_ERANGE, "token " + std::to_string(tokens[i]) + " out of range");
+    int rc = ensure_graph(c);
+    if (rc) return rc;
+    std::memcpy(c->tok_host, tokens, (size_t)n * 4);
+    HIPCHK(c, hipMemcpyAsync(c->hist + c->pos, c->tok_host, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
+    if ((rc = set_ctl(c, c->pos, 0))) return rc;
+    for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    c->pos += n;
+    rc = finish_step_outputs(c, logits, argmax);
+    if (rc) return rc;
+    c->have_logits = true;
+    return 0;
+}
+
+int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
+    if (!c || (n > 0 && !out)) return TF_HIP_EINVAL;
+    if (n <= 0) return 0;
+    HIPCHK(c, hipSetDevice(c->device));
+    if (!c->have_logits) return fail(c, TF_HIP_ESTATE, "generate needs a prior prefill or decode");
+    if (c->pos + n > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
+    int rc = ensure_graph(c);
+    if (rc) return rc;
+    const int pos0 = c->pos;
+    if ((rc = set_ctl(c, 0, 1))) return rc;
+    HIPCHK(c, hipEventRecord(c->ev0, c->st));
+    for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    HIPCHK(c, hipEventRecord(c->ev1, c->st));
+    HIPCHK(c, hipMemcpyAsync(c->tok_host, c->hist + pos0, (size_t)n * 4, hipMemcpyDeviceToHost, c->st));
+    c->pos += n;
+    rc = finish_step_outputs(c, nullptr, nullptr);
+    if (rc) return rc;
+    std::memcpy(out, c->tok_host, (size_t)n * 4);
+    HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
+    c->last_steps = n;
+    return 0;
+}
+
+int tf_hip_get_layer_act(tf_hip_ctx* c, int32_t layer, float* out) {
+    if (!c || !out || layer < 0 || layer > c->hp.n_layer) return TF_HIP_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    HIPCHK(c, hipMemcpy(out, c->taps + (size_t)layer * c->hp.n_embd, (size_t)c->hp.n_embd * 4, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int tf_hip_read_kv(tf_hip_ctx* c, int32_t layer, int32_t which, int32_t pos0, int32_t n, float* out) {
+    if (!c || !out || layer < 0 || layer >= c->hp.n_layer || pos0 < 0 || n < 0 || pos0 + n > c->hp.max_seq)
+        return TF_HIP_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    const tf_hip_hparams& p = c->hp;
+    const float* base = (which ? c->vc : c->kc) + (size_t)layer * c->kv_layer;
+    const size_t hd = (size_t)p.head_dim;
+    if (p.kv_layout == TF_HIP_KV_SEQ_MAJOR) {
+        HIPCHK(c, hipMemcpy(out, base + (size_t)pos0 * p.n_kv_head * hd, (size_t)n * p.n_kv_head * hd * 4,
+                            hipMemcpyDeviceToHost));
+    } else {
+        for (int g = 0; g < p.n_kv_head; ++g)
+            HIPCHK(c, hipMemcpy2D(out + g * hd, (size_t)p.n_kv_head * hd * 4, base + ((size_t)g * p.max_seq + pos0) * hd,
+                                  hd * 4, hd * 4, (size_t)n, hipMemcpyDeviceToHost));
+    }
+    return 0;
+}
+
+int tf_hip_last_timing(const tf_hip_ctx* c, float* total_ms, float* kernel_ms, int32_t* launches, char* name,
+                       int32_t name_len) {
+    if (!c) return TF_HIP_EINVAL;
+    if (total_ms) *total_ms = c->last_ms;
+    if (kernel_ms) *kernel_ms = c->last_ms;
+    if (launches) *launches = c->last_steps;
+    if (name && name_len > 0) std::snprintf(name, (size_t)name_len, "%s", "decode_graph");
+    return 0;
+}
+
+// Profiling variant of tf_hip_generate: the same kernels launched one by one with
+// events around each, per kernel class: summed ms, launches and algorithmic bytes.
+int tf_hip_profile_generate(tf_hip_ctx* c, int32_t n, int32_t* out, float* ms_by_class, int32_t* launches_by_class,
+                            double* bytes_by_class) {
+    if (!c || n <= 0 || !out) return TF_HIP_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    if (!c->have_logits) return fail(c, TF_HIP_ESTATE, "generate needs a prior prefill or decode");
+    if (c->pos + n > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
+    int rc = check_ready(c);
+    if (rc) return rc;
+    const int pos0 = c->pos;
+    if ((rc = set_ctl(c, 0, 1))) return rc;
+    Prof prof;
+    for (int i = 0; i < n; ++i) {
+        const hipError_t e = enqueue_step(c, &prof);
+        if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("profile step: ") + hipGetErrorString(e));
+    }
+    HIPCHK(c, hipMemcpyAsync(c->tok_host, c->hist + pos0, (size_t)n * 4, hipMemcpyDeviceToHost, c->st));
+    c->pos += n;
+    rc = finish_step_outputs(c, nullptr, nullptr);
+    if (rc) return rc;
+    std::memcpy(out, c->tok_host, (size_t)n * 4);
+    for (int k = 0; k < kNumClasses; ++k) {
+        if (ms_by_class) ms_by_class[k] = 0;
+        if (launches_by_class) launches_by_class[k] = 0;
+        if (bytes_by_class) bytes_by_class[k] = 0;
+    }
+    for (size_t i = 0; i < prof.cls.size(); ++i) {
+        float ms = 0;
+        (void)hipEventElapsedTime(&ms, prof.ev[2 * i], prof.ev[2 * i + 1]);
+        const int k = prof.cls[i];
+        if (ms_by_class) ms_by_class[k] += ms;
+        if (launches_by_class) launches_by_class[k] += 1;
+        if (bytes_by_class) bytes_by_class[k] += prof.bytes[i];
+    }
+    for (hipEvent_t e : prof.ev) (void)hipEventDestroy(e);
+    return 0;
+}
+
+const char* tf_hip_kernel_class_name(int32_t k) { return (k >= 0 && k < kNumClasses) ? kClassNames[k] : ""; }
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- op-level entry points
+
+namespace {
+
+struct OpScope {
+    hipStream_t st = nullptr;
+    std::vector<void*> mem;
+    ~OpScope() {
+        if (st) (void)hipStreamSynchronize(st);
+        for (void* p : mem) (void)hipFree(p);
+        if (st) (void)hipStreamDestroy(st);
+    }
+    template <typename T>
+    hipError_t alloc(T** p, size_t bytes) {
+        void* d = nullptr;
+        hipError_t e = hipMalloc(&d, bytes ? bytes : 16);
+        if (e == hipSuccess) mem.push_back(d);
+        *p = (T*)d;
+        return e;
+    }
+};
+
+#define OPCHK(call)                                                                   \
+    do {                                                                              \
+        hipError_t e_ = (call);                                                       \
+        if (e_ != hipSuccess) return e_ == hipErrorOutOfMemory ? TF_HIP_ENOMEM : TF_HIP_EDEVICE; \
+    } while (0)
+
+int op_begin(int device, OpScope& s) {
+    OPCHK(hipSetDevice(device));
+    OPCHK(hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking));
+    return 0;
+}
+
+int op_upload_mat(OpScope& s, int t, const void* w, int64_t K, int64_t N, DevMat& m) {
+    uint8_t* raw = nullptr;
+    const size_t nb = gguf_nbytes(t, K, N);
+    OPCHK(s.alloc(&raw, nb));
+    OPCHK(hipMemcpy(raw, w, nb, hipMemcpyHostToDevice));
+    OPCHK(make_devmat(t, K, N, raw, m, s.mem, s.st));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tf_hip_dequant_rows(int device, int t, const void* w, int64_t ne0, int64_t ne1, int64_t row0, int64_t nrows,
+                        float* out) {
+    if (!w || !out || blck_elems(t) == 0 || !row_ok(t, ne0) || ne1 <= 0 || row0 < 0 || nrows <= 0 ||
+        row0 + nrows > ne1)
+        return TF_HIP_EINVAL;
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    DevMat m;
+    const size_t rb = gguf_nbytes(t, ne0, 1);
+    if ((rc = op_upload_mat(s, t, (const uint8_t*)w + row0 * rb, ne0, nrows, m))) return rc;
+    float* d_out = nullptr;
+    OPCHK(s.alloc(&d_out, (size_t)nrows * ne0 * 4));
+    OPCHK(launch_dequant_rows(m, 0, nrows, d_out, s.st));
+    OPCHK(hipMemcpyAsync(out, d_out, (size_t)nrows * ne0 * 4, hipMemcpyDeviceToHost, s.st));
+    OPCHK(hipStreamSynchronize(s.st));
+    return 0;
+}
+
+int tf_hip_matmul(int device, int t, const void* w, int64_t ne0, int64_t ne1, const float* x, int32_t n_rows_x,
+                  float* y) {
+    if (!w || !x || !y || blck_elems(t) == 0 || !row_ok(t, ne0) || ne1 <= 0 || n_rows_x <= 0) return TF_HIP_EINVAL;
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    DevMat m;
+    if ((rc = op_upload_mat(s, t, w, ne0, ne1, m))) return rc;
+    float *dx = nullptr, *dy = nullptr;
+    OPCHK(s.alloc(&dx, (size_t)n_rows_x * ne0 * 4));
+    OPCHK(s.alloc(&dy, (size_t)n_rows_x * ne1 * 4));
+    OPCHK(hipMemcpy(dx, x, (size_t)n_rows_x * ne0 * 4, hipMemcpyHostToDevice));
+    const int R = pick_rows(ne1);
+    for (int i = 0; i < n_rows_x; ++i) {
+        GemvArgs a;
+        a.type = t;
+        a.K = ne0;
+        a.mode = GEMV_STORE;
+        a.x = dx + (size_t)i * ne0;
+        add_seg(a, m, dy + (size_t)i * ne1, nullptr, nullptr, R);
+        OPCHK(launch_gemv(a, R, s.st));
+    }
+    OPCHK(hipMemcpyAsync(y, dy, (size_t)n_rows_x * ne1 * 4, hipMemcpyDeviceToHost, s.st));
+    OPCHK(hipStreamSynchronize(s.st));
+    return 0;
+}
+
+int tf_hip_rmsnorm(int device, const float* x, const float* w, int32_t n, int32_t rows, float eps, float* out) {
+    if (!x || !w || !out || n <= 0 || rows <= 0) return TF_HIP_EINVAL;
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    float *dx, *dw, *dout;
+    OPCHK(s.alloc(&dx, (size_t)n * rows * 4));
+    OPCHK(s.alloc(&dw, (size_t)n * 4));
+    OPCHK(s.alloc(&dout, (size_t)n * rows * 4));
+    OPCHK(hipMemcpy(dx, x, (size_t)n * rows * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemcpy(dw, w, (size_t)n * 4, hipMemcpyHostToDevice));
+    OPCHK(launch_rmsnorm_rows(dx, dw, n, rows, eps, dout, s.st));
+    OPCHK(hipMemcpyAsync(out, dout, (size_t)n * rows * 4, hipMemcpyDeviceToHost, s.st));
+    OPCHK(hipStreamSynchronize(s.st));
+    return 0;
+}
+
+int tf_hip_attn_decode(int device, const float* q, const float* k_rows, const float* v_rows, int32_t n_heads,
+                       int32_t n_kv, int32_t hd, int32_t n_pos, int32_t max_seq, int32_t layout, float* out) {
+    if (!q || !k_rows || !v_rows || !out || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > 8 ||
+        hd % 8 || hd > 256 || hd <= 0 || n_pos <= 0 || n_pos > max_seq || (layout != 0 && layout != 1))
+        return TF_HIP_EINVAL;
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    const size_t cache = (size_t)n_kv * max_seq * hd;
+    std::vector<float> hk(cache, 0.0f), hv(cache, 0.0f);
+    for (int p = 0; p < n_pos; ++p)
+        for (int g = 0; g < n_kv; ++g) {
+            const size_t o = layout ? ((size_t)g * max_seq + p) * hd : ((size_t)p * n_kv + g) * hd;
+            std::memcpy(&hk[o], k_rows + ((size_t)p * n_kv + g) * hd, (size_t)hd * 4);
+            std::memcpy(&hv[o], v_rows + ((size_t)p * n_kv + g) * hd, (size_t)hd * 4);
+        }
+    int S = std::max(1, std::min(64, (max_seq + 63) / 64));
+    float *dq, *dk, *dv, *dout, *pk, *pv, *po, *pml;
+    unsigned* cnt;
+    OPCHK(s.alloc(&dq, (size_t)n_heads * hd * 4));
+    OPCHK(s.alloc(&dk, cache * 4));
+    OPCHK(s.alloc(&dv, cache * 4));
+    OPCHK(s.alloc(&dout, (size_t)n_heads * hd * 4));
+    OPCHK(s.alloc(&pk, (size_t)n_kv * hd * 4));
+    OPCHK(s.alloc(&pv, (size_t)n_kv * hd * 4));
+    OPCHK(s.alloc(&po, (size_t)n_heads * S * hd * 4));
+    OPCHK(s.alloc(&pml, (size_t)n_heads * S * 2 * 4));
+    OPCHK(s.alloc(&cnt, (size_t)n_kv * 4));
+    OPCHK(hipMemcpy(dq, q, (size_t)n_heads * hd * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemcpy(dk, hk.data(), cache * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemcpy(dv, hv.data(), cache * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemcpy(pk, k_rows + (size_t)(n_pos - 1) * n_kv * hd, (size_t)n_kv * hd * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemcpy(pv, v_rows + (size_t)(n_pos - 1) * n_kv * hd, (size_t)n_kv * hd * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemset(cnt, 0, (size_t)n_kv * 4));
+    AttnArgs a{};
+    a.q = dq;
+    a.knew = pk;
+    a.vnew = pv;
+    a.kc = dk;
+    a.vc = dv;
+    a.rope_cos = dq;  // unused with rope = 0
+    a.rope_sin = dq;
+    a.part_o = po;
+    a.part_ml = pml;
+    a.counter = cnt;
+    a.out = dout;
+    a.ctl = nullptr;
+    a.H = n_heads;
+    a.G = n_kv;
+    a.hd = hd;
+    a.max_seq = max_seq;
+    a.layout = layout;
+    a.S = S;
+    a.rope = 0;
+    a.store_kv = 0;
+    a.fixed_pos = n_pos - 1;
+    a.fixed_start = 0;
+    OPCHK(launch_attn_decode(a, s.st));
+    OPCHK(hipMemcpyAsync(out, dout, (size_t)n_heads * hd * 4, hipMemcpyDeviceToHost, s.st));
+    OPCHK(hipStreamSynchronize(s.st));
+    return 0;
+}
+
+int tf_hip_argmax(int device, const float* x, int32_t n, int32_t* out) {
+    if (!x || !out || n <= 0) return TF_HIP_EINVAL;
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    float* dx;
+    Ctl* ctl;
+    OPCHK(s.alloc(&dx, (size_t)n * 4));
+    OPCHK(s.alloc(&ctl, sizeof(Ctl)));
+    OPCHK(hipMemcpy(dx, x, (size_t)n * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemset(ctl, 0, sizeof(Ctl)));
+    OPCHK(launch_argmax(dx, n, ctl, s.st));
+    Ctl h;
+    OPCHK(hipMemcpyAsync(&h, ctl, sizeof(Ctl), hipMemcpyDeviceToHost, s.st));
+    OPCHK(hipStreamSynchronize(s.st));
+    *out = key_to_index(h.key);
+    return 0;
+}
+
+int tf_hip_read_stream(int device, size_t nbytes, int32_t iters, double* best, double* median) {
+    if (nbytes < 16 || iters <= 0 || !best || !median) return TF_HIP_EINVAL;
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    const size_t n4 = nbytes / 16;
+    float4* p;
+    double* sink;
+    const int blocks = 8 * device_cu_count();
+    OPCHK(s.alloc(&p, n4 * 16));
+    OPCHK(s.alloc(&sink, (size_t)blocks * kWavesPerBlock * sizeof(double)));
+    OPCHK(hipMemset(p, 0, n4 * 16));
+    hipEvent_t e0, e1;
+    OPCHK(hipEventCreate(&e0));
+    OPCHK(hipEventCreate(&e1));
+    std::vector<double> gbs;
+    OPCHK(launch_read_stream(p, n4, sink, blocks, s.st));  // warm-up
+    for (int i = 0; i < iters; ++i) {
+        OPCHK(hipEventRecord(e0, s.st));
+        OPCHK(launch_read_stream(p, n4, sink, blocks, s.st));
+        OPCHK(hipEventRecord(e1, s.st));
+        OPCHK(hipEventSynchronize(e1));
+        float ms = 0;
+        OPCHK(hipEventElapsedTime(&ms, e0, e1));
+        gbs.push_back((double)n4 * 16 / (ms * 1e-3) / 1e9);
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    std::sort(gbs.begin(), gbs.end());
+    *best = gbs.back();
+    *median = gbs[gbs.size() / 2];
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,121 @@
+// Internal types shared by the HIP translation units of libtf_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "tf_hip.h"
+
+namespace tfk {
+
+constexpr int kWave = 64;        // CDNA wavefront
+constexpr int kBlock = 256;      // threads per workgroup for the streaming kernels
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+// One weight matrix [N rows x K] in the backend's HBM layout. The GGUF bytes are
+// split into streams so that every lane step is one aligned 16-byte load:
+//   Q8_0: q  = u8 [N][K]    q+128 (offset binary), s = f16 d [N][K/32]
+//   Q4_0: q  = u8 [N][K/2]  the GGUF nibble bytes (element j low, j+16 high), s = f16 d [N][K/32]
+//   Q4_1: q  = as Q4_0,     s = f16 pairs (d, m) [N][K/32]
+//   Q6_K: q  = u8 [N][K/2]  low nibbles of each 32-element group (element j low, j+16 high)
+//         q2 = u8 [N][K/4]  top two bits: byte j of a group holds elements j, j+8, j+16, j+24
+//         s  = i8 [N][K/16] sub-block scales, s2 = f16 d [N][K/256]
+//   F32:  q  = f32 [N][K];  F16: q = f16 [N][K]
+// Every value the GGUF block holds is kept; only its position changes, so the bytes
+// per row equal the GGUF row bytes.
+struct DevMat {
+    int type = -1;
+    int64_t K = 0, N = 0;
+    uint8_t* q = nullptr;
+    uint8_t* q2 = nullptr;
+    uint8_t* s = nullptr;
+    uint8_t* s2 = nullptr;
+    size_t gguf_bytes = 0;
+    bool valid() const { return type >= 0; }
+};
+
+// Control block in device memory; the captured decode graph reads and advances it.
+struct Ctl {
+    int32_t pos;         // position of the token this step consumes
+    int32_t att_start;   // first cache position attention covers (prefill semantics)
+    int32_t mode;        // 0: token staged by the host at hist[pos], 1: argmax of the previous step
+    int32_t spare;
+    unsigned long long key;  // argmax key of the last lm_head: (ordered value << 32) | ~index
+    int32_t last_token;
+    int32_t err;
+};
+
+__host__ __device__ inline int32_t key_to_index(unsigned long long k) {
+    return (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+}
+
+// Epilogue of a GEMV segment.
+enum GemvMode : int {
+    GEMV_STORE = 0,   // y[r] = acc (+ bias[r])
+    GEMV_RESID = 1,   // y[r] += acc; tap[r] = y[r] when tap != nullptr
+    GEMV_SILU = 2,    // paired rows: y[r] = silu(acc_gate) * acc_up
+    GEMV_LOGITS = 3,  // y[r] = acc when y != nullptr; argmax folded into ctl->key
+};
+
+struct GemvSeg {
+    DevMat a;            // weight (gate for GEMV_SILU)
+    DevMat b;            // up matrix for GEMV_SILU
+    float* y = nullptr;
+    const float* bias = nullptr;
+    float* tap = nullptr;
+    int64_t groups = 0;  // row groups in this segment
+};
+
+constexpr int kMaxSegs = 3;
+
+struct GemvArgs {
+    GemvSeg seg[kMaxSegs];
+    int n_seg = 0;
+    int64_t total_groups = 0;
+    int64_t K = 0;
+    int type = -1;
+    int mode = GEMV_STORE;
+    const float* x = nullptr;       // input vector(s): n_x rows of K floats
+    const float* norm_w = nullptr;  // rmsnorm weight applied to x in the prologue, or nullptr
+    float eps = 0;
+    Ctl* ctl = nullptr;             // GEMV_LOGITS: argmax target; bumps ctl->pos when bump_pos
+    int bump_pos = 0;
+    float* norm_out = nullptr;      // optional copy of the normed x (parity tap of the final norm)
+};
+
+struct AttnArgs {
+    const float* q;         // [H][hd] raw (bias added, not rotated)
+    const float* knew;      // [G][hd] raw
+    const float* vnew;      // [G][hd]
+    float* kc;              // this layer's K cache
+    float* vc;              // this layer's V cache
+    const float* rope_cos;  // [max_seq][hd/2]
+    const float* rope_sin;
+    float* part_o;          // [H][S][hd]
+    float* part_ml;         // [H][S][2]
+    unsigned int* counter;  // [G]
+    float* out;             // [H][hd]
+    const Ctl* ctl;
+    int H, G, hd, max_seq, layout, S, rope, store_kv;
+    int fixed_pos;          // >= 0: use this position instead of ctl->pos (op-level entry)
+    int fixed_start;
+};
+
+// Launchers (k_*.hip).
+hipError_t launch_gemv(const GemvArgs& a, int rows_per_wave, hipStream_t st);
+int64_t gemv_groups(int64_t n_rows, int rows_per_wave);
+size_t gemv_lds_bytes(int64_t K);
+hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st);
+hipError_t launch_embed(const DevMat& emb, float* x, Ctl* ctl, int32_t* hist, int D, hipStream_t st);
+hipError_t launch_dequant_rows(const DevMat& m, int64_t row0, int64_t nrows, float* out, hipStream_t st);
+hipError_t launch_repack(int type, const uint8_t* raw, int64_t K, int64_t N, DevMat& m, hipStream_t st);
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, int n, int rows, float eps, float* out,
+                               hipStream_t st);
+hipError_t launch_argmax(const float* x, int n, Ctl* ctl, hipStream_t st);
+hipError_t launch_read_stream(const float4* p, size_t n4, double* out, int blocks, hipStream_t st);
+int device_cu_count();
+
+}  // namespace tfk

@@ -1,0 +1,211 @@
+// tinferno_hip: the reference CLI (main.cpp:40-146) with the token loop on the MI355X.
+//
+// Same flags and output: prompt ids from --tokens (no BOS added, main.cpp:99), prefill,
+// then up to --n-predict tokens, stopping when the sampled id is eos after the first
+// (main.cpp:112-122); prefill/decode rates on stderr. Adds --device. --prompt needs
+// the reference's BPE tokenizer, which stays on the reference's side of the boundary.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <numeric>
+#include <random>
+#include <sstream>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "model.hpp"
+
+using namespace tfh;
+
+namespace {
+
+[[noreturn]] void die(const std::string& msg) {
+    std::fprintf(stderr, "tinferno: %s\n", msg.c_str());
+    std::exit(1);
+}
+
+double now_s() {
+    using clock = std::chrono::steady_clock;
+    return std::chrono::duration<double>(clock::now().time_since_epoch()).count();
+}
+
+void usage() {
+    std::fprintf(stderr,
+                 "tinferno_hip - tinferno's token loop on an MI355X (gfx950)\n"
+                 "\n"
+                 "usage: tinferno_hip --model PATH [options]\n"
+                 "  --model PATH         GGUF file (F32 / F16 / Q8_0 / Q4_0 / Q4_1 / Q6_K)\n"
+                 "  --tokens 1,2,3       comma-separated prompt ids\n"
+                 "  --n-predict N        tokens to generate (default 64)\n"
+                 "  --stage v0..v5       stage preset (default v2; selects the KV layout)\n"
+                 "  --threads N          accepted for compatibility (the GPU does not use it)\n"
+                 "  --temp T             temperature; 0 = greedy (default 0)\n"
+                 "  --top-p P            nucleus sampling (default 0.9)\n"
+                 "  --seed N             rng seed (default 42)\n"
+                 "  --max-seq N          KV cache length (default 4096)\n"
+                 "  --kv-layout seq|head override KV layout\n"
+                 "  --device N           HIP device (default 0)\n"
+                 "  --profile            print the per-kernel-class breakdown of one greedy pass\n");
+}
+
+std::vector<int> parse_tokens(const std::string& s) {
+    std::vector<int> v;
+    std::stringstream ss(s);
+    std::string item;
+    while (std::getline(ss, item, ','))
+        if (!item.empty()) v.push_back(std::stoi(item));
+    return v;
+}
+
+// sample_logits of sampler.cpp:15-52 (temperature, top-p, std::mt19937).
+int sample_logits(const float* logits, int n, float temperature, float top_p, std::mt19937& rng) {
+    if (temperature <= 0.0f) {
+        int b = 0;
+        for (int i = 1; i < n; ++i)
+            if (logits[i] > logits[b]) b = i;
+        return b;
+    }
+    std::vector<int> idx((size_t)n);
+    std::iota(idx.begin(), idx.end(), 0);
+    std::sort(idx.begin(), idx.end(), [&](int a, int b) { return logits[a] > logits[b]; });
+    std::vector<float> p((size_t)n);
+    const float m = logits[idx[0]];
+    float s = 0;
+    for (int i = 0; i < n; ++i) {
+        p[(size_t)i] = std::exp((logits[idx[(size_t)i]] - m) / temperature);
+        s += p[(size_t)i];
+    }
+    for (int i = 0; i < n; ++i) p[(size_t)i] /= s;
+    int last = n;
+    if (top_p < 1.0f) {
+        float acc = 0;
+        last = 0;
+        for (int i = 0; i < n; ++i) {
+            acc += p[(size_t)i];
+            last = i + 1;
+            if (acc >= top_p) break;
+        }
+        float z = 0;
+        for (int i = 0; i < last; ++i) z += p[(size_t)i];
+        for (int i = 0; i < last; ++i) p[(size_t)i] /= z;
+    }
+    std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+    const float r = dist(rng);
+    float acc = 0;
+    for (int i = 0; i < last; ++i) {
+        acc += p[(size_t)i];
+        if (r <= acc) return idx[(size_t)i];
+    }
+    return idx[(size_t)last - 1];
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    std::string model_path, prompt, token_str, stage = "v2", kv_layout;
+    int n_predict = 64, seed = 42, max_seq = 4096, device = 0;
+    float temp = 0, topp = 0.9f;
+    bool profile = false;
+    for (int i = 1; i < argc; ++i) {
+        std::string a = argv[i];
+        auto next = [&]() -> std::string {
+            if (i + 1 >= argc) die("missing value for " + a);
+            return argv[++i];
+        };
+        if (a == "--model") model_path = next();
+        else if (a == "--prompt") prompt = next();
+        else if (a == "--tokens") token_str = next();
+        else if (a == "--n-predict") n_predict = std::stoi(next());
+        else if (a == "--stage") stage = next();
+        else if (a == "--threads") (void)std::stoi(next());
+        else if (a == "--temp") temp = std::stof(next());
+        else if (a == "--top-p") topp = std::stof(next());
+        else if (a == "--seed") seed = std::stoi(next());
+        else if (a == "--max-seq") max_seq = std::stoi(next());
+        else if (a == "--kv-layout") kv_layout = next();
+        else if (a == "--device") device = std::stoi(next());
+        else if (a == "--pin" || a == "--no-bos") {
+        } else if (a == "--profile") profile = true;
+        else if (a == "-h" || a == "--help") {
+            usage();
+            return 0;
+        } else {
+            die("unknown flag " + a);
+        }
+    }
+    if (model_path.empty()) {
+        usage();
+        return 1;
+    }
+    try {
+        int hw = (int)std::thread::hardware_concurrency();
+        RunConfig cfg = stage_preset(stage, hw > 0 ? hw : 4);
+        cfg.n_predict = n_predict;
+        cfg.temperature = temp;
+        cfg.top_p = topp;
+        cfg.seed = seed;
+        cfg.max_seq = max_seq;
+        cfg.device = device;
+        cfg.profile = profile;
+        if (kv_layout == "head") cfg.kv_layout = KVLayout::HeadMajor;
+        if (kv_layout == "seq") cfg.kv_layout = KVLayout::SeqMajor;
+        if (token_str.empty())
+            die(prompt.empty() ? "empty prompt" : "--prompt needs the reference tokenizer; pass --tokens");
+        Model model(model_path, cfg);
+        std::fprintf(stderr, "%s\n", model.describe().c_str());
+        std::vector<int> ids = parse_tokens(token_str);
+        if (ids.empty()) die("empty prompt");
+
+        const auto& vocab = model.gguf().arr_str("tokenizer.ggml.tokens");
+        auto piece = [&](int id) -> std::string {
+            return (id >= 0 && id < (int)vocab.size()) ? vocab[(size_t)id] : std::string();
+        };
+        std::vector<float> logits((size_t)model.n_vocab());
+        double t0 = now_s();
+        model.prefill(ids.data(), (int)ids.size(), logits.data());
+        const double t_prefill = now_s() - t0;
+
+        std::mt19937 rng((unsigned)seed);
+        std::vector<int> gen;
+        t0 = now_s();
+        for (int i = 0; i < n_predict; ++i) {
+            const int id = temp > 0 ? sample_logits(logits.data(), model.n_vocab(), temp, topp, rng)
+                                    : model.last_argmax();
+            if (id == model.eos() && i > 0) break;
+            gen.push_back(id);
+            std::fputs(piece(id).c_str(), stdout);
+            std::fputc(' ', stdout);
+            std::fflush(stdout);
+            model.decode(id, temp > 0 ? logits.data() : nullptr);
+        }
+        const double t_decode = now_s() - t0;
+        std::fputc('\n', stdout);
+        const int n_in = (int)ids.size(), n_out = (int)gen.size();
+        std::fprintf(stderr, "\nprefill %d tok in %.3fs  (%.1f tok/s)  TTFT %.3fs\n", n_in, t_prefill,
+                     n_in / t_prefill, t_prefill);
+        std::fprintf(stderr, "decode  %d tok in %.3fs  (%.1f tok/s)\n", n_out, t_decode,
+                     n_out / std::max(t_decode, 1e-9));
+        if (profile && model.n_pos() < max_seq) {
+            const int n = std::min(8, max_seq - model.n_pos());
+            std::vector<int32_t> out((size_t)n);
+            float ms[7];
+            int32_t launches[7];
+            double bytes[7];
+            if (tf_hip_profile_generate(model.ctx(), n, out.data(), ms, launches, bytes) == 0) {
+                double tot = 0;
+                for (float m : ms) tot += m;
+                std::fprintf(stderr, "kernels over %d greedy steps:", n);
+                for (int k = 0; k < 7; ++k)
+                    std::fprintf(stderr, "  %s %.1f%% (%.1f GB/s)", tf_hip_kernel_class_name(k), tot > 0 ? 100.0 * ms[k] / tot : 0.0,
+                                 ms[k] > 0 ? bytes[k] / (ms[k] * 1e-3) / 1e9 : 0.0);
+                std::fprintf(stderr, "\n");
+            }
+        }
+    } catch (const std::exception& e) {
+        die(e.what());
+    }
+    return 0;
+}

@@ -1,0 +1,173 @@
+/*
+ * tf_hip.h - C ABI of the MI355X (gfx950) backend for tinferno's token loop.
+ *
+ * The reference runs Model::decode / Model::prefill on CPU threads (model.cpp:183-208)
+ * through free functions over raw fp32 pointers: matmul (matmul.hpp:9), apply_rope
+ * (attention.hpp:23), attn_decode (attention.hpp:27), rmsnorm/silu_mul/softmax
+ * (layers.hpp:7-10), sample_greedy (sampler.hpp:8) and KVCache (kvcache.hpp:7-30).
+ * The reference has no FFI of its own; these entry points are what its Model would
+ * bind to run the same loop on the GPU. Plain C types only: no exceptions cross
+ * this boundary, every call returns a status (0 = ok, negative = error) and the
+ * message of the last failure on a context is tf_hip_last_error().
+ *
+ * Threading: one context per host thread; calls on one context are serialised by
+ * the caller, as the reference's Model is (model.hpp:24-90). Host buffers are
+ * read/written synchronously: outputs are ready when a call returns.
+ */
+#ifndef TF_HIP_H
+#define TF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TF_HIP_OK 0
+#define TF_HIP_EINVAL -1   /* bad argument, shape or state (std::runtime_error in the reference) */
+#define TF_HIP_ERANGE -2   /* max_seq exceeded or token out of range (model.cpp:185, 198) */
+#define TF_HIP_ENOMEM -3   /* device allocation failed */
+#define TF_HIP_EDEVICE -4  /* HIP runtime error */
+#define TF_HIP_ESTATE -5   /* required tensors not uploaded */
+
+/* ggml tensor types accepted by the token loop (tensor.cpp:18-28) */
+#define TF_HIP_TYPE_F32 0
+#define TF_HIP_TYPE_F16 1
+#define TF_HIP_TYPE_Q4_0 2
+#define TF_HIP_TYPE_Q4_1 3
+#define TF_HIP_TYPE_Q8_0 8
+#define TF_HIP_TYPE_Q6_K 14
+
+/* KV cache layouts (kvcache.cpp:21-29) */
+#define TF_HIP_KV_SEQ_MAJOR 0  /* [layer][pos][kv_head][head_dim] */
+#define TF_HIP_KV_HEAD_MAJOR 1 /* [layer][kv_head][pos][head_dim] */
+
+/* Model hyperparameters as Model::Model derives them (model.cpp:9-41). */
+typedef struct tf_hip_hparams {
+    int32_t n_vocab;
+    int32_t n_embd;
+    int32_t n_ff;
+    int32_t n_layer;
+    int32_t n_head;
+    int32_t n_kv_head;
+    int32_t head_dim; /* n_embd / n_head (model.cpp:22-24) */
+    int32_t max_seq;  /* RunConfig::max_seq (common.hpp:112) */
+    int32_t kv_layout;
+    float rms_eps;
+} tf_hip_hparams;
+
+/* Tensor slots (the names Model binds, model.cpp:43-65). */
+#define TF_HIP_SLOT_TOKEN_EMBD 0  /* token_embd.weight [n_vocab x n_embd] */
+#define TF_HIP_SLOT_OUTPUT_NORM 1 /* output_norm.weight F32 [n_embd] */
+#define TF_HIP_SLOT_OUTPUT 2      /* output.weight; absent = tied to token_embd (model.cpp:45-46) */
+#define TF_HIP_LAYER_ATTN_NORM 0
+#define TF_HIP_LAYER_Q 1
+#define TF_HIP_LAYER_K 2
+#define TF_HIP_LAYER_V 3
+#define TF_HIP_LAYER_O 4
+#define TF_HIP_LAYER_BQ 5 /* optional F32 biases (model.cpp:58-60, 85-89) */
+#define TF_HIP_LAYER_BK 6
+#define TF_HIP_LAYER_BV 7
+#define TF_HIP_LAYER_FFN_NORM 8
+#define TF_HIP_LAYER_GATE 9
+#define TF_HIP_LAYER_UP 10
+#define TF_HIP_LAYER_DOWN 11
+#define TF_HIP_LAYER_COUNT 12
+#define TF_HIP_SLOT_LAYER(layer, kind) (16 + (layer) * TF_HIP_LAYER_COUNT + (kind))
+
+typedef struct tf_hip_ctx tf_hip_ctx;
+
+/* Context: device memory for weights, the fp32 KV cache ([n_layer][n_kv_head*max_seq*head_dim]
+ * for K and for V, as KVCache::init, kvcache.cpp:5-14), activations and the decode graph.
+ * Replaces Model::Model's buffer set-up (model.cpp:67-77). */
+int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out);
+int tf_hip_destroy(tf_hip_ctx* ctx);
+const char* tf_hip_last_error(const tf_hip_ctx* ctx);
+
+/* Copies one GGUF tensor (raw GGUF row bytes, ne0 = row length, ne1 = rows) to HBM and
+ * converts it to the backend's layout. Replaces the mmap binding of model.cpp:43-65. */
+int tf_hip_upload_tensor(tf_hip_ctx* ctx, int slot, int ggml_type, int64_t ne0, int64_t ne1, const void* host,
+                         size_t nbytes);
+
+/* RoPE angle tables: cos/sin of (float)pos * freq[i] for pos < n_pos, i < half_dim, computed
+ * by the host exactly as rope_one does (attention.cpp:31-41) so device and host use
+ * identical angles. Row-major [n_pos][half_dim]; n_pos must be >= max_seq. */
+int tf_hip_set_rope_table(tf_hip_ctx* ctx, const float* cos_tab, const float* sin_tab, int32_t n_pos,
+                          int32_t half_dim);
+
+/* Model::prefill (model.cpp:183-195): consumes tokens[0..n) at positions n_pos.. and writes
+ * the last token's logits (n_vocab floats) and/or its greedy argmax. Either output may be
+ * NULL. Attention covers only this call's tokens, as attn_prefill does (attention.cpp:82-111). */
+int tf_hip_prefill(tf_hip_ctx* ctx, const int32_t* tokens, int32_t n, float* logits, int32_t* argmax);
+
+/* Model::decode (model.cpp:197-208): one token at n_pos, logits and/or argmax (either may be NULL). */
+int tf_hip_decode(tf_hip_ctx* ctx, int32_t token, float* logits, int32_t* argmax);
+
+/* The greedy loop of bench_e2e.cpp:49-54 / main.cpp:112-122 run on the device: n times,
+ * tok = argmax of the current logits (sample_greedy, sampler.cpp:8-13), out_tokens[i] = tok,
+ * decode(tok). Requires a prior prefill or decode. No host round trip between steps. */
+int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
+
+/* Model::reset (model.cpp:80-83): n_pos = 0 and the KV cache cleared. */
+int tf_hip_reset(tf_hip_ctx* ctx);
+int tf_hip_get_pos(const tf_hip_ctx* ctx);
+
+/* Parity taps for the last token processed: the residual stream after layer l (l < n_layer),
+ * or the output_norm-ed vector fed to the lm_head (l == n_layer); n_embd floats. */
+int tf_hip_get_layer_act(tf_hip_ctx* ctx, int32_t layer, float* out);
+
+/* KV rows [pos0, pos0+n) of one layer in logical order [n][n_kv_head][head_dim], K (which = 0)
+ * or V (which = 1), whatever the layout (KVCache::k_at / v_at, kvcache.cpp:38-43). */
+int tf_hip_read_kv(tf_hip_ctx* ctx, int32_t layer, int32_t which, int32_t pos0, int32_t n, float* out);
+
+/* Timing of the last tf_hip_generate call, from HIP events on the context's stream:
+ * total device milliseconds of the whole call, and of the dominant decode kernel summed over
+ * the call together with its launch count. */
+int tf_hip_last_timing(const tf_hip_ctx* ctx, float* total_ms, float* kernel_ms, int32_t* kernel_launches,
+                       char* kernel_name, int32_t name_len);
+
+/* The loop of tf_hip_generate with each kernel launched on its own (no graph) and bracketed
+ * by HIP events on the context stream. Per kernel class k < TF_HIP_KERNEL_CLASSES it
+ * reports the summed device milliseconds, the launch count and the algorithmic bytes
+ * (weights read; attention reports 0). Classes: 0 embedding, 1 QKV GEMV, 2 attention,
+ * 3 attn_output GEMV, 4 gate/up GEMV, 5 down GEMV, 6 lm_head GEMV (tf_hip_kernel_class_name). */
+#define TF_HIP_KERNEL_CLASSES 7
+int tf_hip_profile_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens, float* ms_by_class,
+                            int32_t* launches_by_class, double* bytes_by_class);
+const char* tf_hip_kernel_class_name(int32_t k);
+
+/* ---------------------------------------------------------------- op-level entry points
+ * Single calls of one backend kernel on host buffers (copied in and out), for the
+ * per-op parity tests. They run on `device` with temporary allocations. */
+
+/* dequant_row over rows [row0, row0+nrows) of a GGUF tensor (quant.cpp:133-145): out is
+ * [nrows][ne0] fp32. Bit-exact with the reference. */
+int tf_hip_dequant_rows(int device, int ggml_type, const void* w, int64_t ne0, int64_t ne1, int64_t row0,
+                        int64_t nrows, float* out);
+
+/* matmul (matmul.cpp:64-73): y[m][n] = sum_k x[m][k] * W[n][k] for m < n_rows_x.
+ * With n_rows_x == 1 this is the decode GEMV; larger values take the prefill GEMM. */
+int tf_hip_matmul(int device, int ggml_type, const void* w, int64_t ne0, int64_t ne1, const float* x,
+                  int32_t n_rows_x, float* y);
+
+/* rmsnorm (layers.cpp:7-12) of n_rows rows of length n. */
+int tf_hip_rmsnorm(int device, const float* x, const float* w, int32_t n, int32_t n_rows, float eps, float* out);
+
+/* attn_decode (attention.cpp:55-80) for one layer: q [n_heads][hd] (already rotated),
+ * k_rows/v_rows [n_pos][n_kv][hd] logical rows stored into a cache of the given layout and
+ * max_seq before the kernel runs; out [n_heads][hd]. */
+int tf_hip_attn_decode(int device, const float* q, const float* k_rows, const float* v_rows, int32_t n_heads,
+                       int32_t n_kv, int32_t hd, int32_t n_pos, int32_t max_seq, int32_t layout, float* out);
+
+/* sample_greedy (sampler.cpp:8-13): index of the first maximum. */
+int tf_hip_argmax(int device, const float* x, int32_t n, int32_t* out);
+
+/* Read-only HBM stream (the GPU analogue of bench/stream.c:128-141): sums nbytes of device
+ * memory `iters` times; reports the best and median GB/s over the iterations. */
+int tf_hip_read_stream(int device, size_t nbytes, int32_t iters, double* best_gbs, double* median_gbs);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TF_HIP_H */
