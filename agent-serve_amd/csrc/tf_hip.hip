@@ -555,7 +555,6 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
             case TF_HIP_LAYER_DOWN: K = p.n_ff; N = p.n_embd; break;
         }
     }
-    if (slot == TF_HIP_SLOT_TOKEN_EMBD && ne0 == K && ne1 >= N) N = ne1;  // embedding may hold extra rows
     if (ne0 != K || ne1 != N)
         return fail(c, TF_HIP_EINVAL, "tensor shape [" + std::to_string(ne0) + " x " + std::to_string(ne1) +
                                            "] does not match the model, want [" + std::to_string(K) + " x " +

@@ -46,7 +46,8 @@ std::vector<float> rope_freqs(const RopeParams& rp) {
                 f /= rp.scale;
             } else {
                 const float smooth = (rp.orig_ctx / wavelen - rp.low_freq_f) / (rp.high_freq_f - rp.low_freq_f);
-                f = (1.0f - smooth) * f / rp.scale + smooth * f;
+                // the reference's -mfma build fuses smooth * f into the sum
+                f = std::fma(smooth, f, (1.0f - smooth) * f / rp.scale);
             }
         }
         freq[(size_t)i] = f;

@@ -302,7 +302,7 @@ void orc_rope_freqs(float* freq, int n_rot, float theta, int llama3, float scale
                 f /= scale;
             } else {
                 const float smooth = (orig_ctx / wavelen - low_freq_f) / (high_freq_f - low_freq_f);
-                f = (1.0f - smooth) * f / scale + smooth * f;
+                f = fmaf(smooth, f, (1.0f - smooth) * f / scale); /* g++ fuses smooth * f */
             }
         }
         freq[i] = f;

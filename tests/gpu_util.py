@@ -1,0 +1,83 @@
+"""Helpers for the GPU parity tests: random GGUF rows and the model-level comparison."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from conftest import n_threads, rel_err
+from oracle.bind import OracleModel, oracle_lib
+from rows import BLOCK, random_rows, row_bytes  # noqa: F401
+
+def oracle_dequant(t: int, rows: np.ndarray, k: int) -> np.ndarray:
+    L = oracle_lib()
+    out = np.zeros((rows.shape[0], k), np.float32)
+    for i in range(rows.shape[0]):
+        r = np.ascontiguousarray(rows[i])
+        assert L.orc_dequant_row(t, r.ctypes.data, k, out[i].ctypes.data_as(C.POINTER(C.c_float))) == 0
+    return out
+
+
+def oracle_matmul(t: int, rows: np.ndarray, k: int, x: np.ndarray) -> np.ndarray:
+    L = oracle_lib()
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    n = rows.shape[0]
+    y = np.zeros((x.shape[0], n), np.float32)
+    fp = C.POINTER(C.c_float)
+    assert L.orc_matmul(y.ctypes.data_as(fp), x.ctypes.data_as(fp), x.shape[0], t,
+                        np.ascontiguousarray(rows).ctypes.data, n, k, n_threads()) == 0
+    return y
+
+
+def model_parity(pkg, path, prompt, n, max_seq, layout, tol=1e-3, taps=True):
+    """Decode the oracle's greedy stream on both sides, comparing logits, argmax and
+    per-layer activations at every step; then the device greedy loop from a reset.
+    Returns (oracle ids, max logits rel err, max tap rel err, min top-2 margin)."""
+    orc = OracleModel(path, max_seq=max_seq, kv_layout=layout, n_threads=n_threads())
+    hip = pkg.HipModel(path, max_seq=max_seq, kv_layout=layout)
+    try:
+        lo = orc.prefill(prompt)
+        lh, am = hip.prefill(prompt)
+        worst, worst_tap, margin = rel_err(lh, lo), 0.0, np.inf
+
+        def check_taps():
+            w = 0.0
+            for layer in range(orc.n_layer + 1):
+                e = rel_err(hip.layer_act(layer), orc.tap(layer))
+                assert e <= tol, f"layer {layer} activations rel err {e:.3e}"
+                w = max(w, e)
+            return w
+
+        if taps:
+            worst_tap = check_taps()
+        ids = []
+        for step in range(n):
+            top2 = np.sort(lo)[-2:]
+            margin = min(margin, float(top2[1] - top2[0]))
+            t = int(np.argmax(lo))
+            assert am == t, f"step {step}: device argmax {am} != oracle {t} (margin {top2[1] - top2[0]:.3e})"
+            ids.append(t)
+            lo = orc.decode(t)
+            lh, am = hip.decode(t)
+            e = rel_err(lh, lo)
+            assert e <= tol, f"step {step}: logits rel err {e:.3e}"
+            worst = max(worst, e)
+        if taps:
+            worst_tap = max(worst_tap, check_taps())
+        # KV cache contents, layer 0 and last layer, logical order
+        for layer in (0, orc.n_layer - 1):
+            for which in (0, 1):
+                kv_h = hip.read_kv(layer, which, 0, len(prompt) + n)
+                kv_o = orc.read_kv(layer, which, 0, len(prompt) + n)
+                e = rel_err(kv_h, kv_o)
+                assert e <= tol, f"KV layer {layer} which {which} rel err {e:.3e}"
+        # the on-device greedy loop reproduces the stream
+        hip.reset()
+        _, am0 = hip.prefill(prompt, want_logits=False)
+        assert am0 == ids[0]
+        gen = hip.generate(n)
+        assert gen.tolist() == ids, f"device greedy loop {gen.tolist()} != oracle {ids}"
+        return ids, worst, worst_tap, margin
+    finally:
+        hip.close()
+        orc.close()

@@ -1,0 +1,153 @@
+"""Op-level parity of the HIP kernels against the oracle, through the C ABI.
+
+Dequantization and argmax are integer/index work: bit-exact. GEMV, RMSNorm and attention
+are fp32 reductions in a different order than the AVX2 reference: bounded by a
+per-element error budget stated in each test.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from gpu_util import oracle_dequant, oracle_matmul, random_rows
+from oracle.bind import oracle_lib
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q8_0": 8, "Q6_K": 14}
+
+
+@pytest.mark.parametrize("fmt", list(FORMATS))
+def test_dequant_rows_bit_exact(pkg, fmt):
+    t = FORMATS[fmt]
+    rng = np.random.default_rng(7 + t)
+    k = 512 if t != 0 else 96
+    rows = random_rows(rng, t, k, 37)
+    got = pkg.dequant_rows(t, rows, k, 37)
+    want = oracle_dequant(t, rows, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # a sub-range of rows, as the embedding lookup reads one row
+    got = pkg.dequant_rows(t, rows, k, 37, row0=11, nrows=3)
+    assert np.array_equal(got.view(np.uint32), want[11:14].view(np.uint32))
+
+
+# (K, N) of the workloads' matrices (some N trimmed to keep the oracle fast)
+GEMV_SHAPES = {
+    8: [(2048, 512), (2048, 2048), (8192, 384), (896, 128), (896, 4864), (4864, 896), (1536, 256), (8960, 256),
+        (2048, 8200)],
+    2: [(2048, 512), (8192, 256), (256, 64)],
+    3: [(8192, 256), (2048, 96)],
+    14: [(2048, 1024), (1536, 128), (256, 40)],
+    0: [(32, 64), (64, 32), (2048, 64)],
+    1: [(256, 64), (2048, 33)],
+}
+
+
+@pytest.mark.parametrize("t,k,n", [(t, k, n) for t, shapes in GEMV_SHAPES.items() for (k, n) in shapes])
+def test_gemv_matches_oracle(pkg, t, k, n):
+    """y = W x: |y - y_oracle| <= 2e-5 * sum_k |x_k w_nk| per output (fp32 reassociation)."""
+    rng = np.random.default_rng(1000 + k + n + t)
+    rows = random_rows(rng, t, k, n)
+    x = rng.standard_normal(k).astype(np.float32)
+    got = pkg.matmul(t, rows, k, n, x)[0]
+    want = oracle_matmul(t, rows, k, x)[0]
+    budget = np.abs(oracle_dequant(t, rows, k)).astype(np.float64) @ np.abs(x).astype(np.float64)
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= 2e-5 * budget + 1e-30), f"max err/budget {np.max(err / (budget + 1e-30)):.3e}"
+
+
+def test_matmul_several_rows(pkg):
+    rng = np.random.default_rng(3)
+    k, n = 2048, 256
+    rows = random_rows(rng, 8, k, n)
+    x = rng.standard_normal((5, k)).astype(np.float32)
+    got = pkg.matmul(8, rows, k, n, x)
+    want = oracle_matmul(8, rows, k, x)
+    assert rel_err(got, want) < 1e-5
+
+
+@pytest.mark.parametrize("n", [32, 896, 2048, 8960])
+def test_rmsnorm(pkg, n):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((4, n)) * 3).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    got = pkg.rmsnorm(x, w, 1e-5)
+    L = oracle_lib()
+    fp = C.POINTER(C.c_float)
+    for i in range(4):
+        want = np.zeros(n, np.float32)
+        xi = np.ascontiguousarray(x[i])
+        L.orc_rmsnorm(want.ctypes.data_as(fp), xi.ctypes.data_as(fp), w.ctypes.data_as(fp), n, 1e-5)
+        # fp64 sum of squares in another order: at most one ulp of the scale
+        assert rel_err(got[i], want) <= 2.5e-7
+
+
+ATTN_CASES = [  # heads, kv heads, head_dim, n_pos, max_seq
+    (32, 8, 64, 1, 64), (32, 8, 64, 7, 64), (32, 8, 64, 38, 512), (32, 8, 64, 300, 512),
+    (14, 2, 64, 144, 256), (12, 2, 128, 1000, 2048), (12, 2, 128, 4352, 8192), (4, 2, 8, 9, 16),
+]
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("h,g,hd,n_pos,max_seq", ATTN_CASES)
+def test_attn_decode(pkg, layout, h, g, hd, n_pos, max_seq):
+    rng = np.random.default_rng(h * 1000 + n_pos)
+    q = rng.standard_normal((h, hd)).astype(np.float32)
+    k = rng.standard_normal((n_pos, g, hd)).astype(np.float32)
+    v = rng.standard_normal((n_pos, g, hd)).astype(np.float32)
+    got = pkg.attn_decode(q, k, v, max_seq, layout)
+    # oracle over the same cache layout
+    cache_k = np.zeros(g * max_seq * hd, np.float32)
+    cache_v = np.zeros_like(cache_k)
+    for p in range(n_pos):
+        for j in range(g):
+            o = (j * max_seq + p) * hd if layout else (p * g + j) * hd
+            cache_k[o:o + hd] = k[p, j]
+            cache_v[o:o + hd] = v[p, j]
+    want = np.zeros((h, hd), np.float32)
+    scores = np.zeros(max_seq + 1, np.float32)
+    fp = C.POINTER(C.c_float)
+    oracle_lib().orc_attn_decode(want.ctypes.data_as(fp), q.ctypes.data_as(fp), cache_k.ctypes.data_as(fp),
+                                 cache_v.ctypes.data_as(fp), layout, g, max_seq, h, hd, n_pos,
+                                 scores.ctypes.data_as(fp))
+    assert rel_err(got, want) <= 1e-5
+
+
+def test_attn_decode_single_position_returns_v(pkg):
+    """n_pos = 1: softmax weight 1, the output head is its kv head's v (attention.cpp:55-80)."""
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((8, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 64)).astype(np.float32)
+    got = pkg.attn_decode(q, k, v, 16, 0)
+    assert np.array_equal(got, np.repeat(v[0], 4, axis=0))
+
+
+def test_attn_decode_zero_query_is_mean_of_v(pkg):
+    rng = np.random.default_rng(6)
+    n_pos = 50
+    q = np.zeros((4, 64), np.float32)
+    k = rng.standard_normal((n_pos, 1, 64)).astype(np.float32)
+    v = rng.standard_normal((n_pos, 1, 64)).astype(np.float32)
+    got = pkg.attn_decode(q, k, v, 64, 1)
+    assert rel_err(got[0], v[:, 0].mean(axis=0)) < 1e-5
+
+
+def test_argmax_first_maximum(pkg):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal(151936).astype(np.float32)
+    assert pkg.argmax(x) == int(np.argmax(x))
+    x[[17, 90000, 151935]] = 50.0  # ties: the lowest index wins (sampler.cpp:8-13)
+    assert pkg.argmax(x) == 17
+    y = -np.abs(rng.standard_normal(1000).astype(np.float32)) - 1
+    y[999] = -0.5
+    assert pkg.argmax(y) == 999
+    z = np.full(64, -0.0, np.float32)
+    z[10] = 0.0  # -0 and +0 compare equal: the first one wins
+    assert pkg.argmax(z) == 0
+
+
+def test_read_stream_runs(pkg):
+    best, med = pkg.read_stream(1 << 28, iters=3)
+    assert best > 100.0 and med > 0
