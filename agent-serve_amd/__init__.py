@@ -103,6 +103,8 @@ def host_lib() -> C.CDLL:
         "tfh_synth_preset_info": (C.c_int, [C.c_char_p, _i32p]),
         "tfh_synth_prompt": (C.c_int, [C.c_int64, C.c_int32, C.c_int32, _i32p]),
         "tfh_rope_tables": (C.c_int, [C.c_float, C.c_int32, C.c_int32, _f32p, _f32p]),
+        "tfh_quantize_row": (C.c_int, [C.c_int32, _f32p, C.c_int64, vp]),
+        "tfh_gguf_summary": (C.c_int, [C.c_char_p, _u64p, C.c_char_p, C.c_int32]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -142,6 +144,25 @@ def synth_prompt(seed: int, n: int, n_vocab: int) -> np.ndarray:
     if n > 0 and host_lib().tfh_synth_prompt(seed, n, n_vocab, _i(out)) != 0:
         raise RuntimeError(host_lib().tfh_global_error().decode())
     return out
+
+
+def quantize_row(ggml_type: int, x: np.ndarray) -> np.ndarray:
+    """The synthetic writer's quantizer for one row (GGUF block bytes)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    blk = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 8: (32, 34), 14: (256, 210)}[ggml_type]
+    out = np.zeros(len(x) // blk[0] * blk[1], np.uint8)
+    if host_lib().tfh_quantize_row(ggml_type, _f(x), len(x), out.ctypes.data) != 0:
+        raise RuntimeError(host_lib().tfh_global_error().decode())
+    return out
+
+
+def gguf_summary(path: str) -> dict:
+    out = np.zeros(3, np.uint64)
+    arch = C.create_string_buffer(64)
+    if host_lib().tfh_gguf_summary(str(path).encode(), out.ctypes.data_as(_u64p), arch, 64) != 0:
+        raise RuntimeError(host_lib().tfh_global_error().decode())
+    return {"n_tensors": int(out[0]), "weight_bytes": int(out[1]), "file_size": int(out[2]),
+            "arch": arch.value.decode()}
 
 
 def rope_tables(theta: float, n_rot: int, n_pos: int):

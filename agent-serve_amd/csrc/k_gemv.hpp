@@ -1,0 +1,238 @@
+// Fused dequant-GEMV for the decode step (the matmul of matmul.cpp:22-32 with M = 1,
+// which is 99% of the reference's decode time).
+//
+// One workgroup = 4 wavefronts. The prologue stages x (optionally RMSNorm-ed, the
+// rmsnorm of layers.cpp:7-12 fused in) and its 16-element partial sums in LDS. Each
+// wavefront then owns groups of R consecutive output rows: lanes stride over the row
+// in 16-byte steps (formats.hpp), keep U steps of all R rows in flight, and fold the
+// 64 lane partials with a butterfly. Epilogues fuse the QKV bias (model.cpp:122-124),
+// the residual adds (model.cpp:131, 141), SiLU*up (layers.cpp:14-19) and the greedy
+// argmax of the lm_head (sampler.cpp:8-13).
+#pragma once
+#include "formats.hpp"
+
+namespace tfk {
+namespace gemv_detail {
+
+__device__ void stage_x(const GemvArgs& a, float* xs, float* x16, bool need_sums) {
+    const int K = (int)a.K;
+    const int tid = threadIdx.x;
+    if (a.norm_w) {
+        __shared__ double red[kWavesPerBlock];
+        double ss = 0;
+        for (int k = tid; k < K; k += kBlock) {
+            const double v = (double)a.x[k];
+            ss += v * v;  // exact in fp64, as the reference's accumulation terms
+        }
+        ss = wave_sum_d(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        const float inv = 1.0f / sqrtf((float)(ss / K) + a.eps);
+        for (int k = tid; k < K; k += kBlock) xs[k] = a.x[k] * inv * a.norm_w[k];
+    } else {
+        for (int k = tid; k < K; k += kBlock) xs[k] = a.x[k];
+    }
+    __syncthreads();
+    if (a.norm_out && blockIdx.x == 0)
+        for (int k = tid; k < K; k += kBlock) a.norm_out[k] = xs[k];
+    if (need_sums) {
+        for (int c = tid; c < K / 16; c += kBlock) {
+            const float4* p = (const float4*)(xs + 16 * c);
+            const float4 u = p[0], v = p[1], w = p[2], z = p[3];
+            x16[c] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w)) + ((w.x + w.y) + (w.z + w.w)) +
+                     ((z.x + z.y) + (z.z + z.w));
+        }
+        __syncthreads();
+    }
+}
+
+template <int NR>
+__device__ __forceinline__ float pick(const float (&v)[NR], int i) {
+    float r = v[0];
+#pragma unroll
+    for (int j = 1; j < NR; ++j) r = (i == j) ? v[j] : r;
+    return r;
+}
+
+// R rows per group; SILU pairs R gate rows with the same R up rows (NR = 2R streams).
+// A wave walks tiles (group g, tile ti): tile ti of a group covers steps
+// ti*64U + 64u + lane (u < U) of its NR rows. Tiles are double-buffered in registers:
+// the loads of tile t+1 are in flight while tile t is consumed, and the loads of a
+// wave's first tile are issued before the x prologue, which does not need them.
+template <int T, int R, int MODE, int U>
+__global__ __launch_bounds__(kBlock) void k_gemv(const GemvArgs a) {
+    using F = Fmt<T>;
+    using Raw = typename F::Raw;
+    constexpr bool SILU = MODE == GEMV_SILU;
+    constexpr int NR = SILU ? 2 * R : R;
+    extern __shared__ float smem[];
+    float* xs = smem;
+    float* x16 = smem + a.K;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int S = (int)(a.K / F::E);
+    const int TPG = (S + kWave * U - 1) / (kWave * U);
+    const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+
+    auto locate = [&](int64_t g, int& si, int64_t& row0) {
+        si = 0;
+        int64_t gg = g;
+        while (si + 1 < a.n_seg && gg >= a.seg[si].groups) {
+            gg -= a.seg[si].groups;
+            ++si;
+        }
+        row0 = gg * R;
+    };
+    auto load_tile = [&](int64_t g, int ti, Raw (&w)[U][NR]) {
+        int si;
+        int64_t row0;
+        locate(g, si, row0);
+        const GemvSeg& sg = a.seg[si];
+        const int64_t N = sg.a.N;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t row = row0 + r < N ? row0 + r : N - 1;  // tail rows re-read a valid row
+            const RowPtr pa = F::row(sg.a, row);
+            RowPtr pb = pa;
+            if (SILU) pb = F::row(sg.b, row);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int s = ti * kWave * U + u * kWave + lane;
+                if (s < S) {
+                    w[u][r] = F::load(pa, s);
+                    if (SILU) w[u][R + r] = F::load(pb, s);
+                }
+            }
+        }
+    };
+
+    int64_t g = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+    int ti = 0;
+    Raw wa[U][NR], wb[U][NR];
+    if (g < a.total_groups) load_tile(g, 0, wa);
+    stage_x(a, xs, x16, F::kNeedSums);
+
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
+    unsigned long long best = 0;
+
+    auto epilogue = [&](int64_t gq) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[r] = wave_sum(acc[r]);
+        int si;
+        int64_t row0;
+        locate(gq, si, row0);
+        const GemvSeg& sg = a.seg[si];
+        const int64_t row = row0 + lane;
+        if (lane < R && row < sg.a.N) {
+            const float v = pick<NR>(acc, lane);
+            if (SILU) {
+                const float up = pick<NR>(acc, lane + R);
+                sg.y[row] = (v / (1.0f + expf(-v))) * up;
+            } else if (MODE == GEMV_STORE) {
+                sg.y[row] = sg.bias ? v + sg.bias[row] : v;
+            } else if (MODE == GEMV_RESID) {
+                const float nv = sg.y[row] + v;
+                sg.y[row] = nv;
+                if (sg.tap) sg.tap[row] = nv;
+            } else {  // GEMV_LOGITS
+                if (sg.y) sg.y[row] = v;
+                const unsigned long long k = argmax_key(v, row);
+                best = k > best ? k : best;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
+    };
+    // consume `cur` (tile ti of group g) while `nxt` receives the following tile
+    auto step = [&](Raw (&cur)[U][NR], Raw (&nxt)[U][NR]) -> bool {
+        int64_t gn = g;
+        int tn = ti + 1;
+        if (tn == TPG) {
+            tn = 0;
+            gn = g + stride;
+        }
+        const bool more = gn < a.total_groups;
+        if (more) load_tile(gn, tn, nxt);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = ti * kWave * U + u * kWave + lane;
+            if (s < S) {
+#pragma unroll
+                for (int r = 0; r < NR; ++r) acc[r] += F::dot(cur[u][r], xs, x16, s);
+            }
+        }
+        if (ti == TPG - 1) epilogue(g);
+        g = gn;
+        ti = tn;
+        return more;
+    };
+    if (g < a.total_groups) {
+        for (;;) {
+            if (!step(wa, wb)) break;
+            if (!step(wb, wa)) break;
+        }
+    }
+
+    if (MODE == GEMV_LOGITS) {
+        __shared__ unsigned long long wbest[kWavesPerBlock];
+        best = wave_max_u64(best);
+        if (lane == 0) wbest[wave] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long b = wbest[0];
+            for (int i = 1; i < kWavesPerBlock; ++i) b = wbest[i] > b ? wbest[i] : b;
+            atomicMax(&a.ctl->key, b);
+            if (a.bump_pos && blockIdx.x == 0) a.ctl->pos += 1;
+        }
+    }
+}
+
+template <int T, int R, int U>
+hipError_t launch_t(const GemvArgs& a, int blocks, size_t lds, hipStream_t st) {
+    switch (a.mode) {
+        case GEMV_STORE: hipLaunchKernelGGL((k_gemv<T, R, GEMV_STORE, U>), dim3(blocks), dim3(kBlock), lds, st, a); break;
+        case GEMV_RESID: hipLaunchKernelGGL((k_gemv<T, R, GEMV_RESID, U>), dim3(blocks), dim3(kBlock), lds, st, a); break;
+        case GEMV_SILU: hipLaunchKernelGGL((k_gemv<T, R, GEMV_SILU, U>), dim3(blocks), dim3(kBlock), lds, st, a); break;
+        case GEMV_LOGITS: hipLaunchKernelGGL((k_gemv<T, R, GEMV_LOGITS, U>), dim3(blocks), dim3(kBlock), lds, st, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Steps in flight per row and tile (U): enough to cover the row (up to 8 x 16 B per lane),
+// fewer when many rows share a wave.
+template <int T>
+hipError_t launch_r(const GemvArgs& a, int R, int blocks, size_t lds, hipStream_t st) {
+    const int S = (int)(a.K / Fmt<T>::E);
+    const int NR = a.mode == GEMV_SILU ? 2 * R : R;
+    int U = (S + kWave - 1) / kWave;
+    const int cap = NR >= 4 ? 2 : NR >= 2 ? 4 : 8;
+    U = U > cap ? cap : U;
+    U = U >= 8 ? 8 : U >= 4 ? 4 : U >= 2 ? 2 : 1;
+    switch (R * 16 + U) {
+        case 1 * 16 + 1: return launch_t<T, 1, 1>(a, blocks, lds, st);
+        case 1 * 16 + 2: return launch_t<T, 1, 2>(a, blocks, lds, st);
+        case 1 * 16 + 4: return launch_t<T, 1, 4>(a, blocks, lds, st);
+        case 1 * 16 + 8: return launch_t<T, 1, 8>(a, blocks, lds, st);
+        case 2 * 16 + 1: return launch_t<T, 2, 1>(a, blocks, lds, st);
+        case 2 * 16 + 2: return launch_t<T, 2, 2>(a, blocks, lds, st);
+        case 2 * 16 + 4: return launch_t<T, 2, 4>(a, blocks, lds, st);
+        case 4 * 16 + 1: return launch_t<T, 4, 1>(a, blocks, lds, st);
+        case 4 * 16 + 2: return launch_t<T, 4, 2>(a, blocks, lds, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace gemv_detail
+
+// Instantiated once per format in k_gemv_<format>.hip.
+template <int T>
+hipError_t launch_gemv_fmt(const GemvArgs& a, int R, int blocks, size_t lds, hipStream_t st) {
+    return gemv_detail::launch_r<T>(a, R, blocks, lds, st);
+}
+
+}  // namespace tfk

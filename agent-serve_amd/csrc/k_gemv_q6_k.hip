@@ -1,0 +1,6 @@
+// GEMV kernels for Q6_K weights (k_gemv.hpp).
+#include "k_gemv.hpp"
+
+namespace tfk {
+template hipError_t launch_gemv_fmt<TF_HIP_TYPE_Q6_K>(const GemvArgs&, int, int, size_t, hipStream_t);
+}  // namespace tfk

@@ -9,29 +9,12 @@ namespace tfk {
 
 namespace {
 
-// Dequantize `count` steps of row r starting at step s0 (one thread per step).
-template <int T>
-__device__ void dequant_steps(const DevMat& m, int64_t r, int s, float* out) {
-    using F = Fmt<T>;
-    const RowPtr p = F::row(m, r);
-    F::dequant(F::load(p, s), out);
-}
-
-__device__ void dequant_step_rt(const DevMat& m, int64_t r, int s, float* out) {
-    switch (m.type) {
-        case TF_HIP_TYPE_Q8_0: dequant_steps<TF_HIP_TYPE_Q8_0>(m, r, s, out); break;
-        case TF_HIP_TYPE_Q4_0: dequant_steps<TF_HIP_TYPE_Q4_0>(m, r, s, out); break;
-        case TF_HIP_TYPE_Q4_1: dequant_steps<TF_HIP_TYPE_Q4_1>(m, r, s, out); break;
-        case TF_HIP_TYPE_Q6_K: dequant_steps<TF_HIP_TYPE_Q6_K>(m, r, s, out); break;
-        case TF_HIP_TYPE_F16: dequant_steps<TF_HIP_TYPE_F16>(m, r, s, out); break;
-        case TF_HIP_TYPE_F32: dequant_steps<TF_HIP_TYPE_F32>(m, r, s, out); break;
-    }
-}
-
 // dequant_row of the token's embedding row (model.cpp:199). The token is the one the
 // host staged at hist[pos] (mode 0) or the previous step's argmax (mode 1), which is
 // recorded there; the argmax key is cleared for this step's lm_head.
+template <int T>
 __global__ __launch_bounds__(kBlock) void k_embed(const DevMat emb, float* x, Ctl* ctl, int32_t* hist, int D) {
+    using F = Fmt<T>;
     __shared__ int tok;
     if (threadIdx.x == 0) {
         const int p = ctl->pos;
@@ -46,25 +29,27 @@ __global__ __launch_bounds__(kBlock) void k_embed(const DevMat emb, float* x, Ct
         ctl->key = 0ull;
     }
     __syncthreads();
-    const int E = fmt_step_elems(emb.type);
-    const int steps = D / E;
-    for (int s = threadIdx.x; s < steps; s += kBlock) {
-        float v[32];
-        dequant_step_rt(emb, tok, s, v);
-        for (int i = 0; i < E; ++i) x[(int64_t)s * E + i] = v[i];
+    const RowPtr rp = F::row(emb, tok);
+    for (int s = threadIdx.x; s < D / F::E; s += kBlock) {
+        float v[F::E];
+        F::dequant(F::load(rp, s), v);
+#pragma unroll
+        for (int i = 0; i < F::E; i += 4) *(float4*)(x + (int64_t)s * F::E + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
     }
 }
 
+template <int T>
 __global__ __launch_bounds__(kBlock) void k_dequant_rows(const DevMat m, int64_t row0, int64_t nrows, float* out) {
-    const int E = fmt_step_elems(m.type);
-    const int64_t steps = m.K / E;
+    using F = Fmt<T>;
+    const int64_t steps = m.K / F::E;
     const int64_t total = nrows * steps;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
         const int64_t r = i / steps;
         const int s = (int)(i % steps);
-        float v[32];
-        dequant_step_rt(m, row0 + r, s, v);
-        for (int j = 0; j < E; ++j) out[r * m.K + (int64_t)s * E + j] = v[j];
+        float v[F::E];
+        F::dequant(F::load(F::row(m, row0 + r), s), v);
+#pragma unroll
+        for (int j = 0; j < F::E; ++j) out[r * m.K + (int64_t)s * F::E + j] = v[j];
     }
 }
 
@@ -184,14 +169,26 @@ int device_cu_count() {
     return cus;
 }
 
+#define TF_DISPATCH_TYPE(type, CALL)                                  \
+    switch (type) {                                                    \
+        case TF_HIP_TYPE_Q8_0: { constexpr int T_ = TF_HIP_TYPE_Q8_0; CALL; break; } \
+        case TF_HIP_TYPE_Q4_0: { constexpr int T_ = TF_HIP_TYPE_Q4_0; CALL; break; } \
+        case TF_HIP_TYPE_Q4_1: { constexpr int T_ = TF_HIP_TYPE_Q4_1; CALL; break; } \
+        case TF_HIP_TYPE_Q6_K: { constexpr int T_ = TF_HIP_TYPE_Q6_K; CALL; break; } \
+        case TF_HIP_TYPE_F16: { constexpr int T_ = TF_HIP_TYPE_F16; CALL; break; }   \
+        case TF_HIP_TYPE_F32: { constexpr int T_ = TF_HIP_TYPE_F32; CALL; break; }   \
+        default: return hipErrorInvalidValue;                          \
+    }
+
 hipError_t launch_embed(const DevMat& emb, float* x, Ctl* ctl, int32_t* hist, int D, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, st, emb, x, ctl, hist, D);
+    TF_DISPATCH_TYPE(emb.type, hipLaunchKernelGGL((k_embed<T_>), dim3(1), dim3(kBlock), 0, st, emb, x, ctl, hist, D));
     return hipGetLastError();
 }
 
 hipError_t launch_dequant_rows(const DevMat& m, int64_t row0, int64_t nrows, float* out, hipStream_t st) {
     const int64_t steps = m.K / fmt_step_elems(m.type);
-    hipLaunchKernelGGL(k_dequant_rows, dim3(grid_for(nrows * steps)), dim3(kBlock), 0, st, m, row0, nrows, out);
+    const int blocks = grid_for(nrows * steps);
+    TF_DISPATCH_TYPE(m.type, hipLaunchKernelGGL((k_dequant_rows<T_>), dim3(blocks), dim3(kBlock), 0, st, m, row0, nrows, out));
     return hipGetLastError();
 }
 

@@ -48,7 +48,6 @@ struct tf_hip_ctx {
     bool rope_set = false;
     float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr;
     float *logits = nullptr, *taps = nullptr, *part_o = nullptr, *part_ml = nullptr;
-    unsigned* counters = nullptr;
     Ctl* ctl = nullptr;
     Ctl* ctl_host = nullptr;      // pinned staging
     int32_t* hist = nullptr;      // device token per position
@@ -257,7 +256,8 @@ struct Launcher {
 };
 
 // One decode step (model.cpp:197-208) on the context stream.
-hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof) {
+// pos/att_start only size the profile's byte counts; the kernels read them from Ctl.
+hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof, int pos = 0, int att_start = 0) {
     const tf_hip_hparams& hp = c->hp;
     const int D = hp.n_embd, F = hp.n_ff;
     Launcher L{c, prof};
@@ -304,7 +304,6 @@ hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof) {
             a.rope_sin = c->rope_sin;
             a.part_o = c->part_o;
             a.part_ml = c->part_ml;
-            a.counter = c->counters + (size_t)l * hp.n_kv_head;
             a.out = c->att;
             a.ctl = c->ctl;
             a.H = hp.n_head;
@@ -317,7 +316,9 @@ hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof) {
             a.store_kv = 1;
             a.fixed_pos = -1;
             a.fixed_start = 0;
-            L.run(2, 0.0, [&] { return launch_attn_decode(a, c->st); });
+            // K and V rows of positions [att_start, pos] and the new row written
+            const double kv_bytes = (double)hp.n_kv_head * hp.head_dim * 4.0 * 2.0 * (pos - att_start + 2);
+            L.run(2, kv_bytes, [&] { return launch_attn_decode(a, c->st); });
         }
         {
             const DevMat& wo = M(TF_HIP_LAYER_O);
@@ -452,9 +453,7 @@ int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out) {
     c->vecs.assign((size_t)n_slots, nullptr);
     c->vec_len.assign((size_t)n_slots, 0);
 
-    // split count: enough workgroups per kv head to stream long caches, at most 64
-    int S = (p.max_seq + 63) / 64;
-    S = std::max(1, std::min(S, 64));
+    const int S = attn_splits(p.max_seq);
     c->S = S;
     c->kv_layer = (size_t)p.n_kv_head * p.max_seq * p.head_dim;
     const size_t D = (size_t)p.n_embd;
@@ -467,7 +466,7 @@ int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out) {
         (rc = dalloc(c, &c->taps, (size_t)(p.n_layer + 1) * D * 4)) ||
         (rc = dalloc(c, &c->part_o, (size_t)p.n_head * S * p.head_dim * 4)) ||
         (rc = dalloc(c, &c->part_ml, (size_t)p.n_head * S * 2 * 4)) ||
-        (rc = dalloc(c, &c->counters, (size_t)p.n_layer * p.n_kv_head * 4)) || (rc = dalloc(c, &c->ctl, sizeof(Ctl))) ||
+        (rc = dalloc(c, &c->ctl, sizeof(Ctl))) ||
         (rc = dalloc(c, &c->hist, (size_t)p.max_seq * 4)) ||
         (rc = dalloc(c, &c->rope_cos, (size_t)p.max_seq * (p.head_dim / 2) * 4)) ||
         (rc = dalloc(c, &c->rope_sin, (size_t)p.max_seq * (p.head_dim / 2) * 4)))
@@ -475,8 +474,7 @@ int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out) {
     if (hipHostMalloc((void**)&c->ctl_host, sizeof(Ctl), 0) != hipSuccess) return bail(TF_HIP_ENOMEM);
     if (hipHostMalloc((void**)&c->tok_host, (size_t)p.max_seq * 4, 0) != hipSuccess) return bail(TF_HIP_ENOMEM);
     std::memset(c->ctl_host, 0, sizeof(Ctl));
-    if (hipMemset(c->counters, 0, (size_t)p.n_layer * p.n_kv_head * 4) != hipSuccess ||
-        hipMemset(c->ctl, 0, sizeof(Ctl)) != hipSuccess || hipMemset(c->kc, 0, c->kv_layer * p.n_layer * 4) != hipSuccess ||
+    if (hipMemset(c->ctl, 0, sizeof(Ctl)) != hipSuccess || hipMemset(c->kc, 0, c->kv_layer * p.n_layer * 4) != hipSuccess ||
         hipMemset(c->vc, 0, c->kv_layer * p.n_layer * 4) != hipSuccess ||
         hipMemset(c->taps, 0, (size_t)(p.n_layer + 1) * D * 4) != hipSuccess)
         return bail(TF_HIP_EDEVICE);
@@ -726,7 +724,7 @@ int tf_hip_profile_generate(tf_hip_ctx* c, int32_t n, int32_t* out, float* ms_by
     if ((rc = set_ctl(c, 0, 1))) return rc;
     Prof prof;
     for (int i = 0; i < n; ++i) {
-        const hipError_t e = enqueue_step(c, &prof);
+        const hipError_t e = enqueue_step(c, &prof, pos0 + i, 0);
         if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("profile step: ") + hipGetErrorString(e));
     }
     HIPCHK(c, hipMemcpyAsync(c->tok_host, c->hist + pos0, (size_t)n * 4, hipMemcpyDeviceToHost, c->st));
@@ -881,9 +879,8 @@ int tf_hip_attn_decode(int device, const float* q, const float* k_rows, const fl
             std::memcpy(&hk[o], k_rows + ((size_t)p * n_kv + g) * hd, (size_t)hd * 4);
             std::memcpy(&hv[o], v_rows + ((size_t)p * n_kv + g) * hd, (size_t)hd * 4);
         }
-    int S = std::max(1, std::min(64, (max_seq + 63) / 64));
+    const int S = attn_splits(max_seq);
     float *dq, *dk, *dv, *dout, *pk, *pv, *po, *pml;
-    unsigned* cnt;
     OPCHK(s.alloc(&dq, (size_t)n_heads * hd * 4));
     OPCHK(s.alloc(&dk, cache * 4));
     OPCHK(s.alloc(&dv, cache * 4));
@@ -892,13 +889,11 @@ int tf_hip_attn_decode(int device, const float* q, const float* k_rows, const fl
     OPCHK(s.alloc(&pv, (size_t)n_kv * hd * 4));
     OPCHK(s.alloc(&po, (size_t)n_heads * S * hd * 4));
     OPCHK(s.alloc(&pml, (size_t)n_heads * S * 2 * 4));
-    OPCHK(s.alloc(&cnt, (size_t)n_kv * 4));
     OPCHK(hipMemcpy(dq, q, (size_t)n_heads * hd * 4, hipMemcpyHostToDevice));
     OPCHK(hipMemcpy(dk, hk.data(), cache * 4, hipMemcpyHostToDevice));
     OPCHK(hipMemcpy(dv, hv.data(), cache * 4, hipMemcpyHostToDevice));
     OPCHK(hipMemcpy(pk, k_rows + (size_t)(n_pos - 1) * n_kv * hd, (size_t)n_kv * hd * 4, hipMemcpyHostToDevice));
     OPCHK(hipMemcpy(pv, v_rows + (size_t)(n_pos - 1) * n_kv * hd, (size_t)n_kv * hd * 4, hipMemcpyHostToDevice));
-    OPCHK(hipMemset(cnt, 0, (size_t)n_kv * 4));
     AttnArgs a{};
     a.q = dq;
     a.knew = pk;
@@ -909,7 +904,6 @@ int tf_hip_attn_decode(int device, const float* q, const float* k_rows, const fl
     a.rope_sin = dq;
     a.part_o = po;
     a.part_ml = pml;
-    a.counter = cnt;
     a.out = dout;
     a.ctl = nullptr;
     a.H = n_heads;

@@ -96,13 +96,17 @@ struct AttnArgs {
     const float* rope_sin;
     float* part_o;          // [H][S][hd]
     float* part_ml;         // [H][S][2]
-    unsigned int* counter;  // [G]
     float* out;             // [H][hd]
     const Ctl* ctl;
     int H, G, hd, max_seq, layout, S, rope, store_kv;
     int fixed_pos;          // >= 0: use this position instead of ctl->pos (op-level entry)
     int fixed_start;
 };
+
+// Attention splits: positions per split at least kAttnMinChunk; one split (no merge
+// launch) when max_seq <= 512.
+constexpr int kAttnMinChunk = 64;
+int attn_splits(int max_seq);
 
 // Launchers (k_*.hip).
 hipError_t launch_gemv(const GemvArgs& a, int rows_per_wave, hipStream_t st);

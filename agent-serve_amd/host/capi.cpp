@@ -2,6 +2,7 @@
 // open a GGUF as a Model over the HIP backend, run it, and write synthetic GGUFs.
 // Every function returns 0 on success and a negative status on failure; the message
 // is tfh_last_error(handle) (or tfh_global_error() for calls without a model).
+#include <cstdio>
 #include <cstring>
 #include <exception>
 #include <stdexcept>
@@ -147,6 +148,22 @@ int tfh_synth_prompt(int64_t seed, int32_t n, int32_t n_vocab, int32_t* out) {
     return guard(nullptr, [&] {
         const auto ids = tfh::synth_prompt((uint64_t)seed, n, n_vocab);
         std::memcpy(out, ids.data(), ids.size() * sizeof(int32_t));
+    });
+}
+
+// The writer's block quantizers (one row of n elements of a ggml type).
+int tfh_quantize_row(int32_t ggml_type, const float* x, int64_t n, uint8_t* out) {
+    return guard(nullptr, [&] { tfh::quantize_row(ggml_type, x, n, out); });
+}
+
+// Summary of a GGUF file as the host reader sees it: out = n_tensors, weight_bytes, file_size.
+int tfh_gguf_summary(const char* path, uint64_t* out, char* arch, int32_t arch_len) {
+    return guard(nullptr, [&] {
+        tfh::GgufFile g(path);
+        out[0] = g.tensors().size();
+        out[1] = g.weight_bytes();
+        out[2] = g.file_size();
+        if (arch && arch_len > 0) std::snprintf(arch, (size_t)arch_len, "%s", g.arch().c_str());
     });
 }
 

@@ -1,0 +1,194 @@
+"""Decode throughput of tinferno's token loop on one MI355X.
+
+Workload: the Llama-3.2-1B-shape Q8_0 synthetic GGUF (16 layers, d_model 2048, 32/8 heads,
+head_dim 64, FFN 8192, vocab 128256, tied lm_head, seed 42), a 6-token prompt from the
+seed, greedy decode at batch 1, max-seq 512. A step is one decode token: embedding, 16
+layers, final norm, lm_head and the greedy argmax (Model::decode + sample_greedy).
+
+    python bench.py [--gpus 1] [--steps 32] [--warmup 8] [--no-cpu]
+
+Prints one JSON line. `value` is decode tok/s of K steps of the on-device greedy loop
+(tf_hip_generate: one captured graph per step, inputs resident in HBM), timed between
+two synchronisations. `roofline` is the dominant kernel's achieved algorithmic GB/s from
+HIP events around each launch of a second, kernel-by-kernel pass over the same steps;
+`cpu_baseline` is the reference --stage v2 path (compiled from its own sources) timed
+on this host's cores over the same prompt and steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import statistics
+import sys
+import tempfile
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import __graft_entry__  # noqa: E402
+
+PRESET = "llama1b_q8"
+PROMPT_TOKENS = 6
+MAX_SEQ = 512
+HBM_PEAK_GBS = 8000.0
+PUBLISHED_CPU_TOK_S = 10.74  # reference --stage v2, Llama-3.2-1B Q8_0, Ryzen 5 4600H
+
+
+def host_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def model_path() -> str:
+    d = pathlib.Path(tempfile.gettempdir()) / "tinferno_bench"
+    d.mkdir(parents=True, exist_ok=True)
+    return str(d / f"{PRESET}-seed42.gguf")
+
+
+def cpu_baseline(path, prompt, n_decode, want_ids):
+    """The reference --stage v2 Model (oracle/_ref) on this host: bench_e2e's once()
+    (reset, prefill, n x (sample_greedy + decode)), 1 warm-up + 3 runs, median tok/s."""
+    from oracle.bind import RefModel, ref_available
+
+    if not ref_available():
+        return None, None
+    threads = host_threads()
+    ref = RefModel(path, max_seq=MAX_SEQ, kv_layout=0, n_threads=threads)
+    ref.generate(prompt, min(4, n_decode))
+    runs = []
+    ids = None
+    for _ in range(3):
+        ids, _, dec_s = ref.generate(prompt, n_decode)
+        runs.append(n_decode / dec_s)
+    ref.close()
+    base = {
+        "value": round(statistics.median(runs), 3),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "reference",
+        "sample": f"reference --stage v2 (oracle/_ref, {threads} threads): {PROMPT_TOKENS}-token prompt + "
+                  f"{n_decode} greedy decode tokens of the same model, median of 3 runs after 1 warm-up",
+    }
+    match = bool(want_ids is not None and list(ids) == list(want_ids[: len(ids)]))
+    return base, match
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs the token loop on one GPU; --gpus {args.gpus} is not supported "
+              "(batch-1 decode of a 1.3 GB model fits one MI355X; multi-GPU sharding is design-only)",
+              file=sys.stderr)
+        return 2
+    K, W = args.steps, args.warmup
+    if K < 1 or PROMPT_TOKENS + max(K, W) > MAX_SEQ:
+        print(f"bench.py: --steps/--warmup must keep {PROMPT_TOKENS} + steps within max-seq {MAX_SEQ}",
+              file=sys.stderr)
+        return 2
+
+    pkg = __graft_entry__.load_package()
+    path = model_path()
+    info = pkg.synth_preset_info(PRESET)
+    if not os.path.exists(path):
+        t0 = time.time()
+        pkg.synth_write(PRESET, path, threads=host_threads())
+        print(f"bench.py: wrote {path} in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    prompt = pkg.synth_prompt(info["seed"], PROMPT_TOKENS, info["n_vocab"])
+
+    m = pkg.HipModel(path, max_seq=MAX_SEQ, kv_layout=0)
+    # warm-up: W untimed decode steps
+    m.prefill(prompt, want_logits=False)
+    if W > 0:
+        m.generate(W)
+    # timed: K greedy decode steps after an untimed prefill
+    m.reset()
+    t0 = time.perf_counter()
+    m.prefill(prompt, want_logits=False)
+    prefill_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    ids = m.generate(K)  # synchronous: returns after the device finished all K steps
+    wall_s = time.perf_counter() - t0
+    dev_ms, _, _, _ = m.last_timing()
+    ms_per_step = wall_s * 1e3 / K
+    value = K / wall_s
+    # algorithmic bytes of the K steps (weights once per step, one embedding row, the KV cache)
+    step_bytes = [m.decode_bytes(PROMPT_TOKENS + i) for i in range(K)]
+    step_gbs = sum(step_bytes) / wall_s / 1e9
+
+    # kernel-by-kernel pass over the same K steps: the dominant kernel's launches
+    m.reset()
+    m.prefill(prompt, want_logits=False)
+    ids_prof, prof = m.profile_generate(K)
+    dom = max(prof, key=lambda k: prof[k][0])
+    d_ms, d_launch, d_bytes = prof[dom]
+    achieved = (d_bytes / d_launch) / (d_ms / d_launch * 1e-3) / 1e9
+    m.close()
+    read_best, read_med = pkg.read_stream(4 << 30, iters=10)
+
+    cpu, match = (None, None) if args.no_cpu else cpu_baseline(path, prompt, K, ids)
+
+    out = {
+        "metric": "decode tok/s & % of HBM roofline, Llama-3.2-1B-shape Q8_0, batch 1",
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / PUBLISHED_CPU_TOK_S, 1),
+        "vs_baseline_ref": f"{PUBLISHED_CPU_TOK_S} tok/s: reference --stage v2, Llama-3.2-1B Q8_0, "
+                           "Ryzen 5 4600H 6c/12t (published)",
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "Llama-3.2-1B-shape Q8_0 synthetic GGUF (L16 D2048 H32/8 hd64 F8192 V128256, tied "
+                        "lm_head, N(0,0.02) seed 42), 6-token prompt, greedy decode, max-seq 512, batch 1",
+            "prompt_tokens": PROMPT_TOKENS,
+            "decode_tokens": K,
+            "max_seq": MAX_SEQ,
+            "weights": "Q8_0",
+            "kv_cache": "fp32 seq-major",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": dom,
+            "launches": d_launch,
+            "bytes_per_launch": round(d_bytes / d_launch),
+            "avg_launch_us": round(d_ms / d_launch * 1e3, 3),
+        },
+        "step_hbm_gb_s": round(step_gbs, 1),
+        "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        "read_stream_gb_s": round(read_best, 1),
+        "step_frac_of_read_stream": round(step_gbs / read_best, 4),
+        "bytes_per_step": round(statistics.mean(step_bytes)),
+        "device_ms_per_step": round(dev_ms / K, 4),
+        "prefill_tok_s": round(PROMPT_TOKENS / prefill_s, 1),
+        "kernel_ms_by_class": {k: round(v[0] / K, 4) for k, v in prof.items()},
+        "tokens_match_profile_pass": bool(list(ids) == list(ids_prof)),
+        "tokens_match_reference": match,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
