@@ -21,11 +21,26 @@ __device__ __forceinline__ float ub1(uint32_t w) { return (float)((w >> 8) & 0xF
 __device__ __forceinline__ float ub2(uint32_t w) { return (float)((w >> 16) & 0xFFu); }
 __device__ __forceinline__ float ub3(uint32_t w) { return (float)(w >> 24); }
 
-// Butterfly sums: partners add the same two values, so every lane ends with the
-// bit-identical total and the result does not depend on scheduling.
+// DPP lane permutes within a row of 16 lanes (no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within 16
+
+// Wavefront sum. Each step adds a value and its partner's, and both partners add the
+// same two values, so every lane ends with the bit-identical total, independent of
+// scheduling: DPP within rows of 16 lanes, then two cross-row exchanges.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
     return v;
 }
 

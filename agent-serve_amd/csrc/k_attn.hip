@@ -19,7 +19,14 @@ namespace {
 
 constexpr int kMaxRep = 8;     // query heads per kv head supported (GQA ratio)
 constexpr int kAttnTile = 32;  // positions per K/V tile in LDS
-constexpr int kMaxPairs = kMaxRep * 256 / kBlock;  // (head, dim) pairs per thread, head_dim <= 256
+
+// Per-thread register counts for head_dim <= HDM (64, 128 or 256).
+template <int HDM>
+struct AttnShape {
+    static constexpr int kPairs = kMaxRep * HDM / kBlock;             // (head, dim) pairs of P.V
+    static constexpr int kQPairs = kMaxRep * HDM / 2 / kBlock;        // rotation pairs
+    static constexpr int kTileVec = kAttnTile * HDM / 4 / kBlock;     // float4 of a K (or V) tile
+};
 
 __device__ __forceinline__ int64_t kv_index(int layout, int G, int max_seq, int hd, int g, int p) {
     return layout == TF_HIP_KV_HEAD_MAJOR ? ((int64_t)g * max_seq + p) * hd : ((int64_t)p * G + g) * hd;
@@ -41,7 +48,11 @@ __device__ __forceinline__ Split split_of(const AttnArgs& a) {
     return sp;
 }
 
+template <int HDM>
 __global__ __launch_bounds__(kBlock) void k_attn_decode(const AttnArgs a) {
+    constexpr int kMaxPairs = AttnShape<HDM>::kPairs;
+    constexpr int kQPairs = AttnShape<HDM>::kQPairs;
+    constexpr int kTileVec = AttnShape<HDM>::kTileVec;
     const int g = blockIdx.x / a.S;
     const int s = blockIdx.x % a.S;
     const int hd = a.hd, d2 = hd / 2, hd4 = hd / 4;
@@ -63,32 +74,64 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const AttnArgs a) {
     float* pr = vt + kAttnTile * hd;       // [n_rep][kAttnTile] scores, then weights
     float* st = pr + n_rep * kAttnTile;    // [n_rep][3] running max, running sum, rescale
 
+    // K/V rows of a tile, kTileVec float4 of each per thread, loaded into registers;
+    // indices past the tile re-load its last element (never stored) so the loads
+    // stay unconditional
+    auto load_tile = [&](int t0, float4 (&kr)[kTileVec], float4 (&vr)[kTileVec]) {
+        const int tn = min(kAttnTile, p1 - t0);
+#pragma unroll
+        for (int k = 0; k < kTileVec; ++k) {
+            int i = tid + k * kBlock;
+            i = i < tn * hd4 ? i : tn * hd4 - 1;
+            const int j = i / hd4, c = i % hd4;
+            const int64_t o = kv_index(a.layout, a.G, a.max_seq, hd, g, t0 + j) + 4 * c;
+            kr[k] = *(const float4*)(a.kc + o);
+            vr[k] = *(const float4*)(a.vc + o);
+        }
+    };
+    // one memory round for everything the first tile needs
+    const int nq = n_rep * d2;
+    float qa[kQPairs], qb[kQPairs], ca[kQPairs], sa[kQPairs];
     const float* cs = a.rope_cos + (int64_t)pos * d2;
     const float* sn = a.rope_sin + (int64_t)pos * d2;
-    for (int i = tid; i < n_rep * d2; i += kBlock) {
+#pragma unroll
+    for (int k = 0; k < kQPairs; ++k) {
+        int i = tid + k * kBlock;
+        i = i < nq ? i : nq - 1;
         const int r = i / d2, j = i % d2;
         const float* qh = a.q + (int64_t)(g * n_rep + r) * hd;
-        const float x0 = qh[j], x1 = qh[j + d2];
-        if (a.rope) {
-            qs[r * hd + j] = fmaf(x0, cs[j], -(x1 * sn[j]));
-            qs[r * hd + j + d2] = fmaf(x0, sn[j], x1 * cs[j]);
-        } else {
-            qs[r * hd + j] = x0;
-            qs[r * hd + j + d2] = x1;
+        qa[k] = qh[j];
+        qb[k] = qh[j + d2];
+        ca[k] = cs[j];
+        sa[k] = sn[j];
+    }
+    const int jk = tid < d2 ? tid : d2 - 1;
+    const float* kh = a.knew + (int64_t)g * hd;
+    const float k0 = kh[jk], k1 = kh[jk + d2], kc0 = cs[jk], ks0 = sn[jk];
+    const int jv = tid < hd ? tid : hd - 1;
+    const float v0 = a.vnew[(int64_t)g * hd + jv];
+    float4 kr_a[kTileVec], vr_a[kTileVec], kr_b[kTileVec], vr_b[kTileVec];
+    load_tile(p0, kr_a, vr_a);
+
+#pragma unroll
+    for (int k = 0; k < kQPairs; ++k) {
+        const int i = tid + k * kBlock;
+        if (i < nq) {
+            const int r = i / d2, j = i % d2;
+            if (a.rope) {
+                qs[r * hd + j] = fmaf(qa[k], ca[k], -(qb[k] * sa[k]));
+                qs[r * hd + j + d2] = fmaf(qa[k], sa[k], qb[k] * ca[k]);
+            } else {
+                qs[r * hd + j] = qa[k];
+                qs[r * hd + j + d2] = qb[k];
+            }
         }
     }
-    for (int j = tid; j < d2; j += kBlock) {
-        const float* kh = a.knew + (int64_t)g * hd;
-        const float x0 = kh[j], x1 = kh[j + d2];
-        if (a.rope) {
-            kn[j] = fmaf(x0, cs[j], -(x1 * sn[j]));
-            kn[j + d2] = fmaf(x0, sn[j], x1 * cs[j]);
-        } else {
-            kn[j] = x0;
-            kn[j + d2] = x1;
-        }
+    if (tid < d2) {
+        kn[tid] = a.rope ? fmaf(k0, kc0, -(k1 * ks0)) : k0;
+        kn[tid + d2] = a.rope ? fmaf(k0, ks0, k1 * kc0) : k1;
     }
-    for (int j = tid; j < hd; j += kBlock) vn[j] = a.vnew[(int64_t)g * hd + j];
+    if (tid < hd) vn[tid] = v0;
     if (tid < n_rep) {
         st[3 * tid] = -INFINITY;
         st[3 * tid + 1] = 0.0f;
@@ -107,42 +150,38 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const AttnArgs a) {
 #pragma unroll
     for (int k = 0; k < kMaxPairs; ++k) o_acc[k] = 0.0f;
 
-    for (int t0 = p0; t0 < p1; t0 += kAttnTile) {
+    auto tile = [&](int t0, float4 (&kr)[kTileVec], float4 (&vr)[kTileVec], float4 (&kn_r)[kTileVec],
+                    float4 (&vn_r)[kTileVec]) {
         const int tn = min(kAttnTile, p1 - t0);
-        // K and V rows of the tile, one memory round for the whole tile
-        for (int i = tid; i < tn * hd4; i += kBlock) {
-            const int j = i / hd4, c = i % hd4;
-            const int p = t0 + j;
-            float4 kv, vv;
-            if (p == pos) {
-                kv = *(const float4*)(kn + 4 * c);
-                vv = *(const float4*)(vn + 4 * c);
-            } else {
-                const int64_t o = kv_index(a.layout, a.G, a.max_seq, hd, g, p) + 4 * c;
-                kv = *(const float4*)(a.kc + o);
-                vv = *(const float4*)(a.vc + o);
+        if (t0 + kAttnTile < p1) load_tile(t0 + kAttnTile, kn_r, vn_r);  // next tile in flight
+#pragma unroll
+        for (int k = 0; k < kTileVec; ++k) {
+            const int i = tid + k * kBlock;
+            if (i < tn * hd4) {
+                const int j = i / hd4, c = i % hd4;
+                const bool is_new = t0 + j == pos;  // not in the cache yet: the rotated k and v
+                *(float4*)(kt + j * ks + 4 * c) = is_new ? *(const float4*)(kn + 4 * c) : kr[k];
+                *(float4*)(vt + j * hd + 4 * c) = is_new ? *(const float4*)(vn + 4 * c) : vr[k];
             }
-            *(float4*)(kt + j * ks + 4 * c) = kv;
-            *(float4*)(vt + j * hd + 4 * c) = vv;
         }
         __syncthreads();
         // scores in the order of dot_f32 (8 lanes over i = 0, 8, ..., then hsum8; quant.cpp:198-214)
         for (int i = tid; i < n_rep * tn; i += kBlock) {
             const int r = i / tn, j = i % tn;
             const float* qr = qs + r * hd;
-            const float* kr = kt + j * ks;
+            const float* krow = kt + j * ks;
             float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             for (int e = 0; e < hd; e += 8) {
-                const float4 qa = *(const float4*)(qr + e), qb = *(const float4*)(qr + e + 4);
-                const float4 ka = *(const float4*)(kr + e), kb = *(const float4*)(kr + e + 4);
-                c[0] = fmaf(qa.x, ka.x, c[0]);
-                c[1] = fmaf(qa.y, ka.y, c[1]);
-                c[2] = fmaf(qa.z, ka.z, c[2]);
-                c[3] = fmaf(qa.w, ka.w, c[3]);
-                c[4] = fmaf(qb.x, kb.x, c[4]);
-                c[5] = fmaf(qb.y, kb.y, c[5]);
-                c[6] = fmaf(qb.z, kb.z, c[6]);
-                c[7] = fmaf(qb.w, kb.w, c[7]);
+                const float4 q0 = *(const float4*)(qr + e), q1 = *(const float4*)(qr + e + 4);
+                const float4 x0 = *(const float4*)(krow + e), x1 = *(const float4*)(krow + e + 4);
+                c[0] = fmaf(q0.x, x0.x, c[0]);
+                c[1] = fmaf(q0.y, x0.y, c[1]);
+                c[2] = fmaf(q0.z, x0.z, c[2]);
+                c[3] = fmaf(q0.w, x0.w, c[3]);
+                c[4] = fmaf(q1.x, x1.x, c[4]);
+                c[5] = fmaf(q1.y, x1.y, c[5]);
+                c[6] = fmaf(q1.z, x1.z, c[6]);
+                c[7] = fmaf(q1.w, x1.w, c[7]);
             }
             pr[r * kAttnTile + j] = scale * (((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7])));
         }
@@ -176,6 +215,13 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const AttnArgs a) {
             }
         }
         __syncthreads();
+    };
+    for (int t0 = p0; t0 < p1;) {
+        tile(t0, kr_a, vr_a, kr_b, vr_b);
+        t0 += kAttnTile;
+        if (t0 >= p1) break;
+        tile(t0, kr_b, vr_b, kr_a, vr_a);
+        t0 += kAttnTile;
     }
 #pragma unroll
     for (int k = 0; k < kMaxPairs; ++k) {
@@ -227,7 +273,12 @@ hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
     const int n_rep = a.H / a.G;
     const size_t lds = sizeof(float) * ((size_t)n_rep * a.hd + 2 * (size_t)a.hd + (size_t)kAttnTile * (a.hd + 4) +
                                         (size_t)kAttnTile * a.hd + (size_t)n_rep * kAttnTile + 3 * (size_t)n_rep);
-    hipLaunchKernelGGL(k_attn_decode, dim3(a.G * a.S), dim3(kBlock), lds, st, a);
+    if (a.hd <= 64)
+        hipLaunchKernelGGL(k_attn_decode<64>, dim3(a.G * a.S), dim3(kBlock), lds, st, a);
+    else if (a.hd <= 128)
+        hipLaunchKernelGGL(k_attn_decode<128>, dim3(a.G * a.S), dim3(kBlock), lds, st, a);
+    else
+        hipLaunchKernelGGL(k_attn_decode<256>, dim3(a.G * a.S), dim3(kBlock), lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.S == 1) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3((a.H * a.hd + kBlock - 1) / kBlock), dim3(kBlock), 0, st, a);

@@ -18,7 +18,12 @@ size_t gemv_lds_bytes(int64_t K) { return (size_t)K * 4 + (size_t)(K / 16) * 4; 
 
 hipError_t launch_gemv(const GemvArgs& a, int R, hipStream_t st) {
     if (a.total_groups <= 0) return hipSuccess;
-    const int cap = 4 * device_cu_count();
+    // Workgroups per CU by matrix height (swept on MI355X for the decode shapes):
+    // one for N <= 4096 rows, two up to 16384, four above (the lm_head).
+    int64_t rows = 0;
+    for (int i = 0; i < a.n_seg; ++i) rows += a.seg[i].a.N * (a.mode == GEMV_SILU ? 2 : 1);
+    const int per_cu = rows <= 4096 ? 1 : rows <= 16384 ? 2 : 4;
+    const int cap = per_cu * device_cu_count();
     const int64_t want = (a.total_groups + kWavesPerBlock - 1) / kWavesPerBlock;
     const int blocks = (int)(want < cap ? want : cap);
     const size_t lds = gemv_lds_bytes(a.K);

@@ -14,30 +14,59 @@
 namespace tfk {
 namespace gemv_detail {
 
+constexpr int kStageVec = 9;  // float4 of x per thread: K <= 9 * 4 * kBlock = 9216
+
+// x (optionally RMSNorm-ed) and its 16-element partial sums into LDS. Every load of x
+// and of the norm weight is issued before the first one is used.
 __device__ void stage_x(const GemvArgs& a, float* xs, float* x16, bool need_sums) {
-    const int K = (int)a.K;
+    const int K4 = (int)(a.K / 4);
     const int tid = threadIdx.x;
+    const float4* x4 = (const float4*)a.x;
+    // indices past the end re-load the last element (never stored): unconditional loads
+    float4 xv[kStageVec];
+#pragma unroll
+    for (int i = 0; i < kStageVec; ++i) {
+        const int j = tid + i * kBlock;
+        xv[i] = x4[j < K4 ? j : K4 - 1];
+    }
     if (a.norm_w) {
+        const float4* w4 = (const float4*)a.norm_w;
+        float4 wv[kStageVec];
+#pragma unroll
+        for (int i = 0; i < kStageVec; ++i) {
+            const int j = tid + i * kBlock;
+            wv[i] = w4[j < K4 ? j : K4 - 1];
+        }
         __shared__ double red[kWavesPerBlock];
-        double ss = 0;
-        for (int k = tid; k < K; k += kBlock) {
-            const double v = (double)a.x[k];
-            ss += v * v;  // exact in fp64, as the reference's accumulation terms
+        double ss = 0;  // every x*x is exact in fp64, as in the reference's accumulation
+#pragma unroll
+        for (int i = 0; i < kStageVec; ++i) {
+            const float4 v = xv[i];
+            const double t = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+            ss += tid + i * kBlock < K4 ? t : 0.0;
         }
         ss = wave_sum_d(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
         ss = (red[0] + red[1]) + (red[2] + red[3]);
-        const float inv = 1.0f / sqrtf((float)(ss / K) + a.eps);
-        for (int k = tid; k < K; k += kBlock) xs[k] = a.x[k] * inv * a.norm_w[k];
-    } else {
-        for (int k = tid; k < K; k += kBlock) xs[k] = a.x[k];
+        const float inv = 1.0f / sqrtf((float)(ss / a.K) + a.eps);
+#pragma unroll
+        for (int i = 0; i < kStageVec; ++i) {
+            const float4 v = xv[i], w = wv[i];
+            xv[i] = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kStageVec; ++i) {
+        const int j = tid + i * kBlock;
+        if (j < K4) {
+            ((float4*)xs)[j] = xv[i];
+            if (a.norm_out && blockIdx.x == 0) ((float4*)a.norm_out)[j] = xv[i];
+        }
     }
     __syncthreads();
-    if (a.norm_out && blockIdx.x == 0)
-        for (int k = tid; k < K; k += kBlock) a.norm_out[k] = xs[k];
     if (need_sums) {
-        for (int c = tid; c < K / 16; c += kBlock) {
+        for (int c = tid; c < (int)(a.K / 16); c += kBlock) {
             const float4* p = (const float4*)(xs + 16 * c);
             const float4 u = p[0], v = p[1], w = p[2], z = p[3];
             x16[c] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w)) + ((w.x + w.y) + (w.z + w.w)) +
@@ -99,11 +128,12 @@ __global__ __launch_bounds__(kBlock) void k_gemv(const GemvArgs a) {
             if (SILU) pb = F::row(sg.b, row);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int s = ti * kWave * U + u * kWave + lane;
-                if (s < S) {
-                    w[u][r] = F::load(pa, s);
-                    if (SILU) w[u][R + r] = F::load(pb, s);
-                }
+                // steps past the row end re-load its last step (masked out in step()): the
+                // loads stay unconditional, so their wait counts stay exact
+                int s = ti * kWave * U + u * kWave + lane;
+                s = s < S ? s : S - 1;
+                w[u][r] = F::load(pa, s);
+                if (SILU) w[u][R + r] = F::load(pb, s);
             }
         }
     };
@@ -160,9 +190,12 @@ __global__ __launch_bounds__(kBlock) void k_gemv(const GemvArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int s = ti * kWave * U + u * kWave + lane;
-            if (s < S) {
+            const bool in_row = s < S;
+            const int sc = in_row ? s : S - 1;
 #pragma unroll
-                for (int r = 0; r < NR; ++r) acc[r] += F::dot(cur[u][r], xs, x16, s);
+            for (int r = 0; r < NR; ++r) {
+                const float d = F::dot(cur[u][r], xs, x16, sc);
+                acc[r] += in_row ? d : 0.0f;
             }
         }
         if (ti == TPG - 1) epilogue(g);
@@ -208,21 +241,16 @@ hipError_t launch_t(const GemvArgs& a, int blocks, size_t lds, hipStream_t st) {
 template <int T>
 hipError_t launch_r(const GemvArgs& a, int R, int blocks, size_t lds, hipStream_t st) {
     const int S = (int)(a.K / Fmt<T>::E);
-    const int NR = a.mode == GEMV_SILU ? 2 * R : R;
+    // steps in flight per row and tile: the whole row where it fits 4 x 16 B per lane
     int U = (S + kWave - 1) / kWave;
-    const int cap = NR >= 4 ? 2 : NR >= 2 ? 4 : 8;
-    U = U > cap ? cap : U;
-    U = U >= 8 ? 8 : U >= 4 ? 4 : U >= 2 ? 2 : 1;
+    U = U >= 4 ? 4 : U >= 2 ? 2 : 1;
     switch (R * 16 + U) {
         case 1 * 16 + 1: return launch_t<T, 1, 1>(a, blocks, lds, st);
         case 1 * 16 + 2: return launch_t<T, 1, 2>(a, blocks, lds, st);
         case 1 * 16 + 4: return launch_t<T, 1, 4>(a, blocks, lds, st);
-        case 1 * 16 + 8: return launch_t<T, 1, 8>(a, blocks, lds, st);
         case 2 * 16 + 1: return launch_t<T, 2, 1>(a, blocks, lds, st);
         case 2 * 16 + 2: return launch_t<T, 2, 2>(a, blocks, lds, st);
         case 2 * 16 + 4: return launch_t<T, 2, 4>(a, blocks, lds, st);
-        case 4 * 16 + 1: return launch_t<T, 4, 1>(a, blocks, lds, st);
-        case 4 * 16 + 2: return launch_t<T, 4, 2>(a, blocks, lds, st);
     }
     return hipErrorInvalidValue;
 }

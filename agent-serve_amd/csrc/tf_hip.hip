@@ -168,13 +168,9 @@ hipError_t make_devmat(int t, int64_t K, int64_t N, const uint8_t* d_raw, DevMat
     return launch_repack(t, d_raw, K, N, m, st);
 }
 
-// Rows per wavefront: as many as keep at least two workgroups per CU busy.
-int pick_rows(int64_t n_rows) {
-    const int64_t want = 2LL * device_cu_count() * kWavesPerBlock;
-    if (n_rows >= 4 * want) return 4;
-    if (n_rows >= 2 * want) return 2;
-    return 1;
-}
+// Rows per wavefront: two (swept on MI355X for the decode shapes); one for matrices
+// too short to give every CU a group.
+int pick_rows(int64_t n_rows) { return n_rows >= 2LL * kWavesPerBlock * device_cu_count() ? 2 : 1; }
 
 void add_seg(GemvArgs& a, const DevMat& m, float* y, const float* bias, float* tap, int R) {
     GemvSeg& s = a.seg[a.n_seg++];
@@ -335,7 +331,7 @@ hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof, int pos = 0, int att_start = 
             const DevMat& wg = M(TF_HIP_LAYER_GATE);
             const DevMat& wu = M(TF_HIP_LAYER_UP);
             if (wg.type == wu.type) {
-                const int R = pick_rows(2 * wg.N) > 1 ? 2 : 1;
+                const int R = pick_rows(wg.N);
                 GemvArgs a;
                 a.type = wg.type;
                 a.K = D;
