@@ -68,6 +68,7 @@ def hip_lib() -> C.CDLL:
                                          C.c_int32, C.c_int32, _f32p]),
         "tf_hip_argmax": (C.c_int, [C.c_int, _f32p, C.c_int32, _i32p]),
         "tf_hip_read_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p]),
+        "tf_hip_copy_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -327,4 +328,11 @@ def argmax(x: np.ndarray, device: int = 0) -> int:
 def read_stream(nbytes: int, iters: int = 10, device: int = 0):
     best, med = C.c_double(0), C.c_double(0)
     _op(hip_lib().tf_hip_read_stream(device, nbytes, iters, C.byref(best), C.byref(med)), "tf_hip_read_stream")
+    return float(best.value), float(med.value)
+
+
+def copy_stream(nbytes: int, iters: int = 10, device: int = 0):
+    """Device-to-device copy of nbytes; GB/s counts bytes read plus bytes written."""
+    best, med = C.c_double(0), C.c_double(0)
+    _op(hip_lib().tf_hip_copy_stream(device, nbytes, iters, C.byref(best), C.byref(med)), "tf_hip_copy_stream")
     return float(best.value), float(med.value)

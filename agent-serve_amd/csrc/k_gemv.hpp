@@ -17,17 +17,21 @@ namespace gemv_detail {
 constexpr int kStageVec = 9;  // float4 of x per thread: K <= 9 * 4 * kBlock = 9216
 
 // x (optionally RMSNorm-ed) and its 16-element partial sums into LDS. Every load of x
-// and of the norm weight is issued before the first one is used.
+// and of the norm weight is issued before the first one is used, and the prologue ends
+// with every load complete, the first weight tile's included (issued earlier, it has
+// landed by the time x has): the main loop then starts with no stale pending loads in
+// the compiler's wait bookkeeping.
 __device__ void stage_x(const GemvArgs& a, float* xs, float* x16, bool need_sums) {
     const int K4 = (int)(a.K / 4);
+    const int nv = (K4 + kBlock - 1) / kBlock;  // float4 of x per thread actually needed
     const int tid = threadIdx.x;
     const float4* x4 = (const float4*)a.x;
-    // indices past the end re-load the last element (never stored): unconditional loads
+    // indices past the end re-load the last element (never stored)
     float4 xv[kStageVec];
 #pragma unroll
     for (int i = 0; i < kStageVec; ++i) {
         const int j = tid + i * kBlock;
-        xv[i] = x4[j < K4 ? j : K4 - 1];
+        if (i < nv) xv[i] = x4[j < K4 ? j : K4 - 1];
     }
     if (a.norm_w) {
         const float4* w4 = (const float4*)a.norm_w;
@@ -35,15 +39,17 @@ __device__ void stage_x(const GemvArgs& a, float* xs, float* x16, bool need_sums
 #pragma unroll
         for (int i = 0; i < kStageVec; ++i) {
             const int j = tid + i * kBlock;
-            wv[i] = w4[j < K4 ? j : K4 - 1];
+            if (i < nv) wv[i] = w4[j < K4 ? j : K4 - 1];
         }
         __shared__ double red[kWavesPerBlock];
         double ss = 0;  // every x*x is exact in fp64, as in the reference's accumulation
 #pragma unroll
         for (int i = 0; i < kStageVec; ++i) {
-            const float4 v = xv[i];
-            const double t = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-            ss += tid + i * kBlock < K4 ? t : 0.0;
+            if (i < nv) {
+                const float4 v = xv[i];
+                const double t = (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+                ss += tid + i * kBlock < K4 ? t : 0.0;
+            }
         }
         ss = wave_sum_d(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -52,14 +58,16 @@ __device__ void stage_x(const GemvArgs& a, float* xs, float* x16, bool need_sums
         const float inv = 1.0f / sqrtf((float)(ss / a.K) + a.eps);
 #pragma unroll
         for (int i = 0; i < kStageVec; ++i) {
-            const float4 v = xv[i], w = wv[i];
-            xv[i] = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+            if (i < nv) {
+                const float4 v = xv[i], w = wv[i];
+                xv[i] = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+            }
         }
     }
 #pragma unroll
     for (int i = 0; i < kStageVec; ++i) {
         const int j = tid + i * kBlock;
-        if (j < K4) {
+        if (i < nv && j < K4) {
             ((float4*)xs)[j] = xv[i];
             if (a.norm_out && blockIdx.x == 0) ((float4*)a.norm_out)[j] = xv[i];
         }
@@ -74,14 +82,7 @@ __device__ void stage_x(const GemvArgs& a, float* xs, float* x16, bool need_sums
         }
         __syncthreads();
     }
-}
-
-template <int NR>
-__device__ __forceinline__ float pick(const float (&v)[NR], int i) {
-    float r = v[0];
-#pragma unroll
-    for (int j = 1; j < NR; ++j) r = (i == j) ? v[j] : r;
-    return r;
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt = expcnt = lgkmcnt = 0
 }
 
 // R rows per group; SILU pairs R gate rows with the same R up rows (NR = 2R streams).
@@ -100,29 +101,42 @@ __global__ __launch_bounds__(kBlock) void k_gemv(const GemvArgs a) {
     float* x16 = smem + a.K;
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // groups are wave-uniform
     const int S = (int)(a.K / F::E);
     const int TPG = (S + kWave * U - 1) / (kWave * U);
-    const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
 
-    auto locate = [&](int64_t g, int& si, int64_t& row0) {
-        si = 0;
-        int64_t gg = g;
-        while (si + 1 < a.n_seg && gg >= a.seg[si].groups) {
-            gg -= a.seg[si].groups;
-            ++si;
+    // the segment holding group g, chosen with compile-time indices: a runtime index into
+    // the kernel arguments would become a vector load whose wait drains the weight loads
+    // in flight
+    auto locate = [&](int g, int& row0) -> const GemvSeg& {
+        if (a.n_seg > 1 && g >= (int)a.seg[0].groups) {
+            g -= (int)a.seg[0].groups;
+            if (a.n_seg > 2 && g >= (int)a.seg[1].groups) {
+                row0 = (g - (int)a.seg[1].groups) * R;
+                return a.seg[2];
+            }
+            row0 = g * R;
+            return a.seg[1];
         }
-        row0 = gg * R;
+        row0 = g * R;
+        return a.seg[0];
     };
-    auto load_tile = [&](int64_t g, int ti, Raw (&w)[U][NR]) {
-        int si;
-        int64_t row0;
-        locate(g, si, row0);
-        const GemvSeg& sg = a.seg[si];
-        const int64_t N = sg.a.N;
+    // a tile's weight loads, plus what the group's epilogue reads (the residual row for
+    // RESID, the bias row for STORE; a harmless word of x where there is none), issued
+    // with the tile so that its wait is the tile's
+    auto load_tile = [&](int g, int ti, Raw (&w)[U][NR], float& extra) {
+        int row0;
+        const GemvSeg& sg = locate(g, row0);
+        const int N = (int)sg.a.N;
+        if (MODE == GEMV_RESID || MODE == GEMV_STORE) {
+            int re = row0 + (lane < R ? lane : R - 1);
+            re = re < N ? re : N - 1;
+            const float* ep = MODE == GEMV_RESID ? sg.y : sg.bias;
+            extra = ep ? ep[re] : a.x[0];
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int64_t row = row0 + r < N ? row0 + r : N - 1;  // tail rows re-read a valid row
+            const int row = row0 + r < N ? row0 + r : N - 1;  // tail rows re-read a valid row
             const RowPtr pa = F::row(sg.a, row);
             RowPtr pb = pa;
             if (SILU) pb = F::row(sg.b, row);
@@ -138,10 +152,16 @@ __global__ __launch_bounds__(kBlock) void k_gemv(const GemvArgs a) {
         }
     };
 
-    int64_t g = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+    // groups g, g + stride, ... of this wave, TPG tiles each: the tile count is known up
+    // front, so the loop below has a single back edge and no exit path with loads pending
+    const int total = (int)a.total_groups;
+    const int stride = gridDim.x * kWavesPerBlock;
+    int g = blockIdx.x * kWavesPerBlock + wave;
+    const int n_tiles = g < total ? ((total - 1 - g) / stride + 1) * TPG : 0;
     int ti = 0;
     Raw wa[U][NR], wb[U][NR];
-    if (g < a.total_groups) load_tile(g, 0, wa);
+    float ea = 0.0f, eb = 0.0f;
+    if (n_tiles > 0) load_tile(g, 0, wa, ea);
     stage_x(a, xs, x16, F::kNeedSums);
 
     float acc[NR];
@@ -149,44 +169,48 @@ __global__ __launch_bounds__(kBlock) void k_gemv(const GemvArgs a) {
     for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
     unsigned long long best = 0;
 
-    auto epilogue = [&](int64_t gq) {
+    // lane r writes row r of the group (every lane holds every row's total)
+    auto epilogue = [&](int gq, float extra) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) acc[r] = wave_sum(acc[r]);
-        int si;
-        int64_t row0;
-        locate(gq, si, row0);
-        const GemvSeg& sg = a.seg[si];
-        const int64_t row = row0 + lane;
-        if (lane < R && row < sg.a.N) {
-            const float v = pick<NR>(acc, lane);
-            if (SILU) {
-                const float up = pick<NR>(acc, lane + R);
-                sg.y[row] = (v / (1.0f + expf(-v))) * up;
-            } else if (MODE == GEMV_STORE) {
-                sg.y[row] = sg.bias ? v + sg.bias[row] : v;
-            } else if (MODE == GEMV_RESID) {
-                const float nv = sg.y[row] + v;
-                sg.y[row] = nv;
-                if (sg.tap) sg.tap[row] = nv;
-            } else {  // GEMV_LOGITS
-                if (sg.y) sg.y[row] = v;
-                const unsigned long long k = argmax_key(v, row);
-                best = k > best ? k : best;
+        int row0;
+        const GemvSeg& sg = locate(gq, row0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = row0 + r;
+            if (lane == r && row < (int)sg.a.N) {
+                const float v = acc[r];
+                if (SILU) {
+                    sg.y[row] = (v / (1.0f + expf(-v))) * acc[R + r];
+                } else if (MODE == GEMV_STORE) {
+                    sg.y[row] = sg.bias ? v + extra : v;
+                } else if (MODE == GEMV_RESID) {
+                    const float nv = extra + v;
+                    sg.y[row] = nv;
+                    if (sg.tap) sg.tap[row] = nv;
+                } else {  // GEMV_LOGITS
+                    if (sg.y) sg.y[row] = v;
+                    const unsigned long long k = argmax_key(v, row);
+                    best = k > best ? k : best;
+                }
             }
         }
 #pragma unroll
         for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
     };
-    // consume `cur` (tile ti of group g) while `nxt` receives the following tile
-    auto step = [&](Raw (&cur)[U][NR], Raw (&nxt)[U][NR]) -> bool {
-        int64_t gn = g;
+    // consume `cur` (tile ti of group g) while `nxt` receives the following tile; past
+    // the wave's last tile the load re-reads the current one (an L2 hit) so that it
+    // stays unconditional: a load under a branch makes the compiler's wait before the
+    // next use a full drain
+    auto step = [&](Raw (&cur)[U][NR], float& ecur, Raw (&nxt)[U][NR], float& enxt) {
+        int gn = g;
         int tn = ti + 1;
         if (tn == TPG) {
             tn = 0;
             gn = g + stride;
         }
-        const bool more = gn < a.total_groups;
-        if (more) load_tile(gn, tn, nxt);
+        const bool more = gn < total;
+        load_tile(more ? gn : g, more ? tn : ti, nxt, enxt);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int s = ti * kWave * U + u * kWave + lane;
@@ -198,17 +222,16 @@ __global__ __launch_bounds__(kBlock) void k_gemv(const GemvArgs a) {
                 acc[r] += in_row ? d : 0.0f;
             }
         }
-        if (ti == TPG - 1) epilogue(g);
+        if (ti == TPG - 1) epilogue(g, ecur);
         g = gn;
         ti = tn;
-        return more;
     };
-    if (g < a.total_groups) {
-        for (;;) {
-            if (!step(wa, wb)) break;
-            if (!step(wb, wa)) break;
-        }
+    int k = 0;
+    for (; k + 2 <= n_tiles; k += 2) {
+        step(wa, ea, wb, eb);
+        step(wb, eb, wa, ea);
     }
+    if (k < n_tiles) step(wa, ea, wb, eb);
 
     if (MODE == GEMV_LOGITS) {
         __shared__ unsigned long long wbest[kWavesPerBlock];

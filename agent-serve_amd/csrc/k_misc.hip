@@ -147,6 +147,12 @@ __global__ __launch_bounds__(kBlock) void k_read_stream(const float4* p, size_t 
     if ((threadIdx.x & 63) == 0) out[(size_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)] = acc;
 }
 
+// Copy stream (bench/stream.c:106-115 on the GPU): every byte read once and written once.
+__global__ __launch_bounds__(kBlock) void k_copy_stream(float4* __restrict__ dst, const float4* __restrict__ src,
+                                                        size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (size_t)gridDim.x * kBlock) dst[i] = src[i];
+}
+
 int grid_for(int64_t work) {
     const int64_t cap = 16LL * device_cu_count();
     int64_t b = (work + kBlock - 1) / kBlock;
@@ -204,6 +210,11 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, int n, int rows, 
 
 hipError_t launch_argmax(const float* x, int n, Ctl* ctl, hipStream_t st) {
     hipLaunchKernelGGL(k_argmax, dim3(grid_for(n)), dim3(kBlock), 0, st, x, n, ctl);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_stream(float4* dst, const float4* src, size_t n4, int blocks, hipStream_t st) {
+    hipLaunchKernelGGL(k_copy_stream, dim3(blocks), dim3(kBlock), 0, st, dst, src, n4);
     return hipGetLastError();
 }
 

@@ -971,4 +971,37 @@ int tf_hip_read_stream(int device, size_t nbytes, int32_t iters, double* best, d
     return 0;
 }
 
+int tf_hip_copy_stream(int device, size_t nbytes, int32_t iters, double* best, double* median) {
+    if (nbytes < 16 || iters <= 0 || !best || !median) return TF_HIP_EINVAL;
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    const size_t n4 = nbytes / 16;
+    float4 *src, *dst;
+    const int blocks = 8 * device_cu_count();
+    OPCHK(s.alloc(&src, n4 * 16));
+    OPCHK(s.alloc(&dst, n4 * 16));
+    OPCHK(hipMemset(src, 0, n4 * 16));
+    hipEvent_t e0, e1;
+    OPCHK(hipEventCreate(&e0));
+    OPCHK(hipEventCreate(&e1));
+    std::vector<double> gbs;
+    OPCHK(launch_copy_stream(dst, src, n4, blocks, s.st));  // warm-up
+    for (int i = 0; i < iters; ++i) {
+        OPCHK(hipEventRecord(e0, s.st));
+        OPCHK(launch_copy_stream(dst, src, n4, blocks, s.st));
+        OPCHK(hipEventRecord(e1, s.st));
+        OPCHK(hipEventSynchronize(e1));
+        float ms = 0;
+        OPCHK(hipEventElapsedTime(&ms, e0, e1));
+        gbs.push_back(2.0 * (double)n4 * 16 / (ms * 1e-3) / 1e9);
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    std::sort(gbs.begin(), gbs.end());
+    *best = gbs.back();
+    *median = gbs[gbs.size() / 2];
+    return 0;
+}
+
 }  // extern "C"

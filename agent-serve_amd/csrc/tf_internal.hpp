@@ -119,6 +119,7 @@ hipError_t launch_repack(int type, const uint8_t* raw, int64_t K, int64_t N, Dev
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, int n, int rows, float eps, float* out,
                                hipStream_t st);
 hipError_t launch_argmax(const float* x, int n, Ctl* ctl, hipStream_t st);
+hipError_t launch_copy_stream(float4* dst, const float4* src, size_t n4, int blocks, hipStream_t st);
 hipError_t launch_read_stream(const float4* p, size_t n4, double* out, int blocks, hipStream_t st);
 int device_cu_count();
 

@@ -1,0 +1,95 @@
+"""Summaries of rocprofv3 CSV output for the decode step, as short text.
+
+    python3 agent-serve_amd/profsum.py trace <kernel_stats.csv> [--steps K]
+    python3 agent-serve_amd/profsum.py traffic <fetch counter_collection.csv> <write counter_collection.csv>
+        --copy-bytes N
+
+`trace` lists each kernel's calls and average / min duration from a --kernel-trace --stats
+run. `traffic` turns the FETCH_SIZE and WRITE_SIZE counters (KiB per dispatch, one
+--pmc run each) into HBM bytes per dispatch, each scaled by what the same counter reads
+for k_copy_stream, which reads N bytes and writes N bytes; the last line,
+`traffic_bytes_per_launch <kernel> <bytes>`, is what bench.py reads back.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import re
+import sys
+
+
+def short(name: str) -> str:
+    name = re.sub(r"\(tfk::[A-Za-z]+\)$", "", name)
+    name = name.replace("tfk::gemv_detail::", "").replace("tfk::(anonymous namespace)::", "")
+    return re.sub(r"^void ", "", name)[:60]
+
+
+def decode_class(name: str) -> str:
+    """Kernel class of a decode-step dispatch, as tf_hip_profile_generate names them: the
+    GEMV's epilogue mode (0 store, 1 residual, 2 SiLU*up, 3 logits) and steps per tile U
+    tell the QKV, wo, gate/up, down and lm_head launches apart."""
+    m = re.search(r"k_gemv<(\d+), (\d+), (\d+), (\d+)>", name)
+    if m:
+        mode, u = int(m.group(3)), int(m.group(4))
+        return {0: "qkv_gemv", 2: "gateup_gemv", 3: "lmhead_gemv"}.get(mode, "down_gemv" if u == 4 else "wo_gemv")
+    for key, cls in (("k_attn_decode", "attention"), ("k_attn_combine", "attention"), ("k_embed", "embed")):
+        if key in name:
+            return cls
+    return short(name).replace(" ", "")
+
+
+def trace(path: str, steps: int | None) -> None:
+    rows = list(csv.DictReader(open(path)))
+    print(f"{'kernel':60s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'total_ms':>9s}")
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        print(f"{short(r['Name']):60s} {int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.2f} "
+              f"{float(r['MinNs']) / 1e3:9.2f} {float(r['TotalDurationNs']) / 1e6:9.3f}")
+
+
+def counter_means(path: str, counter: str) -> dict[str, tuple[int, float]]:
+    acc: dict[str, list[float]] = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        if r["Counter_Name"] == counter:
+            acc[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return {k: (len(v), sum(v) / len(v)) for k, v in acc.items()}
+
+
+def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> None:
+    fetch = counter_means(fetch_csv, "FETCH_SIZE")
+    write = counter_means(write_csv, "WRITE_SIZE")
+    copy_key = next(k for k in fetch if "k_copy_stream" in k)
+    f_scale = copy_bytes / (fetch[copy_key][1] * 1024.0)
+    w_scale = copy_bytes / (write[copy_key][1] * 1024.0)
+    print(f"k_copy_stream of {copy_bytes} bytes: FETCH_SIZE {fetch[copy_key][1]:.0f} KiB, "
+          f"WRITE_SIZE {write[copy_key][1]:.0f} KiB -> scale fetch {f_scale:.4f}, write {w_scale:.4f}")
+    print(f"{'kernel':60s} {'n':>5s} {'fetch_KiB':>11s} {'write_KiB':>10s} {'hbm_bytes':>12s}")
+    for k, (n, f) in sorted(fetch.items(), key=lambda kv: -kv[1][1]):
+        if k == copy_key:
+            continue
+        w = write.get(k, (0, 0.0))[1]
+        b = f * 1024.0 * f_scale + w * 1024.0 * w_scale
+        print(f"{short(k):60s} {n:5d} {f:11.1f} {w:10.1f} {b:12.0f}")
+    for k, (n, f) in fetch.items():
+        if k == copy_key:
+            continue
+        w = write.get(k, (0, 0.0))[1]
+        print(f"traffic_bytes_per_launch {decode_class(k)} {f * 1024.0 * f_scale + w * 1024.0 * w_scale:.0f}")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("what", choices=["trace", "traffic"])
+    ap.add_argument("files", nargs="+")
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--copy-bytes", type=int, default=1 << 30)
+    a = ap.parse_args()
+    if a.what == "trace":
+        trace(a.files[0], a.steps)
+    else:
+        traffic(a.files[0], a.files[1], a.copy_bytes)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

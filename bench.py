@@ -34,6 +34,8 @@ PRESET = "llama1b_q8"
 PROMPT_TOKENS = 6
 MAX_SEQ = 512
 HBM_PEAK_GBS = 8000.0
+COPY_CALIB_BYTES = 1 << 30
+TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_llama1b_q8_0_traffic.txt"
 PUBLISHED_CPU_TOK_S = 10.74  # reference --stage v2, Llama-3.2-1B Q8_0, Ryzen 5 4600H
 
 
@@ -49,6 +51,20 @@ def model_path() -> str:
     d = pathlib.Path(tempfile.gettempdir()) / "tinferno_bench"
     d.mkdir(parents=True, exist_ok=True)
     return str(d / f"{PRESET}-seed42.gguf")
+
+
+def measured_traffic(kernel_class: str):
+    """HBM bytes per launch of `kernel_class` from the committed counter summary (two
+    rocprofv3 --pmc runs of this script, FETCH_SIZE then WRITE_SIZE, scaled by the
+    counters of the known-size copy it runs); None when no summary covers it."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            f = line.split()
+            if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == kernel_class:
+                return int(float(f[2]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(path, prompt, n_decode, want_ids):
@@ -135,6 +151,8 @@ def main() -> int:
     achieved = (d_bytes / d_launch) / (d_ms / d_launch * 1e-3) / 1e9
     m.close()
     read_best, read_med = pkg.read_stream(4 << 30, iters=10)
+    # known-size copy: the reference dispatch for the HBM byte counters (FETCH_SIZE, WRITE_SIZE)
+    copy_best, _ = pkg.copy_stream(COPY_CALIB_BYTES, iters=3)
 
     cpu, match = (None, None) if args.no_cpu else cpu_baseline(path, prompt, K, ids)
 
@@ -168,7 +186,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dom),
             "kernel": dom,
             "launches": d_launch,
             "bytes_per_launch": round(d_bytes / d_launch),
@@ -177,6 +195,7 @@ def main() -> int:
         "step_hbm_gb_s": round(step_gbs, 1),
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "read_stream_gb_s": round(read_best, 1),
+        "copy_stream_gb_s": round(copy_best, 1),
         "step_frac_of_read_stream": round(step_gbs / read_best, 4),
         "bytes_per_step": round(statistics.mean(step_bytes)),
         "device_ms_per_step": round(dev_ms / K, 4),

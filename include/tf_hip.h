@@ -167,6 +167,11 @@ int tf_hip_argmax(int device, const float* x, int32_t n, int32_t* out);
  * memory `iters` times; reports the best and median GB/s over the iterations. */
 int tf_hip_read_stream(int device, size_t nbytes, int32_t iters, double* best_gbs, double* median_gbs);
 
+/* Copy stream (the GPU analogue of kernel_copy, bench/stream.c:106-115): copies nbytes
+ * between two device buffers `iters` times; GB/s counts the bytes read plus the bytes
+ * written. Its kernel (k_copy_stream) is also the known-size reference for HBM counters. */
+int tf_hip_copy_stream(int device, size_t nbytes, int32_t iters, double* best_gbs, double* median_gbs);
+
 #ifdef __cplusplus
 }
 #endif

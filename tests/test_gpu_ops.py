@@ -151,3 +151,8 @@ def test_argmax_first_maximum(pkg):
 def test_read_stream_runs(pkg):
     best, med = pkg.read_stream(1 << 28, iters=3)
     assert best > 100.0 and med > 0
+
+
+def test_copy_stream_runs(pkg):
+    best, med = pkg.copy_stream(1 << 28, iters=3)
+    assert best > 100.0 and med > 0
