@@ -55,6 +55,8 @@ def hip_lib() -> C.CDLL:
         "tf_hip_decode": (C.c_int, [vp, C.c_int32, _f32p, _i32p]),
         "tf_hip_generate": (C.c_int, [vp, C.c_int32, _i32p]),
         "tf_hip_reset": (C.c_int, [vp]),
+        "tf_hip_set_decode_path": (C.c_int, [vp, C.c_int32]),
+        "tf_hip_get_decode_path": (C.c_int, [vp]),
         "tf_hip_get_pos": (C.c_int, [vp]),
         "tf_hip_get_layer_act": (C.c_int, [vp, C.c_int32, _f32p]),
         "tf_hip_read_kv": (C.c_int, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _f32p]),
@@ -231,6 +233,23 @@ class HipModel:
 
     def reset(self):
         self._check(self._L.tfh_reset(self._h))
+
+    PATH_GRAPH, PATH_STEP = 0, 1
+
+    def set_decode_path(self, path: int):
+        """PATH_STEP: one persistent kernel per call where the model allows it (default);
+        PATH_GRAPH: the captured per-layer graph, replayed per token."""
+        H = hip_lib()
+        rc = H.tf_hip_set_decode_path(self._L.tfh_ctx(self._h), int(path))
+        if rc != 0:
+            raise RuntimeError(f"tf_hip_set_decode_path({path}) failed: {rc}")
+
+    def decode_path(self) -> int:
+        H = hip_lib()
+        rc = H.tf_hip_get_decode_path(self._L.tfh_ctx(self._h))
+        if rc < 0:
+            raise RuntimeError(H.tf_hip_last_error(self._L.tfh_ctx(self._h)).decode())
+        return rc
 
     def layer_act(self, layer: int) -> np.ndarray:
         out = np.zeros(self.n_embd, np.float32)

@@ -1,0 +1,57 @@
+// Dispatch of the persistent step kernel (k_step.hpp): exchange and LDS sizes, the
+// compiled (layer format, lm_head format, head size) combinations, cooperative launch.
+#include "k_step.hpp"
+
+namespace tfk {
+
+using step_detail::attn_lds_floats;
+
+size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg) {
+    const size_t n_rep = (size_t)(H / G);
+    return 2 * ((size_t)D + (size_t)D + (size_t)G * (n_rep + 2) * hd + (size_t)H * hd + (size_t)F + (size_t)n_wg +
+                2 * (size_t)n_wg);
+}
+
+size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg) {
+    const int n_rep = H / G;
+    const int region = step_detail::region_floats(D, F, n_rep, hd, n_wg);
+    const size_t table = ((size_t)n_layer * sizeof(StepLayer) + 15) / 16 * 16;
+    const size_t floats = (size_t)(D + 3) / 4 * 4 + (size_t)(region + 3) / 4 * 4 + (size_t)(n_rep + 2) * hd +
+                          (size_t)n_rep * hd;
+    return table + 4 * floats;
+}
+
+namespace {
+
+template <int TL, int TO, int HDM>
+hipError_t launch_t(const StepArgs& a, int n_wg, hipStream_t st) {
+    const void* fn = (const void*)step_detail::k_step<TL, TO, HDM>;
+    const size_t lds = step_lds_bytes(a.n_layer, a.D, a.F, a.H, a.G, a.hd, n_wg);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    int per_cu = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kStepThreads, lds);
+    if (e != hipSuccess) return e;
+    if (per_cu < 1 || n_wg > per_cu * device_cu_count()) return hipErrorCooperativeLaunchTooLarge;
+    StepArgs arg = a;
+    void* params[] = {(void*)&arg};
+    return hipLaunchCooperativeKernel(fn, dim3(n_wg), dim3(kStepThreads), params, (unsigned)lds, st);
+}
+
+}  // namespace
+
+bool step_supported(int tl, int to, int hd) {
+    if (hd > 128) return false;
+    return (tl == TF_HIP_TYPE_Q8_0 && to == TF_HIP_TYPE_Q8_0) || (tl == TF_HIP_TYPE_F32 && to == TF_HIP_TYPE_F32 && hd <= 64);
+}
+
+hipError_t launch_step(const StepArgs& a, int tl, int to, int n_wg, hipStream_t st) {
+    if (tl == TF_HIP_TYPE_Q8_0 && to == TF_HIP_TYPE_Q8_0)
+        return a.hd <= 64 ? launch_t<TF_HIP_TYPE_Q8_0, TF_HIP_TYPE_Q8_0, 64>(a, n_wg, st)
+                          : launch_t<TF_HIP_TYPE_Q8_0, TF_HIP_TYPE_Q8_0, 128>(a, n_wg, st);
+    if (tl == TF_HIP_TYPE_F32 && to == TF_HIP_TYPE_F32 && a.hd <= 64)
+        return launch_t<TF_HIP_TYPE_F32, TF_HIP_TYPE_F32, 64>(a, n_wg, st);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace tfk

@@ -1,0 +1,714 @@
+// Persistent decode step: one cooperative launch runs n tokens of the token loop
+// (Model::decode, model.cpp:197-208, and the per-token layers of Model::prefill,
+// model.cpp:144-195) with one workgroup of 8 waves per CU.
+//
+// Per layer (layer_decode, model.cpp:108-142), five phases:
+//   1 QKV GEMV, attn_norm fused, bias added          -> q, k, v   (model.cpp:110-124)
+//   2 attention, one workgroup per kv head            -> att       (model.cpp:125-130)
+//   3 wo GEMV + residual                              -> x         (model.cpp:131)
+//   4 gate/up GEMV, ffn_norm fused, SiLU(gate)*up     -> h         (model.cpp:133-139)
+//   5 down GEMV + residual                            -> x         (model.cpp:140-141)
+// then output_norm + lm_head + greedy argmax (model.cpp:204-207, sampler.cpp:8-13).
+//
+// Workgroups hand activations to each other as 64-bit words (epoch << 32 | float bits)
+// stored and loaded with agent-scope relaxed atomics. Each (token, layer, phase) has its
+// own epoch, so a consumer knows a word is current when it carries that epoch: no fence,
+// counter or grid barrier is involved. Every workgroup also publishes one word at the end
+// of a layer and the next layer waits for all of them, which makes each layer boundary a
+// barrier; exchange buffers alternate by layer parity, so a buffer is rewritten only after
+// every workgroup has finished reading it. Each wave issues the loads of its first two
+// weight tiles before it waits for its phase's input, so HBM keeps streaming while the
+// hand-off completes. Every wait is bounded: past the limit, or once another workgroup
+// has flagged a failure, it flags ctl->err and goes on, and the host reports the error.
+#pragma once
+#include "formats.hpp"
+
+namespace tfk {
+namespace step_detail {
+
+typedef unsigned long long u64;
+
+constexpr int kT = kStepThreads;   // threads per workgroup
+constexpr int kNW = kT / kWave;    // waves per workgroup
+constexpr int kGD = 8;             // exchange words per thread for d_model-sized inputs (<= 4096)
+constexpr int kGF = 20;            // and for d_ff-sized ones (<= 10240)
+constexpr int kGW = 2;             // and for per-workgroup words (<= 1024)
+constexpr int kMaxRep = 8;         // query heads per kv head
+constexpr int kTile = 32;          // attention positions per LDS tile
+constexpr int kSpinLimit = 1 << 20;  // about a second of polling
+constexpr int kErrToken = 1;
+constexpr int kErrTimeout = 2;
+
+__device__ __forceinline__ void put(u64* p, float v, uint32_t e) {
+    __hip_atomic_store(p, ((u64)e << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 get(u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ int get_err(Ctl* c) {
+    return __hip_atomic_load(&c->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void set_err(Ctl* c, int v) {
+    __hip_atomic_store(&c->err, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits for the na words pa[0..na) of epoch ea and writes their values to da (LDS), and
+// for the nb words pb[0..nb) of epoch eb (arrival words; values unused). Thread tid reads
+// words tid + i*kT. Every load of the first pass is issued before any is checked; a word
+// that does not carry its epoch yet is read again (bit i of `pend`) until it does.
+// Needs na <= NA * kT, nb <= NB * kT, NA + NB <= 32.
+template <int NA, int NB>
+__device__ __forceinline__ void gather(u64* pa, int na, uint32_t ea, float* da, u64* pb, int nb, uint32_t eb,
+                                       Ctl* ctl) {
+    const int tid = threadIdx.x;
+    u64 wa[NA], wb[NB];
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+        if (tid + i * kT < na) wa[i] = get(pa + tid + i * kT);
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+        if (tid + i * kT < nb) wb[i] = get(pb + tid + i * kT);
+    uint32_t pend = 0;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int j = tid + i * kT;
+        if (j < na) {
+            if ((uint32_t)(wa[i] >> 32) == ea)
+                da[j] = __uint_as_float((uint32_t)wa[i]);
+            else
+                pend |= 1u << i;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+        if (tid + i * kT < nb && (uint32_t)(wb[i] >> 32) != eb) pend |= 1u << (NA + i);
+    for (int spin = 0; pend; ++spin) {
+        if (spin >= kSpinLimit || ((spin & 1023) == 1023 && get_err(ctl))) {
+            set_err(ctl, kErrTimeout);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            if (pend & (1u << i)) {
+                const int j = tid + i * kT;
+                const u64 w = get(pa + j);
+                if ((uint32_t)(w >> 32) == ea) {
+                    da[j] = __uint_as_float((uint32_t)w);
+                    pend &= ~(1u << i);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (pend & (1u << (NA + i))) {
+                const u64 w = get(pb + tid + i * kT);
+                if ((uint32_t)(w >> 32) == eb) pend &= ~(1u << (NA + i));
+            }
+        }
+    }
+}
+
+// xs = rmsnorm(xr) (layers.cpp:7-12: fp64 sum of squares, inv = 1/sqrtf(ss/n + eps),
+// x * inv * w) when w is set, else a copy; then the 16-element sums of xs when wanted.
+// wr holds this thread's norm weights xs[tid + i*kT], loaded by the caller.
+template <int NWR>
+__device__ __forceinline__ void stage(const float* xr, int K, bool norm, const float (&wr)[NWR], float eps, float* xs, float* x16,
+                      bool sums, double* red) {
+    const int tid = threadIdx.x;
+    __syncthreads();  // xr / xs written by the gather
+    if (norm) {
+        double ss = 0;
+        for (int j = tid; j < K; j += kT) {
+            const double v = xr[j];
+            ss += v * v;
+        }
+        ss = wave_sum_d(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        ss = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+        const float inv = 1.0f / sqrtf((float)(ss / K) + eps);
+#pragma unroll
+        for (int i = 0; i < NWR; ++i) {
+            const int j = tid + i * kT;
+            if (j < K) xs[j] = (xr[j] * inv) * wr[i];
+        }
+        __syncthreads();
+    }
+    if (sums) {
+        for (int c = tid; c < K / 16; c += kT) {
+            const float4* p = (const float4*)(xs + 16 * c);
+            const float4 u = p[0], v = p[1], w = p[2], z = p[3];
+            x16[c] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w)) + ((w.x + w.y) + (w.z + w.w)) +
+                     ((z.x + z.y) + (z.z + z.w));
+        }
+    }
+    __syncthreads();
+}
+
+// Norm weights of this thread (elements tid + i*kT), read before the phase's weight tiles
+// so that waiting for them never waits for the tiles.
+template <int NWR>
+__device__ __forceinline__ void load_norm(const float* w, int K, float (&wr)[NWR]) {
+#pragma unroll
+    for (int i = 0; i < NWR; ++i) {
+        const int j = threadIdx.x + i * kT;
+        wr[i] = w ? w[j < K ? j : K - 1] : 1.0f;
+    }
+}
+
+// Rows of up to three matrices of one format (the segments), grouped R rows at a time;
+// wave wid of nw takes groups wid, wid + nw, ... (wid < 0: no rows). A group's rows are
+// walked in tiles of U*64 lane steps, double-buffered in registers; the first two tiles
+// are loaded before prep() (the phase's input hand-off), the rest stream behind the
+// compute. Loads are unconditional (indices clamped, contributions masked) so that the
+// compiler's waits stay partial. seg_of(si, 0 | 1) is segment si's matrix (1: the up
+// matrix of SILU), bias_of(si) its bias or nullptr; epi(si, row, v, v_up, bias) runs on
+// lane r for row r. The workgroup synchronises before prep(), so prep may overwrite the
+// LDS the previous phase read.
+template <int T, int R, int MODE, int U, class SegOf, class BiasOf, class Prep, class Epi>
+__device__ __forceinline__ void gemv_phase(int nseg, const int (&groups)[3], SegOf&& seg_of, BiasOf&& bias_of, int K,
+                                           int wid, int nw, const float* xs, const float* x16, Prep&& prep,
+                                           Epi&& epi) {
+    using F = Fmt<T>;
+    using Raw = typename F::Raw;
+    constexpr bool SILU = MODE == GEMV_SILU;
+    constexpr int NR = SILU ? 2 * R : R;
+    const int lane = threadIdx.x & 63;
+    const int S = K / F::E;
+    const int TPG = (S + kWave * U - 1) / (kWave * U);
+    const int total = groups[0] + (nseg > 1 ? groups[1] : 0) + (nseg > 2 ? groups[2] : 0);
+    const int n_tiles = (wid >= 0 && wid < total) ? ((total - 1 - wid) / nw + 1) * TPG : 0;
+
+    // segment and first row of group g (compile-time segment indices only)
+    auto locate = [&](int g, int& row0) -> int {
+        if (nseg > 1 && g >= groups[0]) {
+            g -= groups[0];
+            if (nseg > 2 && g >= groups[1]) {
+                row0 = (g - groups[1]) * R;
+                return 2;
+            }
+            row0 = g * R;
+            return 1;
+        }
+        row0 = g * R;
+        return 0;
+    };
+    auto load_k = [&](int k, Raw (&w)[U][NR], float& extra) {
+        k = k < n_tiles ? k : n_tiles - 1;
+        const int g = wid + (k / TPG) * nw;
+        const int ti = k - (k / TPG) * TPG;
+        int row0;
+        const int si = locate(g, row0);
+        const DevMat& ma = seg_of(si, 0);
+        const int N = (int)ma.N;
+        if (MODE == GEMV_STORE) {
+            const float* bias = bias_of(si);
+            int re = row0 + (lane < R ? lane : R - 1);
+            re = re < N ? re : N - 1;
+            extra = bias ? bias[re] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = row0 + r < N ? row0 + r : N - 1;
+            const RowPtr pa = F::row(ma, row);
+            RowPtr pb = pa;
+            if (SILU) pb = F::row(seg_of(si, 1), row);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                int s = ti * kWave * U + u * kWave + lane;
+                s = s < S ? s : S - 1;
+                w[u][r] = F::load(pa, s);
+                if (SILU) w[u][R + r] = F::load(pb, s);
+            }
+        }
+    };
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
+    auto consume = [&](int k, Raw (&w)[U][NR], float extra) {
+        const int g = wid + (k / TPG) * nw;
+        const int ti = k - (k / TPG) * TPG;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = ti * kWave * U + u * kWave + lane;
+            const bool in_row = s < S;
+            const int sc = in_row ? s : S - 1;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const float d = F::dot(w[u][r], xs, x16, sc);
+                acc[r] += in_row ? d : 0.0f;
+            }
+        }
+        if (ti == TPG - 1) {
+#pragma unroll
+            for (int r = 0; r < NR; ++r) acc[r] = wave_sum(acc[r]);
+            int row0;
+            const int si = locate(g, row0);
+            const int N = (int)seg_of(si, 0).N;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (lane == r && row0 + r < N) epi(si, row0 + r, acc[r], SILU ? acc[R + r] : 0.0f, extra);
+#pragma unroll
+            for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
+        }
+    };
+
+    Raw wa[U][NR], wb[U][NR];
+    float ea = 0.0f, eb = 0.0f;
+    __builtin_amdgcn_sched_barrier(0);  // keep this phase's code out of the previous one's
+    if (n_tiles > 0) {
+        load_k(0, wa, ea);
+        load_k(1, wb, eb);
+    }
+    __syncthreads();
+    prep();
+    int k = 0;
+    for (; k + 2 <= n_tiles; k += 2) {
+        consume(k, wa, ea);
+        load_k(k + 2, wa, ea);
+        consume(k + 1, wb, eb);
+        load_k(k + 3, wb, eb);
+    }
+    if (k < n_tiles) consume(k, wa, ea);
+}
+
+__device__ __forceinline__ int64_t kv_at(int layout, int G, int max_seq, int hd, int g, int p) {
+    return layout == TF_HIP_KV_HEAD_MAJOR ? ((int64_t)g * max_seq + p) * hd : ((int64_t)p * G + g) * hd;
+}
+
+// Attention of kv head g over positions [start, pos] (attn_decode, attention.cpp:55-80),
+// with the RoPE of its query heads and key (attention.cpp:31-46) and the KV store
+// (kvcache.cpp:31-36). qkv (LDS) holds the head block [n_rep q heads | k | v] as the QKV
+// phase left it; the output heads go to out (LDS, [n_rep][hd]). The same workgroup runs
+// head g for every token of a launch, so the rows it stores are the ones it later reads
+// on this CU.
+template <int HDM>
+__device__ __noinline__ void attn_head(const StepArgs& a, const StepLayer& ly, int g, int pos, int start, float* qkv, float* sm,
+                          float* out) {
+    constexpr int kTV = (kTile * HDM / 4 + kT - 1) / kT;  // float4 of a K (or V) tile per thread
+    constexpr int kPairs = (kMaxRep * HDM + kT - 1) / kT;  // (head, dim) pairs of P.V per thread
+    const int hd = a.hd, d2 = hd / 2, hd4 = hd / 4;
+    const int n_rep = a.H / a.G;
+    const int tid = threadIdx.x;
+    const int ks = hd + 4;
+    float* qs = qkv;                  // [n_rep][hd], rotated in place
+    float* kn = qkv + n_rep * hd;     // [hd]
+    float* vn = kn + hd;              // [hd]
+    float* kt = sm;                   // [kTile][hd + 4]
+    float* vt = kt + kTile * ks;      // [kTile][hd]
+    float* pr = vt + kTile * hd;      // [n_rep][kTile]
+    float* st = pr + n_rep * kTile;   // [n_rep][3]
+    const float* cs = a.rope_cos + (int64_t)pos * d2;
+    const float* sn = a.rope_sin + (int64_t)pos * d2;
+    const int p1 = pos + 1;
+
+    auto load_tile = [&](int t0, float4 (&kr)[kTV], float4 (&vr)[kTV]) {
+        const int tn = min(kTile, p1 - t0);
+#pragma unroll
+        for (int k = 0; k < kTV; ++k) {
+            int i = tid + k * kT;
+            i = i < tn * hd4 ? i : tn * hd4 - 1;
+            const int j = i / hd4, c = i % hd4;
+            const int64_t o = kv_at(a.layout, a.G, a.max_seq, hd, g, t0 + j) + 4 * c;
+            kr[k] = *(const float4*)(ly.kc + o);
+            vr[k] = *(const float4*)(ly.vc + o);
+        }
+    };
+    float4 kr_a[kTV], vr_a[kTV], kr_b[kTV], vr_b[kTV];
+    load_tile(start, kr_a, vr_a);
+    // RoPE (rope_one, with the reference build's contractions)
+    for (int i = tid; i < (n_rep + 1) * d2; i += kT) {
+        const int r = i / d2, j = i % d2;
+        float* v = qs + r * hd;  // r == n_rep is the key
+        const float x0 = v[j], x1 = v[j + d2], c = cs[j], s = sn[j];
+        v[j] = fmaf(x0, c, -(x1 * s));
+        v[j + d2] = fmaf(x0, s, x1 * c);
+    }
+    if (tid < n_rep) {
+        st[3 * tid] = -INFINITY;
+        st[3 * tid + 1] = 0.0f;
+    }
+    __syncthreads();
+    {
+        const int64_t o = kv_at(a.layout, a.G, a.max_seq, hd, g, pos);
+        for (int j = tid; j < hd; j += kT) {
+            ly.kc[o + j] = kn[j];
+            ly.vc[o + j] = vn[j];
+        }
+    }
+    const float scale = 1.0f / sqrtf((float)hd);
+    float o_acc[kPairs];
+#pragma unroll
+    for (int k = 0; k < kPairs; ++k) o_acc[k] = 0.0f;
+    const int lane = tid & 63, wave = tid >> 6;
+
+    auto tile = [&](int t0, float4 (&kr)[kTV], float4 (&vr)[kTV], float4 (&kn_r)[kTV], float4 (&vn_r)[kTV]) {
+        const int tn = min(kTile, p1 - t0);
+        if (t0 + kTile < p1) load_tile(t0 + kTile, kn_r, vn_r);
+#pragma unroll
+        for (int k = 0; k < kTV; ++k) {
+            const int i = tid + k * kT;
+            if (i < tn * hd4) {
+                const int j = i / hd4, c = i % hd4;
+                const bool is_new = t0 + j == pos;  // the cache row may still be the old one
+                *(float4*)(kt + j * ks + 4 * c) = is_new ? *(const float4*)(kn + 4 * c) : kr[k];
+                *(float4*)(vt + j * hd + 4 * c) = is_new ? *(const float4*)(vn + 4 * c) : vr[k];
+            }
+        }
+        __syncthreads();
+        // scores in dot_f32's order (8 lanes, then hsum8; quant.cpp:198-214)
+        for (int i = tid; i < n_rep * tn; i += kT) {
+            const int r = i / tn, j = i % tn;
+            const float* qr = qs + r * hd;
+            const float* krow = kt + j * ks;
+            float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int e = 0; e < hd; e += 8) {
+                const float4 q0 = *(const float4*)(qr + e), q1 = *(const float4*)(qr + e + 4);
+                const float4 x0 = *(const float4*)(krow + e), x1 = *(const float4*)(krow + e + 4);
+                c[0] = fmaf(q0.x, x0.x, c[0]);
+                c[1] = fmaf(q0.y, x0.y, c[1]);
+                c[2] = fmaf(q0.z, x0.z, c[2]);
+                c[3] = fmaf(q0.w, x0.w, c[3]);
+                c[4] = fmaf(q1.x, x1.x, c[4]);
+                c[5] = fmaf(q1.y, x1.y, c[5]);
+                c[6] = fmaf(q1.z, x1.z, c[6]);
+                c[7] = fmaf(q1.w, x1.w, c[7]);
+            }
+            pr[r * kTile + j] = scale * (((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7])));
+        }
+        __syncthreads();
+        for (int r = wave; r < n_rep; r += kNW) {
+            const float v = lane < tn ? pr[r * kTile + lane] : -INFINITY;
+            const float m_old = st[3 * r];
+            const float m_new = fmaxf(m_old, wave_max(v));
+            const float e = lane < tn ? expf(v - m_new) : 0.0f;
+            if (lane < tn) pr[r * kTile + lane] = e;
+            const float l_tile = wave_sum(e);
+            if (lane == 0) {
+                const float alpha = expf(m_old - m_new);
+                st[3 * r] = m_new;
+                st[3 * r + 1] = fmaf(st[3 * r + 1], alpha, l_tile);
+                st[3 * r + 2] = alpha;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kPairs; ++k) {
+            const int pi = tid + k * kT;
+            if (pi < n_rep * hd) {
+                const int r = pi / hd, d = pi % hd;
+                float o = o_acc[k] * st[3 * r + 2];
+                for (int j = 0; j < tn; ++j) o = fmaf(pr[r * kTile + j], vt[j * hd + d], o);
+                o_acc[k] = o;
+            }
+        }
+        __syncthreads();
+    };
+    for (int t0 = start; t0 < p1;) {
+        tile(t0, kr_a, vr_a, kr_b, vr_b);
+        t0 += kTile;
+        if (t0 >= p1) break;
+        tile(t0, kr_b, vr_b, kr_a, vr_a);
+        t0 += kTile;
+    }
+#pragma unroll
+    for (int k = 0; k < kPairs; ++k) {
+        const int pi = tid + k * kT;
+        if (pi < n_rep * hd) out[pi] = o_acc[k] / st[3 * (pi / hd) + 1];
+    }
+    __syncthreads();
+}
+
+// Floats of LDS the attention scratch needs.
+__host__ __device__ inline int attn_lds_floats(int n_rep, int hd) {
+    return kTile * (hd + 4) + kTile * hd + n_rep * kTile + 3 * n_rep;
+}
+
+// The shared region: a GEMV input and its 16-element sums, the attention scratch, or the
+// 2 * n_wg argmax words, whichever is largest.
+__host__ __device__ inline int region_floats(int D, int F, int n_rep, int hd, int n_wg) {
+    const int kmax = D > F ? D : F;
+    int r = kmax + kmax / 16;
+    const int att = attn_lds_floats(n_rep, hd);
+    r = att > r ? att : r;
+    return 2 * n_wg > r ? 2 * n_wg : r;
+}
+
+// Launch constants, kept in LDS: phases re-read what they need after their barriers
+// instead of holding dozens of kernel-wide values in registers across the whole launch.
+struct StepConst {
+    StepArgs a;
+    int L, D, F, G, hd, n_rep, Hd, HB, nwg, P, attn_wg0;
+    int o_xr, o_xs, o_x16, o_qkv, o_att;  // LDS byte offsets of the arrays below the layer table
+    uint32_t e0;
+    int pos0;
+    u64 key0;
+    // exchange buffers (word offsets into a.ex), each twice (layer or token parity)
+    int XA, XB, QKV, ATT, HH, DONE, BEST;
+};
+
+template <int TL, int TO, int HDM>
+__global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
+    using FE = Fmt<TO>;  // the embedding table has the lm_head's format (checked by the host)
+    constexpr int NWR = 8;  // norm weights per thread: d_model <= 4096
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ __align__(16) unsigned char sc_raw[sizeof(StepConst)];  // StepConst is not trivially constructible
+    StepConst& sc = *reinterpret_cast<StepConst*>(sc_raw);
+    __shared__ double red[kNW];
+    __shared__ u64 wbest[kNW];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg = blockIdx.x;
+    StepLayer* lay = (StepLayer*)smem;
+    if (tid == 0) {
+        StepConst& c = sc;
+        c.a = args;
+        c.L = args.n_layer;
+        c.D = args.D;
+        c.F = args.F;
+        c.G = args.G;
+        c.hd = args.hd;
+        c.n_rep = args.H / args.G;
+        c.Hd = args.H * args.hd;
+        c.HB = (c.n_rep + 2) * args.hd;  // words of one kv head block [q heads | k | v]
+        c.nwg = gridDim.x;
+        c.P = 6 * c.L + 8;               // epochs per token
+        c.attn_wg0 = c.nwg - c.G;        // workgroups attn_wg0.. run the attention heads
+        const int kmax = c.D > c.F ? c.D : c.F;
+        c.o_xr = (int)(((size_t)c.L * sizeof(StepLayer) + 15) / 16 * 16);
+        c.o_xs = c.o_xr + 4 * ((c.D + 3) / 4 * 4);
+        c.o_x16 = c.o_xs + 4 * kmax;
+        c.o_qkv = c.o_xs + 4 * ((region_floats(c.D, c.F, c.n_rep, c.hd, c.nwg) + 3) / 4 * 4);
+        c.o_att = c.o_qkv + 4 * c.HB;
+        c.e0 = args.ctl->epoch;
+        c.pos0 = args.ctl->pos;
+        c.key0 = args.ctl->key;
+        c.XA = 0;
+        c.XB = c.XA + 2 * c.D;
+        c.QKV = c.XB + 2 * c.D;
+        c.ATT = c.QKV + 2 * c.G * c.HB;
+        c.HH = c.ATT + 2 * c.Hd;
+        c.DONE = c.HH + 2 * c.F;
+        c.BEST = c.DONE + 2 * c.nwg;
+    }
+    {
+        const u64* src = (const u64*)args.layers;
+        u64* dst = (u64*)lay;
+        const int nw = (int)(args.n_layer * sizeof(StepLayer) / 8);
+        for (int i = tid; i < nw; i += kT) dst[i] = src[i];
+    }
+    __syncthreads();
+    float* xr = (float*)(smem + sc.o_xr);
+    float* xs = (float*)(smem + sc.o_xs);
+    float* x16 = (float*)(smem + sc.o_x16);
+    auto E = [&](int t, int l, int p) -> uint32_t { return sc.e0 + (uint32_t)(t * sc.P + 6 * l + p); };
+    auto X = [&](int off) -> u64* { return sc.a.ex + off; };
+    auto no_bias = [](int) -> const float* { return nullptr; };
+    const int n_tokens = args.n_tokens;
+    int tok = 0;
+
+    for (int t = 0; t < n_tokens; ++t) {
+        const bool last = t == n_tokens - 1;
+        for (int l = 0; l < sc.L; ++l) {
+            const StepLayer& ly = lay[l];
+            const int par = l & 1;
+            // ---- 1: QKV (attn_norm fused)
+            {
+                const int D = sc.D;
+                float wr[NWR];
+                load_norm(ly.attn_norm, D, wr);
+                const int groups[3] = {(int)ly.wq.N, (int)ly.wk.N, (int)ly.wv.N};
+                auto seg = [&](int si, int) -> const DevMat& { return si == 0 ? ly.wq : si == 1 ? ly.wk : ly.wv; };
+                auto bias = [&](int si) -> const float* { return si == 0 ? ly.bq : si == 1 ? ly.bk : ly.bv; };
+                auto prep = [&]() {
+                    const StepArgs& a = sc.a;
+                    const int pos = sc.pos0 + t;
+                    if (l == 0) {
+                        // the token: staged in hist, or the previous token's argmax
+                        if (t > 0) {
+                            if (a.greedy) {
+                                float* kb = xs;  // free: the barrier before prep has passed
+                                gather<kGW, 1>(X(sc.BEST) + ((t - 1) & 1) * 2 * sc.nwg, 2 * sc.nwg, E(t - 1, sc.L, 6),
+                                               kb, nullptr, 0, 0, a.ctl);
+                                __syncthreads();
+                                if (tid == 0) {
+                                    u64 b = 0;
+                                    for (int i = 0; i < sc.nwg; ++i) {
+                                        const u64 k = ((u64)__float_as_uint(kb[2 * i]) << 32) |
+                                                      (u64)__float_as_uint(kb[2 * i + 1]);
+                                        b = k > b ? k : b;
+                                    }
+                                    wbest[0] = b;
+                                }
+                                __syncthreads();
+                                tok = key_to_index(wbest[0]);
+                            } else {
+                                gather<1, kGW>(nullptr, 0, 0, nullptr, X(sc.DONE) + ((sc.L - 1) & 1) * sc.nwg, sc.nwg,
+                                               E(t - 1, sc.L - 1, 5), a.ctl);
+                                tok = a.hist[pos];
+                            }
+                        } else {
+                            tok = a.greedy ? key_to_index(sc.key0) : a.hist[pos];
+                        }
+                        if (tok < 0 || tok >= (int)a.embd.N) {
+                            if (tid == 0) set_err(a.ctl, kErrToken);
+                            tok = 0;
+                        }
+                        if (wg == 0 && tid == 0) {
+                            a.hist[pos] = tok;
+                            a.ctl->last_token = tok;
+                        }
+                        // dequant_row of the token's row (model.cpp:199)
+                        const RowPtr rp = FE::row(a.embd, tok);
+                        for (int s = tid; s < D / FE::E; s += kT) {
+                            float v[FE::E];
+                            FE::dequant(FE::load(rp, s), v);
+#pragma unroll
+                            for (int i = 0; i < FE::E; ++i) xr[s * FE::E + i] = v[i];
+                        }
+                    } else {
+                        gather<kGD, kGW>(X(sc.XA) + ((l - 1) & 1) * D, D, E(t, l - 1, 5), xr,
+                                         X(sc.DONE) + ((l - 1) & 1) * sc.nwg, sc.nwg, E(t, l - 1, 5), a.ctl);
+                    }
+                    stage(xr, D, true, wr, a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
+                };
+                auto epi = [&](int si, int row, float v, float, float extra) {
+                    const int hd = sc.hd, n_rep = sc.n_rep, HB = sc.HB;
+                    int idx;
+                    if (si == 0) {  // q row of head h = row / hd
+                        const int h = row / hd;
+                        idx = (h / n_rep) * HB + (h % n_rep) * hd + row % hd;
+                    } else {        // k or v row of kv head row / hd
+                        idx = (row / hd) * HB + (n_rep + si - 1) * hd + row % hd;
+                    }
+                    put(X(sc.QKV) + par * sc.G * HB + idx, bias(si) ? v + extra : v, E(t, l, 1));
+                };
+                gemv_phase<TL, 1, GEMV_STORE, 2>(3, groups, seg, bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
+                                                 prep, epi);
+            }
+            // ---- 2: attention (kv head g on workgroup attn_wg0 + g)
+            if (wg >= sc.attn_wg0) {
+                const int g = wg - sc.attn_wg0;
+                const int HB = sc.HB;
+                float* qkv = (float*)(smem + sc.o_qkv);
+                float* att_out = (float*)(smem + sc.o_att);
+                __syncthreads();  // the QKV phase's waves are done with xs
+                gather<kGD, 1>(X(sc.QKV) + par * sc.G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0, sc.a.ctl);
+                __syncthreads();
+                attn_head<HDM>(sc.a, ly, g, sc.pos0 + t, sc.a.att_start, qkv, xs, att_out);
+                const int nh = sc.n_rep * sc.hd;
+                for (int i = tid; i < nh; i += kT) put(X(sc.ATT) + par * sc.Hd + g * nh + i, att_out[i], E(t, l, 2));
+            } else {
+                // ---- 3: wo + residual (workgroups without an attention head)
+                const int Hd = sc.Hd;
+                float wr[1];
+                const int groups[3] = {(int)ly.wo.N, 0, 0};
+                auto seg = [&](int, int) -> const DevMat& { return ly.wo; };
+                auto prep = [&]() {
+                    gather<kGD, 1>(X(sc.ATT) + par * Hd, Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl);
+                    stage(xs, Hd, false, wr, 0.0f, xs, x16, Fmt<TL>::kNeedSums, red);
+                };
+                auto epi = [&](int, int row, float v, float, float) {
+                    put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
+                };
+                gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, Hd, wg * kNW + wave, sc.attn_wg0 * kNW,
+                                                 xs, x16, prep, epi);
+            }
+            // ---- 4: gate/up (ffn_norm fused), SiLU(gate) * up
+            {
+                const int D = sc.D;
+                float wr[NWR];
+                load_norm(ly.ffn_norm, D, wr);
+                const int groups[3] = {(int)((ly.wg.N + 1) / 2), 0, 0};
+                auto seg = [&](int, int what) -> const DevMat& { return what == 1 ? ly.wu : ly.wg; };
+                auto prep = [&]() {
+                    gather<kGD, 1>(X(sc.XB) + par * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl);
+                    stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
+                };
+                auto epi = [&](int, int row, float v, float up, float) {
+                    put(X(sc.HH) + par * sc.F + row, (v / (1.0f + expf(-v))) * up, E(t, l, 4));
+                };
+                gemv_phase<TL, 2, GEMV_SILU, 2>(1, groups, seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
+                                                prep, epi);
+            }
+            // ---- 5: down + residual
+            {
+                const int F = sc.F;
+                float wr[1];
+                const int groups[3] = {(int)ly.wd.N, 0, 0};
+                auto seg = [&](int, int) -> const DevMat& { return ly.wd; };
+                auto prep = [&]() {
+                    gather<kGF, 1>(X(sc.HH) + par * F, F, E(t, l, 4), xs, nullptr, 0, 0, sc.a.ctl);
+                    stage(xs, F, false, wr, 0.0f, xs, x16, Fmt<TL>::kNeedSums, red);
+                };
+                auto epi = [&](int, int row, float v, float, float) {
+                    const float nv = xr[row] + v;
+                    put(X(sc.XA) + par * sc.D + row, nv, E(t, l, 5));
+                    if (last && sc.a.taps) sc.a.taps[(size_t)l * sc.D + row] = nv;
+                };
+                gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, F, wg * kNW + wave, sc.nwg * kNW, xs, x16,
+                                                 prep, epi);
+                __syncthreads();
+                if (tid == 0) put(X(sc.DONE) + par * sc.nwg + wg, 0.0f, E(t, l, 5));
+            }
+        }
+        // ---- output_norm + lm_head + greedy argmax
+        if (sc.a.lm_every || last) {
+            const int D = sc.D;
+            float wr[NWR];
+            load_norm(sc.a.out_norm, D, wr);
+            const int groups[3] = {(int)((sc.a.out.N + 1) / 2), 0, 0};
+            auto seg = [&](int, int) -> const DevMat& { return sc.a.out; };
+            auto prep = [&]() {
+                const int Lm = sc.L - 1;
+                gather<kGD, kGW>(X(sc.XA) + (Lm & 1) * D, D, E(t, Lm, 5), xr, X(sc.DONE) + (Lm & 1) * sc.nwg, sc.nwg,
+                                 E(t, Lm, 5), sc.a.ctl);
+                stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TO>::kNeedSums, red);
+                if (last && sc.a.taps && wg == 0)
+                    for (int j = tid; j < D; j += kT) sc.a.taps[(size_t)sc.L * D + j] = xs[j];
+            };
+            u64 best = 0;
+            auto epi = [&](int, int row, float v, float, float) {
+                if (last && sc.a.logits) sc.a.logits[row] = v;
+                const u64 k = argmax_key(v, row);
+                best = k > best ? k : best;
+            };
+            gemv_phase<TO, 2, GEMV_LOGITS, 2>(1, groups, seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
+                                              prep, epi);
+            best = wave_max_u64(best);
+            if (lane == 0) wbest[wave] = best;
+            __syncthreads();
+            if (tid == 0) {
+                u64 b = wbest[0];
+                for (int i = 1; i < kNW; ++i) b = wbest[i] > b ? wbest[i] : b;
+                u64* bw = X(sc.BEST) + (t & 1) * 2 * sc.nwg + 2 * wg;
+                put(bw, __uint_as_float((uint32_t)(b >> 32)), E(t, sc.L, 6));
+                put(bw + 1, __uint_as_float((uint32_t)b), E(t, sc.L, 6));
+            }
+            __syncthreads();
+        }
+    }
+    // workgroup 0 folds the last token's keys and advances the control block
+    if (wg == 0) {
+        const int t = n_tokens - 1;
+        float* kb = xs;
+        __syncthreads();
+        gather<kGW, 1>(X(sc.BEST) + (t & 1) * 2 * sc.nwg, 2 * sc.nwg, E(t, sc.L, 6), kb, nullptr, 0, 0, sc.a.ctl);
+        __syncthreads();
+        if (tid == 0) {
+            u64 b = 0;
+            for (int i = 0; i < sc.nwg; ++i) {
+                const u64 k = ((u64)__float_as_uint(kb[2 * i]) << 32) | (u64)__float_as_uint(kb[2 * i + 1]);
+                b = k > b ? k : b;
+            }
+            Ctl* ctl = sc.a.ctl;
+            ctl->key = b;
+            ctl->pos = sc.pos0 + n_tokens;
+            ctl->epoch = sc.e0 + (uint32_t)(n_tokens * sc.P);
+        }
+    }
+}
+
+}  // namespace step_detail
+}  // namespace tfk

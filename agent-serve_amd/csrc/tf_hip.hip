@@ -60,6 +60,14 @@ struct tf_hip_ctx {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     float last_ms = 0;
     int last_steps = 0;
+    bool last_was_step = false;
+    // persistent step kernel (k_step.hpp)
+    int path_opt = TF_HIP_PATH_STEP;  // requested decode path
+    int step_state = -1;              // -1 undecided, 0 graph path, 1 step kernel ready
+    int step_tl = -1, step_to = -1, n_wg = 0;
+    StepLayer* d_layers = nullptr;
+    unsigned long long* ex = nullptr;
+    uint32_t epoch = 0;               // exchange epochs consumed (mirrors ctl->epoch)
     std::string err;
 };
 
@@ -395,6 +403,100 @@ int ensure_graph(tf_hip_ctx* c) {
     return 0;
 }
 
+// Decides once, after every tensor is uploaded, whether the persistent step kernel runs
+// this model: one format for all layer matrices, the embedding in the lm_head's format, a
+// compiled (format, head size) combination, one attention split (max_seq <= 512: longer
+// caches keep the split attention of the graph path), cooperative launch, and inputs
+// within the kernel's per-thread capacities. Returns 1 (step kernel), 0 (graph) or < 0.
+int ensure_step(tf_hip_ctx* c) {
+    if (c->path_opt != TF_HIP_PATH_STEP) return 0;
+    if (c->step_state >= 0) return c->step_state;
+    int rc = check_ready(c);
+    if (rc) return rc;
+    c->step_state = 0;
+    const tf_hip_hparams& p = c->hp;
+    const int tl = mat(c, TF_HIP_SLOT_LAYER(0, TF_HIP_LAYER_Q)).type;
+    const int kinds[7] = {TF_HIP_LAYER_Q,    TF_HIP_LAYER_K,  TF_HIP_LAYER_V,   TF_HIP_LAYER_O,
+                          TF_HIP_LAYER_GATE, TF_HIP_LAYER_UP, TF_HIP_LAYER_DOWN};
+    for (int l = 0; l < p.n_layer; ++l)
+        for (int k : kinds)
+            if (mat(c, TF_HIP_SLOT_LAYER(l, k)).type != tl) return 0;
+    const DevMat& out = output_mat(c);
+    if (mat(c, TF_HIP_SLOT_TOKEN_EMBD).type != out.type || !step_supported(tl, out.type, p.head_dim)) return 0;
+    if (c->S != 1) return 0;
+    int coop = 0;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device) != hipSuccess || !coop) return 0;
+    const int n_wg = device_cu_count();
+    const int n_rep = p.n_head / p.n_kv_head;
+    if (n_wg < 2 * p.n_kv_head || p.n_embd + n_wg > 4096 || p.n_ff > 10240 || 2 * n_wg > 1024 ||
+        (n_rep + 2) * p.head_dim > 4096 || p.n_head * p.head_dim > 4096)
+        return 0;
+    std::vector<StepLayer> tab((size_t)p.n_layer);
+    for (int l = 0; l < p.n_layer; ++l) {
+        auto M = [&](int k) -> const DevMat& { return mat(c, TF_HIP_SLOT_LAYER(l, k)); };
+        auto V = [&](int k) { return vec(c, TF_HIP_SLOT_LAYER(l, k)); };
+        StepLayer& t = tab[(size_t)l];
+        t.wq = M(TF_HIP_LAYER_Q);
+        t.wk = M(TF_HIP_LAYER_K);
+        t.wv = M(TF_HIP_LAYER_V);
+        t.wo = M(TF_HIP_LAYER_O);
+        t.wg = M(TF_HIP_LAYER_GATE);
+        t.wu = M(TF_HIP_LAYER_UP);
+        t.wd = M(TF_HIP_LAYER_DOWN);
+        t.attn_norm = V(TF_HIP_LAYER_ATTN_NORM);
+        t.ffn_norm = V(TF_HIP_LAYER_FFN_NORM);
+        t.bq = V(TF_HIP_LAYER_BQ);
+        t.bk = V(TF_HIP_LAYER_BK);
+        t.bv = V(TF_HIP_LAYER_BV);
+        t.kc = c->kc + (size_t)l * c->kv_layer;
+        t.vc = c->vc + (size_t)l * c->kv_layer;
+    }
+    const size_t words = step_exchange_words(p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, n_wg);
+    if ((rc = dalloc(c, &c->d_layers, tab.size() * sizeof(StepLayer))) || (rc = dalloc(c, &c->ex, words * 8)))
+        return rc;
+    HIPCHK(c, hipMemcpy(c->d_layers, tab.data(), tab.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemset(c->ex, 0, words * 8));  // epoch 0 is never used
+    c->step_tl = tl;
+    c->step_to = out.type;
+    c->n_wg = n_wg;
+    c->step_state = 1;
+    return 1;
+}
+
+// n tokens through the persistent step kernel, from position c->pos.
+int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
+    const tf_hip_hparams& p = c->hp;
+    StepArgs a{};
+    a.layers = c->d_layers;
+    a.embd = mat(c, TF_HIP_SLOT_TOKEN_EMBD);
+    a.out = output_mat(c);
+    a.out_norm = vec(c, TF_HIP_SLOT_OUTPUT_NORM);
+    a.rope_cos = c->rope_cos;
+    a.rope_sin = c->rope_sin;
+    a.ex = c->ex;
+    a.ctl = c->ctl;
+    a.hist = c->hist;
+    a.logits = c->logits;
+    a.taps = c->taps;
+    a.n_layer = p.n_layer;
+    a.D = p.n_embd;
+    a.F = p.n_ff;
+    a.H = p.n_head;
+    a.G = p.n_kv_head;
+    a.hd = p.head_dim;
+    a.max_seq = p.max_seq;
+    a.layout = p.kv_layout;
+    a.eps = p.rms_eps;
+    a.n_tokens = n;
+    a.greedy = greedy;
+    a.lm_every = lm_every;
+    a.att_start = att_start;
+    const hipError_t e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);
+    if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("step kernel launch: ") + hipGetErrorString(e));
+    c->epoch += (uint32_t)(n * (6 * p.n_layer + 8));
+    return 0;
+}
+
 // Writes att_start and mode of the device control block.
 int set_ctl(tf_hip_ctx* c, int att_start, int mode) {
     c->ctl_host->att_start = att_start;
@@ -409,6 +511,7 @@ int finish_step_outputs(tf_hip_ctx* c, float* logits, int32_t* argmax) {
         HIPCHK(c, hipMemcpyAsync(logits, c->logits, (size_t)c->hp.n_vocab * 4, hipMemcpyDeviceToHost, c->st));
     HIPCHK(c, hipMemcpyAsync(c->ctl_host, c->ctl, sizeof(Ctl), hipMemcpyDeviceToHost, c->st));
     HIPCHK(c, hipStreamSynchronize(c->st));
+    if (c->ctl_host->err == 2) return fail(c, TF_HIP_EDEVICE, "step kernel: an exchange wait timed out");
     if (c->ctl_host->err) return fail(c, TF_HIP_EDEVICE, "device reported an invalid token");
     if (c->ctl_host->pos != c->pos) return fail(c, TF_HIP_EDEVICE, "device position out of step");
     if (argmax) *argmax = key_to_index(c->ctl_host->key);
@@ -528,6 +631,7 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
             int rc = dalloc(c, &d, (size_t)want * 4);
             if (rc) return rc;
             c->vecs[(size_t)slot] = d;
+            c->step_state = -1;
         }
         c->vec_len[(size_t)slot] = want;
         HIPCHK(c, hipMemcpy(d, host, (size_t)want * 4, hipMemcpyHostToDevice));
@@ -574,6 +678,7 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
     }
     c->allocs.insert(c->allocs.end(), owned.begin(), owned.end());
     c->mats[(size_t)slot] = m;  // a re-upload leaves the old streams allocated until destroy
+    c->step_state = -1;         // the step kernel's layer table is rebuilt
     return 0;
 }
 
@@ -596,6 +701,7 @@ int tf_hip_reset(tf_hip_ctx* c) {
     c->pos = 0;
     c->have_logits = false;
     std::memset(c->ctl_host, 0, sizeof(Ctl));
+    c->ctl_host->epoch = c->epoch;  // exchange words keep old epochs: never reuse one
     HIPCHK(c, hipMemcpyAsync(c->ctl, c->ctl_host, sizeof(Ctl), hipMemcpyHostToDevice, c->st));
     HIPCHK(c, hipMemsetAsync(c->kc, 0, c->kv_layer * c->hp.n_layer * 4, c->st));
     HIPCHK(c, hipMemsetAsync(c->vc, 0, c->kv_layer * c->hp.n_layer * 4, c->st));
@@ -611,12 +717,18 @@ int tf_hip_decode(tf_hip_ctx* c, int32_t token, float* logits, int32_t* argmax) 
     if (c->pos + 1 > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
     if (token < 0 || token >= mat(c, TF_HIP_SLOT_TOKEN_EMBD).N)
         return fail(c, TF_HIP_ERANGE, "token " + std::to_string(token) + " out of range");
-    int rc = ensure_graph(c);
+    const int use_step = ensure_step(c);
+    if (use_step < 0) return use_step;
+    int rc = use_step ? 0 : ensure_graph(c);
     if (rc) return rc;
     c->tok_host[0] = token;
     HIPCHK(c, hipMemcpyAsync(c->hist + c->pos, c->tok_host, 4, hipMemcpyHostToDevice, c->st));
     if ((rc = set_ctl(c, 0, 0))) return rc;
-    HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    if (use_step) {
+        if ((rc = run_step(c, 1, 0, 1, 0))) return rc;
+    } else {
+        HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    }
     c->pos += 1;
     rc = finish_step_outputs(c, logits, argmax);
     if (rc) return rc;
@@ -633,12 +745,18 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
     for (int i = 0; i < n; ++i)
         if (tokens[i] < 0 || tokens[i] >= V)
             return fail(c, TF_HIP_ERANGE, "token " + std::to_string(tokens[i]) + " out of range");
-    int rc = ensure_graph(c);
+    const int use_step = ensure_step(c);
+    if (use_step < 0) return use_step;
+    int rc = use_step ? 0 : ensure_graph(c);
     if (rc) return rc;
     std::memcpy(c->tok_host, tokens, (size_t)n * 4);
     HIPCHK(c, hipMemcpyAsync(c->hist + c->pos, c->tok_host, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
     if ((rc = set_ctl(c, c->pos, 0))) return rc;
-    for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    if (use_step) {
+        if ((rc = run_step(c, n, 0, 0, c->pos))) return rc;
+    } else {
+        for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    }
     c->pos += n;
     rc = finish_step_outputs(c, logits, argmax);
     if (rc) return rc;
@@ -652,12 +770,18 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     HIPCHK(c, hipSetDevice(c->device));
     if (!c->have_logits) return fail(c, TF_HIP_ESTATE, "generate needs a prior prefill or decode");
     if (c->pos + n > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
-    int rc = ensure_graph(c);
+    const int use_step = ensure_step(c);
+    if (use_step < 0) return use_step;
+    int rc = use_step ? 0 : ensure_graph(c);
     if (rc) return rc;
     const int pos0 = c->pos;
     if ((rc = set_ctl(c, 0, 1))) return rc;
     HIPCHK(c, hipEventRecord(c->ev0, c->st));
-    for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    if (use_step) {
+        if ((rc = run_step(c, n, 1, 1, 0))) return rc;
+    } else {
+        for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    }
     HIPCHK(c, hipEventRecord(c->ev1, c->st));
     HIPCHK(c, hipMemcpyAsync(c->tok_host, c->hist + pos0, (size_t)n * 4, hipMemcpyDeviceToHost, c->st));
     c->pos += n;
@@ -665,8 +789,23 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     if (rc) return rc;
     std::memcpy(out, c->tok_host, (size_t)n * 4);
     HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
-    c->last_steps = n;
+    c->last_steps = use_step ? 1 : n;
+    c->last_was_step = use_step == 1;
     return 0;
+}
+
+int tf_hip_set_decode_path(tf_hip_ctx* c, int32_t path) {
+    if (!c || (path != TF_HIP_PATH_GRAPH && path != TF_HIP_PATH_STEP)) return TF_HIP_EINVAL;
+    c->path_opt = path;
+    if (path == TF_HIP_PATH_STEP && c->step_state == 0) c->step_state = -1;  // decide again
+    return 0;
+}
+
+int tf_hip_get_decode_path(tf_hip_ctx* c) {
+    if (!c) return TF_HIP_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    const int s = ensure_step(c);
+    return s < 0 ? s : (s ? TF_HIP_PATH_STEP : TF_HIP_PATH_GRAPH);
 }
 
 int tf_hip_get_layer_act(tf_hip_ctx* c, int32_t layer, float* out) {
@@ -702,7 +841,7 @@ int tf_hip_last_timing(const tf_hip_ctx* c, float* total_ms, float* kernel_ms, i
     if (total_ms) *total_ms = c->last_ms;
     if (kernel_ms) *kernel_ms = c->last_ms;
     if (launches) *launches = c->last_steps;
-    if (name && name_len > 0) std::snprintf(name, (size_t)name_len, "%s", "decode_graph");
+    if (name && name_len > 0) std::snprintf(name, (size_t)name_len, "%s", c->last_was_step ? "k_step" : "decode_graph");
     return 0;
 }
 

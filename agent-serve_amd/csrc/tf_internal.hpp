@@ -42,7 +42,7 @@ struct Ctl {
     int32_t pos;         // position of the token this step consumes
     int32_t att_start;   // first cache position attention covers (prefill semantics)
     int32_t mode;        // 0: token staged by the host at hist[pos], 1: argmax of the previous step
-    int32_t spare;
+    uint32_t epoch;      // exchange epochs used so far by the persistent step kernel
     unsigned long long key;  // argmax key of the last lm_head: (ordered value << 32) | ~index
     int32_t last_token;
     int32_t err;
@@ -107,6 +107,47 @@ struct AttnArgs {
 // launch) when max_seq <= 512.
 constexpr int kAttnMinChunk = 64;
 int attn_splits(int max_seq);
+
+// ---------------------------------------------------------------- persistent step kernel
+constexpr int kStepThreads = 512;  // one workgroup per CU, 8 waves
+
+// One layer's weights and cache for the persistent step kernel (an array of these lives
+// in device memory).
+struct StepLayer {
+    DevMat wq, wk, wv, wo, wg, wu, wd;
+    const float* attn_norm;
+    const float* ffn_norm;
+    const float* bq;  // F32 biases or nullptr
+    const float* bk;
+    const float* bv;
+    float* kc;        // this layer's K and V cache
+    float* vc;
+};
+
+struct StepArgs {
+    const StepLayer* layers;
+    DevMat embd, out;          // token embedding, lm_head
+    const float* out_norm;
+    const float* rope_cos;     // [max_seq][hd/2]
+    const float* rope_sin;
+    unsigned long long* ex;    // exchange words, see step_exchange_words()
+    Ctl* ctl;
+    int32_t* hist;             // token per position
+    float* logits;             // last token's logits, or nullptr
+    float* taps;               // [L+1][D] per-layer outputs of the last token, or nullptr
+    int n_layer, D, F, H, G, hd, max_seq, layout;
+    float eps;
+    int n_tokens;              // tokens this launch runs
+    int greedy;                // 0: tokens from hist (prefill, decode); 1: each token is the previous argmax
+    int lm_every;              // 1: lm_head for every token; 0: for the last one only (prefill)
+    int att_start;             // first cache position attention covers (0, or the prefill chunk's start)
+};
+
+size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg);
+size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg);
+// true when the model's formats and head size have a compiled step kernel.
+bool step_supported(int type_layers, int type_out, int hd);
+hipError_t launch_step(const StepArgs& a, int type_layers, int type_out, int n_wg, hipStream_t st);
 
 // Launchers (k_*.hip).
 hipError_t launch_gemv(const GemvArgs& a, int rows_per_wave, hipStream_t st);

@@ -109,6 +109,19 @@ int tf_hip_decode(tf_hip_ctx* ctx, int32_t token, float* logits, int32_t* argmax
  * decode(tok). Requires a prior prefill or decode. No host round trip between steps. */
 int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
 
+/* Decode path of prefill / decode / generate. TF_HIP_PATH_STEP (the default): one
+ * persistent cooperative kernel per call runs every token of the call, for models whose
+ * layer matrices share one format the kernel is compiled for (others, and caches longer
+ * than 512 positions, use the graph path). TF_HIP_PATH_GRAPH: one captured graph of
+ * per-layer kernels replayed per token. Both compute the same function; neither has a
+ * counterpart in the reference (a backend choice below Model::decode, model.cpp:197-208).
+ * tf_hip_get_decode_path returns the path the next call will take (needs every tensor
+ * uploaded). */
+#define TF_HIP_PATH_GRAPH 0
+#define TF_HIP_PATH_STEP 1
+int tf_hip_set_decode_path(tf_hip_ctx* ctx, int32_t path);
+int tf_hip_get_decode_path(tf_hip_ctx* ctx);
+
 /* Model::reset (model.cpp:80-83): n_pos = 0 and the KV cache cleared. */
 int tf_hip_reset(tf_hip_ctx* ctx);
 int tf_hip_get_pos(const tf_hip_ctx* ctx);

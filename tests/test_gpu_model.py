@@ -13,15 +13,50 @@ from gpu_util import model_parity
 pytestmark = pytest.mark.gpu
 
 SMALL = ["tiny_f32", "tiny_q8", "tiny_mixq4", "tiny_qwen", "small_q8"]
+GRAPH, STEP = 0, 1  # HipModel.PATH_GRAPH, HipModel.PATH_STEP
 
 
+@pytest.mark.parametrize("path", [GRAPH, STEP], ids=["graph", "step"])
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("preset", SMALL)
-def test_small_models(pkg, gguf, preset, layout):
+def test_small_models(pkg, gguf, preset, layout, path):
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"], 6, info["n_vocab"])
-    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 16, 64, layout)
-    print(f"{preset} layout {layout}: ids {ids} logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 16, 64, layout, decode_path=path)
+    print(f"{preset} layout {layout} path {path}: ids {ids} logits {worst:.2e} taps {worst_tap:.2e} "
+          f"margin {margin:.3e}")
+
+
+@pytest.mark.parametrize("preset,want", [("tiny_q8", STEP), ("tiny_f32", STEP), ("small_q8", STEP),
+                                         ("tiny_mixq4", GRAPH)])
+def test_decode_path_selection(pkg, gguf, preset, want):
+    """The persistent step kernel runs models whose layer matrices share a compiled format;
+    mixed-format models keep the graph path; PATH_GRAPH forces the graph."""
+    hip = pkg.HipModel(gguf(preset), max_seq=64)
+    assert hip.decode_path() == want
+    hip.set_decode_path(GRAPH)
+    assert hip.decode_path() == GRAPH
+    hip.close()
+    big = pkg.HipModel(gguf("tiny_q8"), max_seq=1024)  # split attention: graph path
+    assert big.decode_path() == GRAPH
+    big.close()
+
+
+def test_step_and_graph_agree(pkg, gguf):
+    """Both decode paths give the same greedy stream and logits within 1e-5 from the same state."""
+    path = gguf("small_q8")
+    prompt = np.array([3, 99, 7, 1200, 5, 42, 8], np.int32)
+    out = []
+    for p in (GRAPH, STEP):
+        hip = pkg.HipModel(path, max_seq=64)
+        hip.set_decode_path(p)
+        lp, _ = hip.prefill(prompt)
+        ids = hip.generate(12)
+        ld, _ = hip.decode(int(ids[-1]))
+        out.append((lp, ids, ld))
+        hip.close()
+    assert np.array_equal(out[0][1], out[1][1])
+    assert rel_err(out[0][0], out[1][0]) <= 1e-5 and rel_err(out[0][2], out[1][2]) <= 1e-5
 
 
 def test_reference_ci_prompts(pkg, gguf):
