@@ -7,6 +7,37 @@
 
 namespace tfk {
 
+// Global-memory view of a pointer. A pointer read from LDS (or anywhere the compiler
+// cannot trace to a kernel argument) is generic, and its accesses compile to FLAT
+// instructions, which count in lgkmcnt as well as vmcnt: every later wait for an LDS
+// access would also wait for them. Accessing through this view keeps them global.
+#define TF_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ TF_GLOBAL T* gptr(T* p) {
+    return (TF_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ const TF_GLOBAL T* gptr(const T* p) {
+    return (const TF_GLOBAL T*)p;
+}
+// 8- and 16-byte global loads (HIP's vector classes cannot be assigned from an
+// address-space-qualified lvalue; clang's native vectors can).
+typedef unsigned int tf_u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int tf_u32x4 __attribute__((ext_vector_type(4)));
+typedef float tf_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 gload_u2(const void* p) {
+    const tf_u32x2 v = *(const TF_GLOBAL tf_u32x2*)p;
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint4 gload_u4(const void* p) {
+    const tf_u32x4 v = *(const TF_GLOBAL tf_u32x4*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 gload_f4(const void* p) {
+    const tf_f32x4 v = *(const TF_GLOBAL tf_f32x4*)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // IEEE half bits -> float (v_cvt_f32_f16: exact for every half value).
 __device__ __forceinline__ float h2f(uint32_t bits16) {
     _Float16 v;

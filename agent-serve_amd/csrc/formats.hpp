@@ -40,8 +40,8 @@ struct Fmt<TF_HIP_TYPE_Q8_0> {
     }
     __device__ static Raw load(const RowPtr& p, int s) {
         Raw w;
-        w.q = *(const uint4*)(p.q + 16 * (int64_t)s);
-        w.d = *(const uint16_t*)(p.s + 2 * (s >> 1));
+        w.q = gload_u4(p.q + 16 * (int64_t)s);
+        w.d = *gptr((const uint16_t*)(p.s + 2 * (s >> 1)));
         return w;
     }
     __device__ static float dot(const Raw& w, const float* xs, const float* x16, int s) {
@@ -83,8 +83,8 @@ struct Fmt<TF_HIP_TYPE_Q4_0> {
     }
     __device__ static Raw load(const RowPtr& p, int s) {
         Raw w;
-        w.q = *(const uint4*)(p.q + 16 * (int64_t)s);
-        w.d = *(const uint16_t*)(p.s + 2 * s);
+        w.q = gload_u4(p.q + 16 * (int64_t)s);
+        w.d = *gptr((const uint16_t*)(p.s + 2 * s));
         return w;
     }
     // sum x (n - 8): nibble n of byte j is element j (low) or j + 16 (high)
@@ -133,8 +133,8 @@ struct Fmt<TF_HIP_TYPE_Q4_1> {
     }
     __device__ static Raw load(const RowPtr& p, int s) {
         Raw w;
-        w.q = *(const uint4*)(p.q + 16 * (int64_t)s);
-        w.dm = *(const uint32_t*)(p.s + 4 * s);
+        w.q = gload_u4(p.q + 16 * (int64_t)s);
+        w.dm = *gptr((const uint32_t*)(p.s + 4 * s));
         return w;
     }
     // sum x (n d + m) = d sum x n + m sum x
@@ -188,10 +188,10 @@ struct Fmt<TF_HIP_TYPE_Q6_K> {
     }
     __device__ static Raw load(const RowPtr& p, int s) {
         Raw w;
-        w.lo = *(const uint4*)(p.q + 16 * (int64_t)s);
-        w.hi = *(const uint2*)(p.q2 + 8 * (int64_t)s);
-        w.sc = *(const uint16_t*)(p.s + 2 * s);
-        w.d = *(const uint16_t*)(p.s2 + 2 * (s >> 3));
+        w.lo = gload_u4(p.q + 16 * (int64_t)s);
+        w.hi = gload_u2(p.q2 + 8 * (int64_t)s);
+        w.sc = *gptr((const uint16_t*)(p.s + 2 * s));
+        w.d = *gptr((const uint16_t*)(p.s2 + 2 * (s >> 3)));
         return w;
     }
     // 6-bit values u = lo4 | hi2 << 4 of elements 4i..4i+3 (first) and 16+4i.. (second)
@@ -247,7 +247,7 @@ struct Fmt<TF_HIP_TYPE_F16> {
         uint4 q;
     };
     __device__ static RowPtr row(const DevMat& m, int64_t r) { return {m.q + r * m.K * 2, nullptr, nullptr, nullptr}; }
-    __device__ static Raw load(const RowPtr& p, int s) { return {*(const uint4*)(p.q + 16 * (int64_t)s)}; }
+    __device__ static Raw load(const RowPtr& p, int s) { return {gload_u4(p.q + 16 * (int64_t)s)}; }
     __device__ static float dot(const Raw& w, const float* xs, const float*, int s) {
         const float4* x4 = (const float4*)(xs + 8 * s);
         const float4 a = x4[0], b = x4[1];
@@ -277,7 +277,7 @@ struct Fmt<TF_HIP_TYPE_F32> {
         float4 q;
     };
     __device__ static RowPtr row(const DevMat& m, int64_t r) { return {m.q + r * m.K * 4, nullptr, nullptr, nullptr}; }
-    __device__ static Raw load(const RowPtr& p, int s) { return {*(const float4*)(p.q + 16 * (int64_t)s)}; }
+    __device__ static Raw load(const RowPtr& p, int s) { return {gload_f4(p.q + 16 * (int64_t)s)}; }
     __device__ static float dot(const Raw& w, const float* xs, const float*, int s) {
         const float4 a = *(const float4*)(xs + 4 * s);
         float t = a.x * w.q.x;

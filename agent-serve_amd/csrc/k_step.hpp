@@ -40,14 +40,16 @@ constexpr int kErrToken = 1;
 constexpr int kErrTimeout = 2;
 
 __device__ __forceinline__ void put(u64* p, float v, uint32_t e) {
-    __hip_atomic_store(p, ((u64)e << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gptr(p), ((u64)e << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ u64 get(u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ u64 get(u64* p) {
+    return __hip_atomic_load(gptr(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ int get_err(Ctl* c) {
-    return __hip_atomic_load(&c->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(gptr(&c->err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void set_err(Ctl* c, int v) {
-    __hip_atomic_store(&c->err, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gptr(&c->err), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Waits for the na words pa[0..na) of epoch ea and writes their values to da (LDS), and
@@ -151,7 +153,7 @@ __device__ __forceinline__ void load_norm(const float* w, int K, float (&wr)[NWR
 #pragma unroll
     for (int i = 0; i < NWR; ++i) {
         const int j = threadIdx.x + i * kT;
-        wr[i] = w ? w[j < K ? j : K - 1] : 1.0f;
+        wr[i] = w ? *gptr(w + (j < K ? j : K - 1)) : 1.0f;
     }
 }
 
@@ -204,7 +206,7 @@ __device__ __forceinline__ void gemv_phase(int nseg, const int (&groups)[3], Seg
             const float* bias = bias_of(si);
             int re = row0 + (lane < R ? lane : R - 1);
             re = re < N ? re : N - 1;
-            extra = bias ? bias[re] : 0.0f;
+            extra = bias ? *gptr(bias + re) : 0.0f;
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -282,7 +284,7 @@ __device__ __forceinline__ int64_t kv_at(int layout, int G, int max_seq, int hd,
 // head g for every token of a launch, so the rows it stores are the ones it later reads
 // on this CU.
 template <int HDM>
-__device__ __noinline__ void attn_head(const StepArgs& a, const StepLayer& ly, int g, int pos, int start, float* qkv, float* sm,
+__device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly, int g, int pos, int start, float* qkv, float* sm,
                           float* out) {
     constexpr int kTV = (kTile * HDM / 4 + kT - 1) / kT;  // float4 of a K (or V) tile per thread
     constexpr int kPairs = (kMaxRep * HDM + kT - 1) / kT;  // (head, dim) pairs of P.V per thread
@@ -297,8 +299,8 @@ __device__ __noinline__ void attn_head(const StepArgs& a, const StepLayer& ly, i
     float* vt = kt + kTile * ks;      // [kTile][hd]
     float* pr = vt + kTile * hd;      // [n_rep][kTile]
     float* st = pr + n_rep * kTile;   // [n_rep][3]
-    const float* cs = a.rope_cos + (int64_t)pos * d2;
-    const float* sn = a.rope_sin + (int64_t)pos * d2;
+    const TF_GLOBAL float* cs = gptr(a.rope_cos + (int64_t)pos * d2);
+    const TF_GLOBAL float* sn = gptr(a.rope_sin + (int64_t)pos * d2);
     const int p1 = pos + 1;
 
     auto load_tile = [&](int t0, float4 (&kr)[kTV], float4 (&vr)[kTV]) {
@@ -309,8 +311,8 @@ __device__ __noinline__ void attn_head(const StepArgs& a, const StepLayer& ly, i
             i = i < tn * hd4 ? i : tn * hd4 - 1;
             const int j = i / hd4, c = i % hd4;
             const int64_t o = kv_at(a.layout, a.G, a.max_seq, hd, g, t0 + j) + 4 * c;
-            kr[k] = *(const float4*)(ly.kc + o);
-            vr[k] = *(const float4*)(ly.vc + o);
+            kr[k] = gload_f4(ly.kc + o);
+            vr[k] = gload_f4(ly.vc + o);
         }
     };
     float4 kr_a[kTV], vr_a[kTV], kr_b[kTV], vr_b[kTV];
@@ -331,8 +333,8 @@ __device__ __noinline__ void attn_head(const StepArgs& a, const StepLayer& ly, i
     {
         const int64_t o = kv_at(a.layout, a.G, a.max_seq, hd, g, pos);
         for (int j = tid; j < hd; j += kT) {
-            ly.kc[o + j] = kn[j];
-            ly.vc[o + j] = vn[j];
+            *gptr(ly.kc + o + j) = kn[j];
+            *gptr(ly.vc + o + j) = vn[j];
         }
     }
     const float scale = 1.0f / sqrtf((float)hd);
@@ -546,18 +548,18 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                             } else {
                                 gather<1, kGW>(nullptr, 0, 0, nullptr, X(sc.DONE) + ((sc.L - 1) & 1) * sc.nwg, sc.nwg,
                                                E(t - 1, sc.L - 1, 5), a.ctl);
-                                tok = a.hist[pos];
+                                tok = *gptr(a.hist + pos);
                             }
                         } else {
-                            tok = a.greedy ? key_to_index(sc.key0) : a.hist[pos];
+                            tok = a.greedy ? key_to_index(sc.key0) : *gptr(a.hist + pos);
                         }
                         if (tok < 0 || tok >= (int)a.embd.N) {
                             if (tid == 0) set_err(a.ctl, kErrToken);
                             tok = 0;
                         }
                         if (wg == 0 && tid == 0) {
-                            a.hist[pos] = tok;
-                            a.ctl->last_token = tok;
+                            *gptr(a.hist + pos) = tok;
+                            *gptr(&a.ctl->last_token) = tok;
                         }
                         // dequant_row of the token's row (model.cpp:199)
                         const RowPtr rp = FE::row(a.embd, tok);
@@ -645,7 +647,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 auto epi = [&](int, int row, float v, float, float) {
                     const float nv = xr[row] + v;
                     put(X(sc.XA) + par * sc.D + row, nv, E(t, l, 5));
-                    if (last && sc.a.taps) sc.a.taps[(size_t)l * sc.D + row] = nv;
+                    if (last && sc.a.taps) *gptr(sc.a.taps + (size_t)l * sc.D + row) = nv;
                 };
                 gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, F, wg * kNW + wave, sc.nwg * kNW, xs, x16,
                                                  prep, epi);
@@ -666,11 +668,11 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                                  E(t, Lm, 5), sc.a.ctl);
                 stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TO>::kNeedSums, red);
                 if (last && sc.a.taps && wg == 0)
-                    for (int j = tid; j < D; j += kT) sc.a.taps[(size_t)sc.L * D + j] = xs[j];
+                    for (int j = tid; j < D; j += kT) *gptr(sc.a.taps + (size_t)sc.L * D + j) = xs[j];
             };
             u64 best = 0;
             auto epi = [&](int, int row, float v, float, float) {
-                if (last && sc.a.logits) sc.a.logits[row] = v;
+                if (last && sc.a.logits) *gptr(sc.a.logits + row) = v;
                 const u64 k = argmax_key(v, row);
                 best = k > best ? k : best;
             };
@@ -702,7 +704,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 const u64 k = ((u64)__float_as_uint(kb[2 * i]) << 32) | (u64)__float_as_uint(kb[2 * i + 1]);
                 b = k > b ? k : b;
             }
-            Ctl* ctl = sc.a.ctl;
+            TF_GLOBAL Ctl* ctl = gptr(sc.a.ctl);
             ctl->key = b;
             ctl->pos = sc.pos0 + n_tokens;
             ctl->epoch = sc.e0 + (uint32_t)(n_tokens * sc.P);
