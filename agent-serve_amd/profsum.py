@@ -1,6 +1,7 @@
 """Summaries of rocprofv3 CSV output for the decode step, as short text.
 
     python3 agent-serve_amd/profsum.py trace <kernel_stats.csv> [--steps K]
+    python3 agent-serve_amd/profsum.py steps <kernel_trace.csv>
     python3 agent-serve_amd/profsum.py traffic <fetch counter_collection.csv> <write counter_collection.csv>
         --copy-bytes N
 
@@ -33,10 +34,20 @@ def decode_class(name: str) -> str:
     if m:
         mode, u = int(m.group(3)), int(m.group(4))
         return {0: "qkv_gemv", 2: "gateup_gemv", 3: "lmhead_gemv"}.get(mode, "down_gemv" if u == 4 else "wo_gemv")
-    for key, cls in (("k_attn_decode", "attention"), ("k_attn_combine", "attention"), ("k_embed", "embed")):
+    for key, cls in (("k_attn_decode", "attention"), ("k_attn_combine", "attention"), ("k_embed", "embed"),
+                     ("k_step", "k_step")):
         if key in name:
             return cls
     return short(name).replace(" ", "")
+
+
+def step_dispatches(trace_csv: str) -> list[float]:
+    """Durations (us) of each k_step dispatch, in launch order."""
+    out = []
+    for r in csv.DictReader(open(trace_csv)):
+        if "k_step" in r["Kernel_Name"]:
+            out.append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return out
 
 
 def trace(path: str, steps: int | None) -> None:
@@ -48,11 +59,13 @@ def trace(path: str, steps: int | None) -> None:
 
 
 def counter_means(path: str, counter: str) -> dict[str, tuple[int, float]]:
+    """Mean counter value per kernel name; for k_step (one launch per call, calls of
+    different token counts) the largest dispatch, which is the longest generate call."""
     acc: dict[str, list[float]] = collections.defaultdict(list)
     for r in csv.DictReader(open(path)):
         if r["Counter_Name"] == counter:
             acc[r["Kernel_Name"]].append(float(r["Counter_Value"]))
-    return {k: (len(v), sum(v) / len(v)) for k, v in acc.items()}
+    return {k: (len(v), max(v) if "k_step" in k else sum(v) / len(v)) for k, v in acc.items()}
 
 
 def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> None:
@@ -79,13 +92,16 @@ def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> None:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["trace", "traffic"])
+    ap.add_argument("what", choices=["trace", "traffic", "steps"])
     ap.add_argument("files", nargs="+")
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     a = ap.parse_args()
     if a.what == "trace":
         trace(a.files[0], a.steps)
+    elif a.what == "steps":
+        for i, d in enumerate(step_dispatches(a.files[0])):
+            print(f"k_step dispatch {i}: {d:9.1f} us")
     else:
         traffic(a.files[0], a.files[1], a.copy_bytes)
     return 0
