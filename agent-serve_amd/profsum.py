@@ -2,6 +2,7 @@
 
     python3 agent-serve_amd/profsum.py trace <kernel_stats.csv> [--steps K]
     python3 agent-serve_amd/profsum.py steps <kernel_trace.csv>
+    python3 agent-serve_amd/profsum.py stepcounters <fetch counter_collection.csv> <write counter_collection.csv>
     python3 agent-serve_amd/profsum.py traffic <fetch counter_collection.csv> <write counter_collection.csv>
         --copy-bytes N
 
@@ -50,6 +51,22 @@ def step_dispatches(trace_csv: str) -> list[float]:
     return out
 
 
+def step_counters(fetch_csv: str, write_csv: str) -> None:
+    """HBM bytes per decode token of the persistent step kernel from a run of the CLI
+    (one launch for the prompt, then one launch per decoded token): the median over the
+    single-token launches, FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0 (the factors
+    k_copy_stream of a known size gives these counters on MI355X)."""
+    def vals(p, c):
+        return [float(r["Counter_Value"]) for r in csv.DictReader(open(p))
+                if r["Counter_Name"] == c and "k_step" in r["Kernel_Name"]]
+    f, w = vals(fetch_csv, "FETCH_SIZE"), vals(write_csv, "WRITE_SIZE")
+    fm, wm = sorted(f[1:])[len(f[1:]) // 2], sorted(w[1:])[len(w[1:]) // 2]
+    print(f"k_step dispatches: {len(f)} (first = prompt, then one per decoded token)")
+    print(f"decode dispatches: FETCH_SIZE median {fm:.0f} KiB (min {min(f[1:]):.0f}, max {max(f[1:]):.0f}), "
+          f"WRITE_SIZE median {wm:.0f} KiB (min {min(w[1:]):.0f}, max {max(w[1:]):.0f})")
+    print(f"traffic_bytes_per_token k_step {fm * 1024 * 2.0 + wm * 1024 * 1.0:.0f}")
+
+
 def trace(path: str, steps: int | None) -> None:
     rows = list(csv.DictReader(open(path)))
     print(f"{'kernel':60s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'total_ms':>9s}")
@@ -92,13 +109,15 @@ def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> None:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["trace", "traffic", "steps"])
+    ap.add_argument("what", choices=["trace", "traffic", "steps", "stepcounters"])
     ap.add_argument("files", nargs="+")
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     a = ap.parse_args()
     if a.what == "trace":
         trace(a.files[0], a.steps)
+    elif a.what == "stepcounters":
+        step_counters(a.files[0], a.files[1])
     elif a.what == "steps":
         for i, d in enumerate(step_dispatches(a.files[0])):
             print(f"k_step dispatch {i}: {d:9.1f} us")

@@ -37,6 +37,7 @@ MAX_SEQ = 512
 HBM_PEAK_GBS = 8000.0
 COPY_CALIB_BYTES = 1 << 30
 TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_llama1b_q8_0_traffic.txt"
+STEP_TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_llama1b_q8_0_step_kernel_traffic.txt"
 PUBLISHED_CPU_TOK_S = 10.74  # reference --stage v2, Llama-3.2-1B Q8_0, Ryzen 5 4600H
 
 
@@ -54,17 +55,20 @@ def model_path() -> str:
     return str(d / f"{PRESET}-seed42.gguf")
 
 
-def measured_traffic(kernel_class: str):
-    """HBM bytes per launch of `kernel_class` from the committed counter summary (two
-    rocprofv3 --pmc runs of this script, FETCH_SIZE then WRITE_SIZE, scaled by the
-    counters of the known-size copy it runs); None when no summary covers it."""
-    try:
-        for line in TRAFFIC_SUMMARY.read_text().splitlines():
-            f = line.split()
-            if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == kernel_class:
-                return int(float(f[2]))
-    except OSError:
-        pass
+def measured_traffic(kernel_class: str, tokens_per_launch: int = 1):
+    """HBM bytes per launch of `kernel_class` from the committed counter summaries (two
+    rocprofv3 --pmc runs, FETCH_SIZE then WRITE_SIZE, scaled by the counters of a
+    known-size copy); the step kernel's summary is per decoded token. None when no
+    summary covers it."""
+    for path, key, mult in ((TRAFFIC_SUMMARY, "traffic_bytes_per_launch", 1),
+                            (STEP_TRAFFIC_SUMMARY, "traffic_bytes_per_token", tokens_per_launch)):
+        try:
+            for line in path.read_text().splitlines():
+                f = line.split()
+                if len(f) == 3 and f[0] == key and f[1] == kernel_class:
+                    return int(float(f[2]) * mult)
+        except OSError:
+            pass
     return None
 
 
@@ -193,7 +197,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(dom),
+            "traffic": measured_traffic(dom, K if dom == "k_step" else 1),
             "kernel": dom,
             "launches": d_launch,
             "bytes_per_launch": round(d_bytes / d_launch),
