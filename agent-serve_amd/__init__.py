@@ -57,6 +57,8 @@ def hip_lib() -> C.CDLL:
         "tf_hip_reset": (C.c_int, [vp]),
         "tf_hip_set_decode_path": (C.c_int, [vp, C.c_int32]),
         "tf_hip_get_decode_path": (C.c_int, [vp]),
+        "tf_hip_set_prefill_path": (C.c_int, [vp, C.c_int32]),
+        "tf_hip_get_prefill_path": (C.c_int, [vp]),
         "tf_hip_get_pos": (C.c_int, [vp]),
         "tf_hip_get_layer_act": (C.c_int, [vp, C.c_int32, _f32p]),
         "tf_hip_read_kv": (C.c_int, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _f32p]),
@@ -68,6 +70,8 @@ def hip_lib() -> C.CDLL:
         "tf_hip_rmsnorm": (C.c_int, [C.c_int, _f32p, _f32p, C.c_int32, C.c_int32, C.c_float, _f32p]),
         "tf_hip_attn_decode": (C.c_int, [C.c_int, _f32p, _f32p, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                          C.c_int32, C.c_int32, _f32p]),
+        "tf_hip_attn_prefill": (C.c_int, [C.c_int, _f32p, _f32p, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                          _f32p]),
         "tf_hip_argmax": (C.c_int, [C.c_int, _f32p, C.c_int32, _i32p]),
         "tf_hip_read_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p]),
         "tf_hip_copy_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p]),
@@ -251,6 +255,23 @@ class HipModel:
             raise RuntimeError(H.tf_hip_last_error(self._L.tfh_ctx(self._h)).decode())
         return rc
 
+    PREFILL_TOKENS, PREFILL_MFMA = 0, 1
+
+    def set_prefill_path(self, path: int):
+        """PREFILL_MFMA: prompts of two or more tokens on the matrix cores where the model
+        allows it (default); PREFILL_TOKENS: one prompt token at a time on the decode path."""
+        H = hip_lib()
+        rc = H.tf_hip_set_prefill_path(self._L.tfh_ctx(self._h), int(path))
+        if rc != 0:
+            raise RuntimeError(f"tf_hip_set_prefill_path({path}) failed: {rc}")
+
+    def prefill_path(self) -> int:
+        H = hip_lib()
+        rc = H.tf_hip_get_prefill_path(self._L.tfh_ctx(self._h))
+        if rc < 0:
+            raise RuntimeError(H.tf_hip_last_error(self._L.tfh_ctx(self._h)).decode())
+        return rc
+
     def layer_act(self, layer: int) -> np.ndarray:
         out = np.zeros(self.n_embd, np.float32)
         self._check(self._L.tfh_layer_act(self._h, layer, _f(out)))
@@ -334,6 +355,19 @@ def attn_decode(q: np.ndarray, k_rows: np.ndarray, v_rows: np.ndarray, max_seq: 
     out = np.zeros_like(q)
     _op(hip_lib().tf_hip_attn_decode(device, _f(q), _f(k_rows), _f(v_rows), n_heads, n_kv, hd, n_pos, max_seq,
                                      layout, _f(out)), "tf_hip_attn_decode")
+    return out
+
+
+def attn_prefill(q: np.ndarray, k: np.ndarray, v: np.ndarray, device: int = 0) -> np.ndarray:
+    """attn_prefill (attention.cpp:82-111): q [seq][n_heads][hd], k and v [seq][n_kv][hd]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    seq, n_heads, hd = q.shape
+    n_kv = k.shape[1]
+    out = np.zeros_like(q)
+    _op(hip_lib().tf_hip_attn_prefill(device, _f(q), _f(k), _f(v), seq, n_heads, n_kv, hd, _f(out)),
+        "tf_hip_attn_prefill")
     return out
 
 

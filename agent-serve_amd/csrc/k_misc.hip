@@ -38,6 +38,21 @@ __global__ __launch_bounds__(kBlock) void k_embed(const DevMat emb, float* x, Ct
     }
 }
 
+// dequant_row of each prompt token's embedding row (model.cpp:186): row i of x is
+// token tok[i] (tokens are range-checked by the host).
+template <int T>
+__global__ __launch_bounds__(kBlock) void k_embed_rows(const DevMat emb, const int32_t* tok, float* x, int D) {
+    using F = Fmt<T>;
+    const RowPtr rp = F::row(emb, tok[blockIdx.x]);
+    float* xr = x + (int64_t)blockIdx.x * D;
+    for (int s = threadIdx.x; s < D / F::E; s += kBlock) {
+        float v[F::E];
+        F::dequant(F::load(rp, s), v);
+#pragma unroll
+        for (int i = 0; i < F::E; i += 4) *(float4*)(xr + (int64_t)s * F::E + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+    }
+}
+
 template <int T>
 __global__ __launch_bounds__(kBlock) void k_dequant_rows(const DevMat m, int64_t row0, int64_t nrows, float* out) {
     using F = Fmt<T>;
@@ -188,6 +203,12 @@ int device_cu_count() {
 
 hipError_t launch_embed(const DevMat& emb, float* x, Ctl* ctl, int32_t* hist, int D, hipStream_t st) {
     TF_DISPATCH_TYPE(emb.type, hipLaunchKernelGGL((k_embed<T_>), dim3(1), dim3(kBlock), 0, st, emb, x, ctl, hist, D));
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const DevMat& emb, const int32_t* tok, int n, float* x, int D, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    TF_DISPATCH_TYPE(emb.type, hipLaunchKernelGGL((k_embed_rows<T_>), dim3(n), dim3(kBlock), 0, st, emb, tok, x, D));
     return hipGetLastError();
 }
 

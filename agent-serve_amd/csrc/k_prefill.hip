@@ -1,0 +1,525 @@
+// Prefill of prompt tokens on the matrix cores: Model::prefill and layer_prefill
+// (model.cpp:144-195) for a chunk of M tokens at once.
+//
+// k_pf_split     rmsnorm (layers.cpp:7-12) of each row, or the row as it is, scaled by
+//                a power of two and written as two fp16 planes hi + lo (the A operand)
+// k_pf_gemm_q8   matmul (matmul.cpp:64-73) of Q8_0 weights on v_mfma_f32_16x16x32_f16,
+//                epilogues: store (+ F32 bias, model.cpp:85-89), residual add
+//                (add_inplace, layers.cpp:21-23), silu(gate) * up (layers.cpp:14-19)
+// k_pf_rope_store apply_rope_many of q and k (attention.cpp:48-53) and KVCache::store
+//                (kvcache.cpp:31-36) of every row
+// k_pf_attn      causal GQA attention of the chunk (attn_prefill, attention.cpp:82-111)
+//                on v_mfma_f32_16x16x4_f32 with an online softmax
+//
+// Numerics. A Q8_0 weight q is an integer in [-128, 127] and exact in fp16; a
+// 32-element block's products with the fp16 pair (hi, lo) of an activation are exact
+// in the fp32 accumulator, and hi + lo carries 22 significant bits of the fp32
+// activation (24). Each block's two MFMAs start from zero and the block sum is scaled
+// by its fp16 d in fp32 (quant.cpp:266-321 scales block sums the same way), so the
+// result differs from the fp32 reference by summation order and the 2^-22 split, both
+// far inside the 1e-3 parity bound. Scaling rows by 2^e (max |x| in [2^14, 2^15))
+// keeps hi and lo in fp16 range and off its subnormals; the epilogue multiplies the
+// exact inverse back.
+#include "dev_common.hpp"
+#include "tf_internal.hpp"
+
+namespace tfk {
+
+namespace {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- activations -> fp16 pairs
+
+// One workgroup per row. Rows M..Mpad-1 are zeroed so the GEMM tiles past the last
+// token read zeros.
+__global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx, const float* w, float eps, int K,
+                                                     int M, uint16_t* xh, uint16_t* xl, float* rs) {
+    __shared__ double red_d[kWavesPerBlock];
+    __shared__ float red_f[kWavesPerBlock];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    h4_t* hh = (h4_t*)(xh + (int64_t)m * K);
+    h4_t* ll = (h4_t*)(xl + (int64_t)m * K);
+    const int K4 = K / 4;
+    if (m >= M) {
+        const h4_t z = {0, 0, 0, 0};
+        for (int k = tid; k < K4; k += kBlock) {
+            hh[k] = z;
+            ll[k] = z;
+        }
+        if (tid == 0) rs[m] = 0.0f;
+        return;
+    }
+    const float4* xr = (const float4*)(x + (int64_t)m * ldx);
+    const float4* wr = (const float4*)w;
+    float inv = 1.0f;
+    if (w) {
+        double ss = 0;
+        for (int k = tid; k < K4; k += kBlock) {
+            const float4 v = xr[k];
+            ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+        }
+        ss = wave_sum_d(ss);
+        if ((tid & 63) == 0) red_d[tid >> 6] = ss;
+        __syncthreads();
+        ss = (red_d[0] + red_d[1]) + (red_d[2] + red_d[3]);
+        inv = 1.0f / sqrtf((float)(ss / K) + eps);
+    }
+    auto val = [&](int k) {
+        float4 v = xr[k];
+        if (w) {
+            const float4 g = wr[k];
+            v = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+        }
+        return v;
+    };
+    float amax = 0.0f;
+    for (int k = tid; k < K4; k += kBlock) {
+        const float4 v = val(k);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    amax = wave_max(amax);
+    if ((tid & 63) == 0) red_f[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    int ex = 0;
+    (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
+    int e = amax > 0.0f ? 15 - ex : 0;
+    e = e < -100 ? -100 : (e > 100 ? 100 : e);
+    const float sc = ldexpf(1.0f, e);
+    if (tid == 0) rs[m] = ldexpf(1.0f, -e);
+    for (int k = tid; k < K4; k += kBlock) {
+        const float4 v = val(k);
+        const float t[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+        h4_t h, l;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h[j] = (_Float16)t[j];
+            l[j] = (_Float16)(t[j] - (float)h[j]);
+        }
+        hh[k] = h;
+        ll[k] = l;
+    }
+}
+
+// ---------------------------------------------------------------- Q8_0 GEMM
+
+// Eight offset-binary bytes (q + 128) -> the fp16 values q: 0x64XX is the half 1024 + XX,
+// and 1024 + XX - 1152 = q exactly.
+__device__ __forceinline__ h8_t q8_to_h8(uint2 w) {
+    const uint32_t p0 = (w.x & 0xFFu) | ((w.x & 0xFF00u) << 8) | 0x64006400u;
+    const uint32_t p1 = ((w.x >> 16) & 0xFFu) | ((w.x >> 8) & 0xFF0000u) | 0x64006400u;
+    const uint32_t p2 = (w.y & 0xFFu) | ((w.y & 0xFF00u) << 8) | 0x64006400u;
+    const uint32_t p3 = ((w.y >> 16) & 0xFFu) | ((w.y >> 8) & 0xFF0000u) | 0x64006400u;
+    const tf_u32x4 p = {p0, p1, p2, p3};
+    const h8_t off = {1152, 1152, 1152, 1152, 1152, 1152, 1152, 1152};
+    return __builtin_bit_cast(h8_t, p) - off;
+}
+
+// Field of the segment holding output subtile u (uniform per wave: scalar selects).
+#define PF_SEL(s, f) ((s) == 0 ? a.seg[0].f : ((s) == 1 ? a.seg[1].f : a.seg[2].f))
+
+// Workgroup: 4 waves as 2 (rows) x 2 (columns); a wave owns 32 rows x 4 column subtiles
+// of 16 (GEMV_SILU: 2 output subtiles, each a gate and an up subtile). Per 32-element
+// block and (row subtile, column subtile): two MFMAs (hi, lo) from zero, then
+// acc += d * block sum. Operands stream from L2 into registers, one stage of two
+// blocks ahead; every load is unconditional (indices clamped) so the compiler waits
+// only for the stage it consumes.
+template <int MODE>
+__global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous range
+    // of tiles, rows fastest, so the row tiles that share a weight tile share an L2.
+    int b = blockIdx.x;
+    {
+        const int q = (int)gridDim.x / 8;
+        if (b < 8 * q) b = (b % 8) * q + b / 8;
+    }
+    const int MT = a.Mpad / kPfTileM;
+    const int mt = b % MT, nt = b / MT;
+    const int m0 = mt * kPfTileM + (wave & 1) * 32;
+    const int wid = nt * 2 + (wave >> 1);
+    const int K = a.K, nblk = K / 32;
+    const int kq = 8 * (lane >> 4);  // this lane's 8 k of a 32-element block
+    const int l16 = lane & 15;
+
+    const uint8_t* qp[4];
+    const uint16_t* sp[4];
+    float* yp[4];
+    const float* bp[4];
+    int64_t ldy[4];
+    int col[4];
+    bool ok[4];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+        int u = MODE == GEMV_SILU ? wid * 2 + (ni & 1) : wid * 4 + ni;
+        ok[ni] = u < a.n_sub;
+        u = u < a.n_sub ? u : a.n_sub - 1;
+        const int s = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
+        const int c = (u - PF_SEL(s, sub0)) * 16 + l16;
+        const bool up = MODE == GEMV_SILU && ni >= 2;
+        const uint8_t* wq = up ? PF_SEL(s, w2.q) : PF_SEL(s, w.q);
+        const uint8_t* ws = up ? PF_SEL(s, w2.s) : PF_SEL(s, w.s);
+        qp[ni] = wq + (int64_t)c * K + kq;
+        sp[ni] = (const uint16_t*)ws + (int64_t)c * nblk;
+        yp[ni] = PF_SEL(s, y);
+        bp[ni] = PF_SEL(s, bias);
+        ldy[ni] = PF_SEL(s, ldy);
+        col[ni] = c;
+    }
+    const _Float16* ah_p[2];
+    const _Float16* al_p[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+        const int64_t r = m0 + 16 * mi + l16;
+        ah_p[mi] = (const _Float16*)a.xh + r * K + kq;
+        al_p[mi] = (const _Float16*)a.xl + r * K + kq;
+    }
+
+    f4_t acc[2][4];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+    struct Stage {
+        h8_t ah[2][2], al[2][2];  // [row subtile][block]
+        uint2 bq[4][2];           // [column subtile][block]
+        uint32_t d[4];            // the two blocks' fp16 scales
+    };
+    const int S = K / 64;
+    auto load = [&](int s, Stage& g) {
+        s = s < S ? s : S - 1;
+        const int k0 = s * 64;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                g.ah[mi][j] = *(const TF_GLOBAL h8_t*)(ah_p[mi] + k0 + 32 * j);
+                g.al[mi][j] = *(const TF_GLOBAL h8_t*)(al_p[mi] + k0 + 32 * j);
+            }
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) g.bq[ni][j] = gload_u2(qp[ni] + k0 + 32 * j);
+            g.d[ni] = *(const TF_GLOBAL uint32_t*)(sp[ni] + 2 * s);
+        }
+    };
+    auto compute = [&](const Stage& g) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            h8_t bh[4];
+            float dv[4];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                bh[ni] = q8_to_h8(g.bq[ni][j]);
+                dv[ni] = h2f(g.d[ni] >> (16 * j));
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    f4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], bh[ni], (f4_t){0.0f, 0.0f, 0.0f, 0.0f},
+                                                                   0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], bh[ni], t, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[mi][ni][r] = fmaf(dv[ni], t[r], acc[mi][ni][r]);
+                }
+        }
+    };
+    Stage s0, s1;
+    load(0, s0);
+    int s = 0;
+    for (; s + 2 <= S; s += 2) {
+        load(s + 1, s1);
+        compute(s0);
+        load(s + 2, s0);
+        compute(s1);
+    }
+    if (s < S) compute(s0);
+
+    // epilogue: lane holds rows m0 + 16 mi + 4 (lane / 16) + r of column col[ni]
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+        const int r0 = m0 + 16 * mi + 4 * (lane >> 4);
+        const float4 rsv = *(const float4*)(a.rs + r0);
+        const float rsa[4] = {rsv.x, rsv.y, rsv.z, rsv.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = r0 + r;
+            if (row >= a.M) continue;
+            if (MODE == GEMV_SILU) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    if (!ok[j]) continue;
+                    const float gv = acc[mi][j][r] * rsa[r];
+                    const float uv = acc[mi][j + 2][r] * rsa[r];
+                    yp[j][(int64_t)row * ldy[j] + col[j]] = (gv / (1.0f + expf(-gv))) * uv;
+                }
+            } else {
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    if (!ok[ni]) continue;
+                    const float v = acc[mi][ni][r] * rsa[r];
+                    float* p = yp[ni] + (int64_t)row * ldy[ni] + col[ni];
+                    if (MODE == GEMV_STORE) {
+                        *p = bp[ni] ? v + bp[ni][col[ni]] : v;
+                    } else {
+                        const float nv = *p + v;
+                        *p = nv;
+                        if (row == a.tap_row && a.tap) a.tap[col[ni]] = nv;
+                    }
+                }
+            }
+        }
+    }
+}
+
+#undef PF_SEL
+
+// ---------------------------------------------------------------- RoPE and KV store
+
+// Row i is position pos0 + i: q heads rotated in place, k heads rotated into the cache,
+// v heads copied into it (the same fmaf pattern as the decode path).
+__global__ __launch_bounds__(kBlock) void k_pf_rope_store(float* qkv, int64_t ld, int H, int G, int hd,
+                                                          const float* rope_cos, const float* rope_sin, int pos0,
+                                                          float* kc, float* vc, int layout, int max_seq) {
+    const int i = blockIdx.x, pos = pos0 + i, d2 = hd / 2;
+    float* q = qkv + (int64_t)i * ld;
+    const float* k = q + (int64_t)H * hd;
+    const float* v = k + (int64_t)G * hd;
+    const float* cs = rope_cos + (int64_t)pos * d2;
+    const float* sn = rope_sin + (int64_t)pos * d2;
+    for (int t = threadIdx.x; t < H * d2; t += kBlock) {
+        const int h = t / d2, j = t % d2;
+        float* qh = q + (int64_t)h * hd;
+        const float x0 = qh[j], x1 = qh[j + d2], c = cs[j], s = sn[j];
+        qh[j] = fmaf(x0, c, -(x1 * s));
+        qh[j + d2] = fmaf(x0, s, x1 * c);
+    }
+    for (int t = threadIdx.x; t < G * d2; t += kBlock) {
+        const int g = t / d2, j = t % d2;
+        const float* kh = k + (int64_t)g * hd;
+        const float x0 = kh[j], x1 = kh[j + d2], c = cs[j], s = sn[j];
+        float* o = kc + kv_offset(layout, G, max_seq, hd, g, pos);
+        o[j] = fmaf(x0, c, -(x1 * s));
+        o[j + d2] = fmaf(x0, s, x1 * c);
+    }
+    for (int t = threadIdx.x; t < G * hd; t += kBlock) {
+        const int g = t / hd, j = t % hd;
+        vc[kv_offset(layout, G, max_seq, hd, g, pos) + j] = v[(int64_t)g * hd + j];
+    }
+}
+
+// ---------------------------------------------------------------- causal attention
+
+// Workgroup: 16 consecutive queries of one kv head, one wave per query head of the
+// group. Per tile of 16 keys a wave computes S^T = K Q^T with HD/4 MFMAs (lane group
+// l/16 holds HD/4 consecutive dims of its key row and its query row), so a lane ends up
+// with 4 keys of query l%16; the softmax statistics of a query combine the 4 lanes
+// l%16 + 16 j. O^T = V^T P^T then takes P^T straight from those registers: MFMA r of a
+// tile feeds key 4 (l/16) + r, and V^T as one scalar per lane. Keys run from att_start to
+// the last query of the tile; keys past a query's position score -inf.
+template <int HD>
+__global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, const float* kc, const float* vc,
+                                                 int layout, int G, int max_seq, int n_rep, int n, int pos0,
+                                                 int att_start, float* out, int64_t ldo) {
+    constexpr int DQ = HD / 4;   // dims per lane group in S^T
+    constexpr int NT = HD / 16;  // output dim tiles
+    const int lane = threadIdx.x & 63, r_head = threadIdx.x >> 6;
+    const int qt = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest tiles first
+    const int g = blockIdx.y;
+    const int h = g * n_rep + r_head;
+    const int l16 = lane & 15, grp = lane >> 4;
+    const int qi = qt * 16 + l16;
+    const int qrow = qi < n ? qi : n - 1;
+    const int qpos = pos0 + qrow;
+    const int last = qt * 16 + 15 < n ? qt * 16 + 15 : n - 1;
+    const int k_hi = pos0 + last;  // last key any query of the tile sees
+    const float scale = 1.0f / sqrtf((float)HD);
+
+    float qv[DQ];
+    {
+        const float* qr = q + (int64_t)qrow * ldq + (int64_t)h * HD + grp * DQ;
+#pragma unroll
+        for (int s = 0; s < DQ; s += 4) {
+            const float4 t = gload_f4(qr + s);
+            qv[s] = t.x;
+            qv[s + 1] = t.y;
+            qv[s + 2] = t.z;
+            qv[s + 3] = t.w;
+        }
+    }
+    f4_t ot[NT];
+#pragma unroll
+    for (int d = 0; d < NT; ++d) ot[d] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    for (int kt = att_start; kt <= k_hi; kt += 16) {
+        // K rows: lane's key kt + l16, dims grp*DQ ..
+        float kv[DQ];
+        {
+            int key = kt + l16;
+            key = key <= k_hi ? key : k_hi;
+            const float* kr = kc + kv_offset(layout, G, max_seq, HD, g, key) + grp * DQ;
+#pragma unroll
+            for (int s = 0; s < DQ; s += 4) {
+                const float4 t = gload_f4(kr + s);
+                kv[s] = t.x;
+                kv[s + 1] = t.y;
+                kv[s + 2] = t.z;
+                kv[s + 3] = t.w;
+            }
+        }
+        // V scalars: MFMA r of dim tile d needs V[kt + 4 grp + r][16 d + l16]
+        float vv[4][NT];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            int key = kt + 4 * grp + r;
+            key = key <= k_hi ? key : k_hi;
+            const float* vr = vc + kv_offset(layout, G, max_seq, HD, g, key) + l16;
+#pragma unroll
+            for (int d = 0; d < NT; ++d) vv[r][d] = *gptr(vr + 16 * d);
+        }
+        f4_t st = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < DQ; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[s], qv[s], st, 0, 0, 0);
+        float p[4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = kt + 4 * grp + r;
+            p[r] = key <= qpos ? st[r] * scale : -INFINITY;
+            mt = fmaxf(mt, p[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = expf(m_run - m_new);  // 0 on the first tile
+        float ls = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = p[r] == -INFINITY ? 0.0f : expf(p[r] - m_new);
+            ls += p[r];
+        }
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        l_run = fmaf(l_run, alpha, ls);
+        m_run = m_new;
+#pragma unroll
+        for (int d = 0; d < NT; ++d) {
+            f4_t o = ot[d] * alpha;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r][d], p[r], o, 0, 0, 0);
+            ot[d] = o;
+        }
+    }
+    // lane holds O[query l16][dims 16 d + 4 grp + 0..3]; the 4 lanes of a query share l_run
+    if (qi < n) {
+        float* orow = out + (int64_t)qi * ldo + (int64_t)h * HD + 4 * grp;
+        const float il = 1.0f / l_run;
+#pragma unroll
+        for (int d = 0; d < NT; ++d)
+            *(float4*)(orow + 16 * d) = make_float4(ot[d][0] * il, ot[d][1] * il, ot[d][2] * il, ot[d][3] * il);
+    }
+}
+
+// The last prompt row becomes the decode input of the lm_head GEMV; the control block
+// then describes position pos_last, as after a decode step of that token.
+__global__ __launch_bounds__(kBlock) void k_pf_tail(Ctl* ctl, int pos_last, const int32_t* hist, const float* xrow,
+                                                    float* x, int D) {
+    for (int i = threadIdx.x; i < D; i += kBlock) x[i] = xrow[i];
+    if (threadIdx.x == 0) {
+        ctl->pos = pos_last;
+        ctl->key = 0ull;
+        ctl->last_token = hist[pos_last];
+    }
+}
+
+}  // namespace
+
+bool pf_gemm_supported(int type, int64_t K, int64_t N) {
+    return type == TF_HIP_TYPE_Q8_0 && K % 64 == 0 && N % 16 == 0 && K <= (1 << 20);
+}
+
+hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,
+                           uint16_t* xh, uint16_t* xl, float* rs, hipStream_t st) {
+    if (K % 4 != 0 || ldx % 4 != 0 || Mpad % kPfTileM != 0 || M > Mpad) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_split, dim3(Mpad), dim3(kBlock), 0, st, x, ldx, norm_w, eps, K, M, xh, xl, rs);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st) {
+    if (a.K % 64 != 0 || a.Mpad % kPfTileM != 0 || a.M > a.Mpad || a.M <= 0 || a.n_sub <= 0 || a.n_seg < 1 ||
+        a.n_seg > 3)
+        return hipErrorInvalidValue;
+    for (int s = 0; s < a.n_seg; ++s) {
+        const PfSeg& g = a.seg[s];
+        if (g.w.type != TF_HIP_TYPE_Q8_0 || g.w.K != a.K || g.w.N % 16 != 0 || !g.y) return hipErrorInvalidValue;
+        const int next = s + 1 < a.n_seg ? a.seg[s + 1].sub0 : a.n_sub;
+        if (next - g.sub0 != g.w.N / 16) return hipErrorInvalidValue;
+        if (a.mode == GEMV_SILU && (g.w2.type != TF_HIP_TYPE_Q8_0 || g.w2.K != a.K || g.w2.N != g.w.N))
+            return hipErrorInvalidValue;
+    }
+    if (a.seg[0].sub0 != 0 || (a.mode == GEMV_SILU && a.n_seg != 1)) return hipErrorInvalidValue;
+    const int per_wg = a.mode == GEMV_SILU ? 4 : 8;  // output subtiles per workgroup column
+    const int nt = (a.n_sub + per_wg - 1) / per_wg;
+    const dim3 grid((unsigned)(nt * (a.Mpad / kPfTileM)));
+    switch (a.mode) {
+        case GEMV_STORE: hipLaunchKernelGGL(k_pf_gemm_q8<GEMV_STORE>, grid, dim3(256), 0, st, a); break;
+        case GEMV_RESID: hipLaunchKernelGGL(k_pf_gemm_q8<GEMV_RESID>, grid, dim3(256), 0, st, a); break;
+        case GEMV_SILU: hipLaunchKernelGGL(k_pf_gemm_q8<GEMV_SILU>, grid, dim3(256), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_rope_store(float* qkv, int64_t ld, int n, int H, int G, int hd, const float* rope_cos,
+                                const float* rope_sin, int pos0, float* kc, float* vc, int layout, int max_seq,
+                                hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    if (pos0 < 0 || pos0 + n > max_seq || hd % 2 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_rope_store, dim3(n), dim3(kBlock), 0, st, qkv, ld, H, G, hd, rope_cos, rope_sin, pos0, kc,
+                       vc, layout, max_seq);
+    return hipGetLastError();
+}
+
+bool pf_attn_supported(int hd, int n_rep) {
+    return (hd == 32 || hd == 64 || hd == 128) && n_rep >= 1 && n_rep <= 8;
+}
+
+hipError_t launch_pf_attn(const float* q, int64_t ldq, const float* kc, const float* vc, int layout, int H, int G,
+                          int hd, int max_seq, int n, int pos0, int att_start, float* out, int64_t ldo,
+                          hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int n_rep = H / G;
+    if (H % G != 0 || !pf_attn_supported(hd, n_rep) || att_start < 0 || att_start > pos0 || pos0 + n > max_seq ||
+        ldq % 4 != 0 || ldo % 4 != 0)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((n + 15) / 16), (unsigned)G), block((unsigned)(64 * n_rep));
+    switch (hd) {
+        case 32:
+            hipLaunchKernelGGL(k_pf_attn<32>, grid, block, 0, st, q, ldq, kc, vc, layout, G, max_seq, n_rep, n, pos0,
+                               att_start, out, ldo);
+            break;
+        case 64:
+            hipLaunchKernelGGL(k_pf_attn<64>, grid, block, 0, st, q, ldq, kc, vc, layout, G, max_seq, n_rep, n, pos0,
+                               att_start, out, ldo);
+            break;
+        default:
+            hipLaunchKernelGGL(k_pf_attn<128>, grid, block, 0, st, q, ldq, kc, vc, layout, G, max_seq, n_rep, n, pos0,
+                               att_start, out, ldo);
+            break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_tail(Ctl* ctl, int pos_last, const int32_t* hist, const float* xrow, float* x, int D,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_pf_tail, dim3(1), dim3(kBlock), 0, st, ctl, pos_last, hist, xrow, x, D);
+    return hipGetLastError();
+}
+
+}  // namespace tfk

@@ -60,7 +60,7 @@ struct tf_hip_ctx {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     float last_ms = 0;
     int last_steps = 0;
-    bool last_was_step = false;
+    const char* last_name = "decode_graph";  // what the last timed call ran
     // persistent step kernel (k_step.hpp)
     int path_opt = TF_HIP_PATH_STEP;  // requested decode path
     int step_state = -1;              // -1 undecided, 0 graph path, 1 step kernel ready
@@ -68,6 +68,12 @@ struct tf_hip_ctx {
     StepLayer* d_layers = nullptr;
     unsigned long long* ex = nullptr;
     uint32_t epoch = 0;               // exchange epochs consumed (mirrors ctl->epoch)
+    // prefill on the matrix cores (k_prefill.hip)
+    int pf_opt = TF_HIP_PREFILL_MFMA;  // requested prefill path
+    int pf_state = -1;                 // -1 undecided, 0 per-token path, 1 matrix-core path ready
+    int pf_cap = 0;                    // rows per prefill chunk (multiple of kPfTileM)
+    float *px = nullptr, *pqkv = nullptr, *patt = nullptr, *ph = nullptr, *prs = nullptr;
+    uint16_t *pxh = nullptr, *pxl = nullptr;
     std::string err;
 };
 
@@ -259,6 +265,25 @@ struct Launcher {
     }
 };
 
+// Final rmsnorm and lm_head of c->x (model.cpp:189-193, 204-206): logits, the argmax
+// into ctl->key, the normed row into the last tap, and ctl->pos advanced by one.
+hipError_t launch_lm_head(tf_hip_ctx* c) {
+    const DevMat& wout = output_mat(c);
+    const int R = pick_rows(wout.N);
+    GemvArgs a;
+    a.type = wout.type;
+    a.K = c->hp.n_embd;
+    a.mode = GEMV_LOGITS;
+    a.x = c->x;
+    a.norm_w = vec(c, TF_HIP_SLOT_OUTPUT_NORM);
+    a.eps = c->hp.rms_eps;
+    a.norm_out = c->taps + (size_t)c->hp.n_layer * c->hp.n_embd;
+    a.ctl = c->ctl;
+    a.bump_pos = 1;
+    add_seg(a, wout, c->logits, nullptr, nullptr, R);
+    return launch_gemv(a, R, c->st);
+}
+
 // One decode step (model.cpp:197-208) on the context stream.
 // pos/att_start only size the profile's byte counts; the kernels read them from Ctl.
 hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof, int pos = 0, int att_start = 0) {
@@ -368,19 +393,7 @@ hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof, int pos = 0, int att_start = 
     }
     {
         const DevMat& wout = output_mat(c);
-        const int R = pick_rows(wout.N);
-        GemvArgs a;
-        a.type = wout.type;
-        a.K = D;
-        a.mode = GEMV_LOGITS;
-        a.x = c->x;
-        a.norm_w = vec(c, TF_HIP_SLOT_OUTPUT_NORM);
-        a.eps = hp.rms_eps;
-        a.norm_out = c->taps + (size_t)hp.n_layer * D;
-        a.ctl = c->ctl;
-        a.bump_pos = 1;
-        add_seg(a, wout, c->logits, nullptr, nullptr, R);
-        L.run(6, (double)wout.gguf_bytes, [&] { return launch_gemv(a, R, c->st); });
+        L.run(6, (double)wout.gguf_bytes, [&] { return launch_lm_head(c); });
     }
     return L.err;
 }
@@ -503,6 +516,132 @@ int set_ctl(tf_hip_ctx* c, int att_start, int mode) {
     c->ctl_host->mode = mode;
     HIPCHK(c, hipMemcpyAsync((char*)c->ctl + offsetof(Ctl, att_start), (char*)c->ctl_host + offsetof(Ctl, att_start),
                              2 * sizeof(int32_t), hipMemcpyHostToDevice, c->st));
+    return 0;
+}
+
+// Decides once, after every tensor is uploaded, whether prompts run on the matrix
+// cores: every layer matrix in a format k_pf_gemm handles with row lengths it tiles,
+// and a head size and GQA ratio k_pf_attn handles. Allocates the chunk buffers.
+// Returns 1 (matrix cores), 0 (per-token path) or < 0.
+int ensure_pf(tf_hip_ctx* c) {
+    if (c->pf_opt != TF_HIP_PREFILL_MFMA) return 0;
+    if (c->pf_state >= 0) return c->pf_state;
+    int rc = check_ready(c);
+    if (rc) return rc;
+    c->pf_state = 0;
+    const tf_hip_hparams& p = c->hp;
+    for (int l = 0; l < p.n_layer; ++l) {
+        auto M = [&](int k) -> const DevMat& { return mat(c, TF_HIP_SLOT_LAYER(l, k)); };
+        const int kinds[7] = {TF_HIP_LAYER_Q,    TF_HIP_LAYER_K,  TF_HIP_LAYER_V,   TF_HIP_LAYER_O,
+                              TF_HIP_LAYER_GATE, TF_HIP_LAYER_UP, TF_HIP_LAYER_DOWN};
+        for (int k : kinds)
+            if (!pf_gemm_supported(M(k).type, M(k).K, M(k).N)) return 0;
+    }
+    if (!pf_attn_supported(p.head_dim, p.n_head / p.n_kv_head)) return 0;
+    if (!c->px) {
+        const int cap = std::min((p.max_seq + kPfTileM - 1) / kPfTileM * kPfTileM, kPfChunk);
+        const size_t D = (size_t)p.n_embd, F = (size_t)p.n_ff, NQ = (size_t)c->H + 2 * (size_t)c->KVd;
+        const size_t kmax = std::max({D, F, (size_t)c->H});
+        if ((rc = dalloc(c, &c->px, cap * D * 4)) || (rc = dalloc(c, &c->pqkv, cap * NQ * 4)) ||
+            (rc = dalloc(c, &c->patt, cap * (size_t)c->H * 4)) || (rc = dalloc(c, &c->ph, cap * F * 4)) ||
+            (rc = dalloc(c, &c->prs, (size_t)cap * 4)) || (rc = dalloc(c, &c->pxh, cap * kmax * 2)) ||
+            (rc = dalloc(c, &c->pxl, cap * kmax * 2)))
+            return rc;
+        c->pf_cap = cap;
+    }
+    c->pf_state = 1;
+    return 1;
+}
+
+// n prompt tokens, staged at hist[c->pos ..], through the matrix-core layers in chunks
+// of pf_cap rows; attention of every chunk covers the prompt from c->pos (the reference
+// attends within the prefill call only, attention.cpp:82-111). Ends with the lm_head of
+// the last row; the per-layer taps hold that row.
+int prefill_mfma(tf_hip_ctx* c, int n) {
+    const tf_hip_hparams& p = c->hp;
+    const int D = p.n_embd, F = p.n_ff, Hd = c->H, KVd = c->KVd, NQ = Hd + 2 * KVd;
+    const int start = c->pos;
+    hipError_t e = hipSuccess;
+    auto chk = [&](hipError_t r) {
+        if (e == hipSuccess) e = r;
+    };
+    int nc = 0;
+    for (int c0 = 0; c0 < n && e == hipSuccess; c0 += nc) {
+        nc = std::min(c->pf_cap, n - c0);
+        const int Mpad = (nc + kPfTileM - 1) / kPfTileM * kPfTileM;
+        const int pos0 = start + c0;
+        const bool last = c0 + nc == n;
+        chk(launch_embed_rows(mat(c, TF_HIP_SLOT_TOKEN_EMBD), c->hist + pos0, nc, c->px, D, c->st));
+        auto base = [&](int K) {
+            PfGemmArgs a;
+            a.xh = c->pxh;
+            a.xl = c->pxl;
+            a.rs = c->prs;
+            a.K = K;
+            a.M = nc;
+            a.Mpad = Mpad;
+            return a;
+        };
+        auto seg = [](PfGemmArgs& a, const DevMat& w, float* y, int64_t ldy, const float* bias) {
+            PfSeg& s = a.seg[a.n_seg++];
+            s.w = w;
+            s.y = y;
+            s.ldy = ldy;
+            s.bias = bias;
+            s.sub0 = a.n_sub;
+            a.n_sub += (int)(w.N / 16);
+        };
+        for (int l = 0; l < p.n_layer && e == hipSuccess; ++l) {
+            auto M = [&](int k) -> const DevMat& { return mat(c, TF_HIP_SLOT_LAYER(l, k)); };
+            auto V = [&](int k) { return vec(c, TF_HIP_SLOT_LAYER(l, k)); };
+            float* kc = c->kc + (size_t)l * c->kv_layer;
+            float* vc = c->vc + (size_t)l * c->kv_layer;
+            chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_ATTN_NORM), p.rms_eps, D, nc, Mpad, c->pxh, c->pxl, c->prs,
+                                c->st));
+            {
+                PfGemmArgs a = base(D);
+                a.mode = GEMV_STORE;
+                seg(a, M(TF_HIP_LAYER_Q), c->pqkv, NQ, V(TF_HIP_LAYER_BQ));
+                seg(a, M(TF_HIP_LAYER_K), c->pqkv + Hd, NQ, V(TF_HIP_LAYER_BK));
+                seg(a, M(TF_HIP_LAYER_V), c->pqkv + Hd + KVd, NQ, V(TF_HIP_LAYER_BV));
+                chk(launch_pf_gemm(a, c->st));
+            }
+            chk(launch_pf_rope_store(c->pqkv, NQ, nc, p.n_head, p.n_kv_head, p.head_dim, c->rope_cos, c->rope_sin,
+                                     pos0, kc, vc, p.kv_layout, p.max_seq, c->st));
+            chk(launch_pf_attn(c->pqkv, NQ, kc, vc, p.kv_layout, p.n_head, p.n_kv_head, p.head_dim, p.max_seq, nc,
+                               pos0, start, c->patt, Hd, c->st));
+            chk(launch_pf_split(c->patt, Hd, nullptr, 0.0f, Hd, nc, Mpad, c->pxh, c->pxl, c->prs, c->st));
+            {
+                PfGemmArgs a = base(Hd);
+                a.mode = GEMV_RESID;
+                seg(a, M(TF_HIP_LAYER_O), c->px, D, nullptr);
+                chk(launch_pf_gemm(a, c->st));
+            }
+            chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_FFN_NORM), p.rms_eps, D, nc, Mpad, c->pxh, c->pxl, c->prs,
+                                c->st));
+            {
+                PfGemmArgs a = base(D);
+                a.mode = GEMV_SILU;
+                seg(a, M(TF_HIP_LAYER_GATE), c->ph, F, nullptr);
+                a.seg[0].w2 = M(TF_HIP_LAYER_UP);
+                chk(launch_pf_gemm(a, c->st));
+            }
+            chk(launch_pf_split(c->ph, F, nullptr, 0.0f, F, nc, Mpad, c->pxh, c->pxl, c->prs, c->st));
+            {
+                PfGemmArgs a = base(F);
+                a.mode = GEMV_RESID;
+                seg(a, M(TF_HIP_LAYER_DOWN), c->px, D, nullptr);
+                if (last) {
+                    a.tap = c->taps + (size_t)l * D;
+                    a.tap_row = nc - 1;
+                }
+                chk(launch_pf_gemm(a, c->st));
+            }
+        }
+    }
+    chk(launch_pf_tail(c->ctl, start + n - 1, c->hist, c->px + (size_t)(nc - 1) * D, c->x, D, c->st));
+    chk(launch_lm_head(c));
+    if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("prefill launch: ") + hipGetErrorString(e));
     return 0;
 }
 
@@ -632,6 +771,7 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
             if (rc) return rc;
             c->vecs[(size_t)slot] = d;
             c->step_state = -1;
+            c->pf_state = -1;
         }
         c->vec_len[(size_t)slot] = want;
         HIPCHK(c, hipMemcpy(d, host, (size_t)want * 4, hipMemcpyHostToDevice));
@@ -679,6 +819,7 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
     c->allocs.insert(c->allocs.end(), owned.begin(), owned.end());
     c->mats[(size_t)slot] = m;  // a re-upload leaves the old streams allocated until destroy
     c->step_state = -1;         // the step kernel's layer table is rebuilt
+    c->pf_state = -1;
     return 0;
 }
 
@@ -745,21 +886,30 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
     for (int i = 0; i < n; ++i)
         if (tokens[i] < 0 || tokens[i] >= V)
             return fail(c, TF_HIP_ERANGE, "token " + std::to_string(tokens[i]) + " out of range");
-    const int use_step = ensure_step(c);
+    const int use_pf = n >= 2 ? ensure_pf(c) : 0;
+    if (use_pf < 0) return use_pf;
+    const int use_step = use_pf ? 0 : ensure_step(c);
     if (use_step < 0) return use_step;
-    int rc = use_step ? 0 : ensure_graph(c);
+    int rc = (use_pf || use_step) ? 0 : ensure_graph(c);
     if (rc) return rc;
     std::memcpy(c->tok_host, tokens, (size_t)n * 4);
     HIPCHK(c, hipMemcpyAsync(c->hist + c->pos, c->tok_host, (size_t)n * 4, hipMemcpyHostToDevice, c->st));
     if ((rc = set_ctl(c, c->pos, 0))) return rc;
-    if (use_step) {
+    HIPCHK(c, hipEventRecord(c->ev0, c->st));
+    if (use_pf) {
+        if ((rc = prefill_mfma(c, n))) return rc;
+    } else if (use_step) {
         if ((rc = run_step(c, n, 0, 0, c->pos))) return rc;
     } else {
         for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
     }
+    HIPCHK(c, hipEventRecord(c->ev1, c->st));
     c->pos += n;
     rc = finish_step_outputs(c, logits, argmax);
     if (rc) return rc;
+    HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
+    c->last_steps = use_pf ? 1 : (use_step ? 1 : n);
+    c->last_name = use_pf ? "prefill_mfma" : (use_step ? "k_step" : "decode_graph");
     c->have_logits = true;
     return 0;
 }
@@ -790,7 +940,7 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     std::memcpy(out, c->tok_host, (size_t)n * 4);
     HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
     c->last_steps = use_step ? 1 : n;
-    c->last_was_step = use_step == 1;
+    c->last_name = use_step == 1 ? "k_step" : "decode_graph";
     return 0;
 }
 
@@ -799,6 +949,20 @@ int tf_hip_set_decode_path(tf_hip_ctx* c, int32_t path) {
     c->path_opt = path;
     if (path == TF_HIP_PATH_STEP && c->step_state == 0) c->step_state = -1;  // decide again
     return 0;
+}
+
+int tf_hip_set_prefill_path(tf_hip_ctx* c, int32_t path) {
+    if (!c || (path != TF_HIP_PREFILL_TOKENS && path != TF_HIP_PREFILL_MFMA)) return TF_HIP_EINVAL;
+    c->pf_opt = path;
+    if (path == TF_HIP_PREFILL_MFMA && c->pf_state == 0) c->pf_state = -1;
+    return 0;
+}
+
+int tf_hip_get_prefill_path(tf_hip_ctx* c) {
+    if (!c) return TF_HIP_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    const int s = ensure_pf(c);
+    return s < 0 ? s : (s ? TF_HIP_PREFILL_MFMA : TF_HIP_PREFILL_TOKENS);
 }
 
 int tf_hip_get_decode_path(tf_hip_ctx* c) {
@@ -841,7 +1005,7 @@ int tf_hip_last_timing(const tf_hip_ctx* c, float* total_ms, float* kernel_ms, i
     if (total_ms) *total_ms = c->last_ms;
     if (kernel_ms) *kernel_ms = c->last_ms;
     if (launches) *launches = c->last_steps;
-    if (name && name_len > 0) std::snprintf(name, (size_t)name_len, "%s", c->last_was_step ? "k_step" : "decode_graph");
+    if (name && name_len > 0) std::snprintf(name, (size_t)name_len, "%s", c->last_name);
     return 0;
 }
 
@@ -966,6 +1130,33 @@ int tf_hip_matmul(int device, int t, const void* w, int64_t ne0, int64_t ne1, co
     OPCHK(s.alloc(&dx, (size_t)n_rows_x * ne0 * 4));
     OPCHK(s.alloc(&dy, (size_t)n_rows_x * ne1 * 4));
     OPCHK(hipMemcpy(dx, x, (size_t)n_rows_x * ne0 * 4, hipMemcpyHostToDevice));
+    if (n_rows_x >= 2 && pf_gemm_supported(t, ne0, ne1)) {
+        // several rows: the prefill GEMM on the matrix cores
+        const int Mpad = (n_rows_x + kPfTileM - 1) / kPfTileM * kPfTileM;
+        uint16_t *xh, *xl;
+        float* rs;
+        OPCHK(s.alloc(&xh, (size_t)Mpad * ne0 * 2));
+        OPCHK(s.alloc(&xl, (size_t)Mpad * ne0 * 2));
+        OPCHK(s.alloc(&rs, (size_t)Mpad * 4));
+        OPCHK(launch_pf_split(dx, ne0, nullptr, 0.0f, (int)ne0, n_rows_x, Mpad, xh, xl, rs, s.st));
+        PfGemmArgs a;
+        a.xh = xh;
+        a.xl = xl;
+        a.rs = rs;
+        a.K = (int)ne0;
+        a.M = n_rows_x;
+        a.Mpad = Mpad;
+        a.mode = GEMV_STORE;
+        a.n_seg = 1;
+        a.seg[0].w = m;
+        a.seg[0].y = dy;
+        a.seg[0].ldy = ne1;
+        a.n_sub = (int)(ne1 / 16);
+        OPCHK(launch_pf_gemm(a, s.st));
+        OPCHK(hipMemcpyAsync(y, dy, (size_t)n_rows_x * ne1 * 4, hipMemcpyDeviceToHost, s.st));
+        OPCHK(hipStreamSynchronize(s.st));
+        return 0;
+    }
     const int R = pick_rows(ne1);
     for (int i = 0; i < n_rows_x; ++i) {
         GemvArgs a;
@@ -994,6 +1185,31 @@ int tf_hip_rmsnorm(int device, const float* x, const float* w, int32_t n, int32_
     OPCHK(hipMemcpy(dw, w, (size_t)n * 4, hipMemcpyHostToDevice));
     OPCHK(launch_rmsnorm_rows(dx, dw, n, rows, eps, dout, s.st));
     OPCHK(hipMemcpyAsync(out, dout, (size_t)n * rows * 4, hipMemcpyDeviceToHost, s.st));
+    OPCHK(hipStreamSynchronize(s.st));
+    return 0;
+}
+
+int tf_hip_attn_prefill(int device, const float* q, const float* k, const float* v, int32_t seq, int32_t n_heads,
+                        int32_t n_kv, int32_t hd, float* out) {
+    if (!q || !k || !v || !out || seq <= 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv ||
+        !pf_attn_supported(hd, n_heads / n_kv))
+        return TF_HIP_EINVAL;
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    const size_t nq = (size_t)seq * n_heads * hd, nk = (size_t)seq * n_kv * hd;
+    float *dq, *dk, *dv, *dout;
+    OPCHK(s.alloc(&dq, nq * 4));
+    OPCHK(s.alloc(&dk, nk * 4));
+    OPCHK(s.alloc(&dv, nk * 4));
+    OPCHK(s.alloc(&dout, nq * 4));
+    OPCHK(hipMemcpy(dq, q, nq * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemcpy(dk, k, nk * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemcpy(dv, v, nk * 4, hipMemcpyHostToDevice));
+    // k and v rows [seq][n_kv][hd] are a sequence-major cache of seq positions
+    OPCHK(launch_pf_attn(dq, (int64_t)n_heads * hd, dk, dv, TF_HIP_KV_SEQ_MAJOR, n_heads, n_kv, hd, seq, seq, 0, 0,
+                         dout, (int64_t)n_heads * hd, s.st));
+    OPCHK(hipMemcpyAsync(out, dout, nq * 4, hipMemcpyDeviceToHost, s.st));
     OPCHK(hipStreamSynchronize(s.st));
     return 0;
 }

@@ -143,6 +143,57 @@ struct StepArgs {
     int att_start;             // first cache position attention covers (0, or the prefill chunk's start)
 };
 
+// ---------------------------------------------------------------- prefill on the matrix cores
+// Rows (tokens) of a prefill GEMM workgroup tile; activation buffers are padded to it.
+constexpr int kPfTileM = 64;
+// Rows per prefill chunk: longer prompts run in chunks whose attention covers the
+// prompt so far through the cache.
+constexpr int kPfChunk = 2048;
+
+__host__ __device__ inline int64_t kv_offset(int layout, int G, int max_seq, int hd, int g, int p) {
+    return layout == TF_HIP_KV_HEAD_MAJOR ? ((int64_t)g * max_seq + p) * hd : ((int64_t)p * G + g) * hd;
+}
+
+// One weight matrix of a prefill GEMM and where its output columns go.
+struct PfSeg {
+    DevMat w;                     // weight (gate for GEMV_SILU)
+    DevMat w2;                    // up matrix for GEMV_SILU
+    float* y = nullptr;           // output rows of ldy floats
+    int64_t ldy = 0;
+    const float* bias = nullptr;  // F32 bias added to the output (GEMV_STORE)
+    int sub0 = 0;                 // first 16-column output subtile of this segment
+};
+
+// C[M x N] = A[M x K] . W^T over the matrix cores. A arrives as two fp16 planes whose
+// sum is each row times a power of two (rs holds the inverse), see launch_pf_split.
+struct PfGemmArgs {
+    const uint16_t* xh = nullptr;  // [Mpad][K] fp16 high part
+    const uint16_t* xl = nullptr;  // [Mpad][K] fp16 low part
+    const float* rs = nullptr;     // [Mpad] row scales
+    int K = 0, M = 0, Mpad = 0;
+    PfSeg seg[3];
+    int n_seg = 0;
+    int n_sub = 0;                 // 16-column output subtiles over all segments
+    int mode = GEMV_STORE;         // GEMV_STORE, GEMV_RESID or GEMV_SILU
+    float* tap = nullptr;          // GEMV_RESID: copy of output row tap_row
+    int tap_row = -1;
+};
+
+bool pf_gemm_supported(int type, int64_t K, int64_t N);
+hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,
+                           uint16_t* xh, uint16_t* xl, float* rs, hipStream_t st);
+hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st);
+hipError_t launch_embed_rows(const DevMat& emb, const int32_t* tok, int n, float* x, int D, hipStream_t st);
+hipError_t launch_pf_rope_store(float* qkv, int64_t ld, int n, int H, int G, int hd, const float* rope_cos,
+                                const float* rope_sin, int pos0, float* kc, float* vc, int layout, int max_seq,
+                                hipStream_t st);
+bool pf_attn_supported(int hd, int n_rep);
+hipError_t launch_pf_attn(const float* q, int64_t ldq, const float* kc, const float* vc, int layout, int H, int G,
+                          int hd, int max_seq, int n, int pos0, int att_start, float* out, int64_t ldo,
+                          hipStream_t st);
+hipError_t launch_pf_tail(Ctl* ctl, int pos_last, const int32_t* hist, const float* xrow, float* x, int D,
+                          hipStream_t st);
+
 size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg);
 size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg);
 // true when the model's formats and head size have a compiled step kernel.

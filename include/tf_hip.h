@@ -122,6 +122,18 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
 int tf_hip_set_decode_path(tf_hip_ctx* ctx, int32_t path);
 int tf_hip_get_decode_path(tf_hip_ctx* ctx);
 
+/* Prefill path (no counterpart in the reference, whose layer_prefill is the one
+ * path, model.cpp:144-195): TF_HIP_PREFILL_MFMA runs a prompt of two or more tokens
+ * through the matrix-core GEMMs and the causal chunk attention when every layer
+ * matrix is Q8_0 with row lengths divisible by 64 and output lengths by 16 and the head
+ * size is 32, 64 or 128 (the default); otherwise, and under TF_HIP_PREFILL_TOKENS,
+ * prompt tokens run one at a time through the decode path with attention limited to
+ * the prompt. get returns the path a prompt would take (or < 0 on error). */
+#define TF_HIP_PREFILL_TOKENS 0
+#define TF_HIP_PREFILL_MFMA 1
+int tf_hip_set_prefill_path(tf_hip_ctx* ctx, int32_t path);
+int tf_hip_get_prefill_path(tf_hip_ctx* ctx);
+
 /* Model::reset (model.cpp:80-83): n_pos = 0 and the KV cache cleared. */
 int tf_hip_reset(tf_hip_ctx* ctx);
 int tf_hip_get_pos(const tf_hip_ctx* ctx);
@@ -134,9 +146,10 @@ int tf_hip_get_layer_act(tf_hip_ctx* ctx, int32_t layer, float* out);
  * or V (which = 1), whatever the layout (KVCache::k_at / v_at, kvcache.cpp:38-43). */
 int tf_hip_read_kv(tf_hip_ctx* ctx, int32_t layer, int32_t which, int32_t pos0, int32_t n, float* out);
 
-/* Timing of the last tf_hip_generate call, from HIP events on the context's stream:
- * total device milliseconds of the whole call, and of the dominant decode kernel summed over
- * the call together with its launch count. */
+/* Timing of the last tf_hip_generate or tf_hip_prefill call, from HIP events on the
+ * context's stream: total device milliseconds of the call's kernels, and of the dominant
+ * kernel summed over the call together with its launch count; kernel_name names the path
+ * ("k_step", "decode_graph", "prefill_mfma"). */
 int tf_hip_last_timing(const tf_hip_ctx* ctx, float* total_ms, float* kernel_ms, int32_t* kernel_launches,
                        char* kernel_name, int32_t name_len);
 
@@ -160,7 +173,9 @@ int tf_hip_dequant_rows(int device, int ggml_type, const void* w, int64_t ne0, i
                         int64_t nrows, float* out);
 
 /* matmul (matmul.cpp:64-73): y[m][n] = sum_k x[m][k] * W[n][k] for m < n_rows_x.
- * With n_rows_x == 1 this is the decode GEMV; larger values take the prefill GEMM. */
+ * One row runs the decode GEMV. Two or more rows of a Q8_0 matrix with ne0 % 64 == 0 and
+ * ne1 % 16 == 0 run the prefill GEMM on the matrix cores; other shapes and formats run
+ * the GEMV once per row. */
 int tf_hip_matmul(int device, int ggml_type, const void* w, int64_t ne0, int64_t ne1, const float* x,
                   int32_t n_rows_x, float* y);
 
@@ -172,6 +187,12 @@ int tf_hip_rmsnorm(int device, const float* x, const float* w, int32_t n, int32_
  * max_seq before the kernel runs; out [n_heads][hd]. */
 int tf_hip_attn_decode(int device, const float* q, const float* k_rows, const float* v_rows, int32_t n_heads,
                        int32_t n_kv, int32_t hd, int32_t n_pos, int32_t max_seq, int32_t layout, float* out);
+
+/* attn_prefill (attention.cpp:82-111, attention.hpp:29-30): causal GQA attention of seq
+ * positions over their own rows. q [seq][n_heads][hd], k and v [seq][n_kv][hd] (already
+ * rotated), out [seq][n_heads][hd]; hd 32, 64 or 128, n_heads / n_kv at most 8. */
+int tf_hip_attn_prefill(int device, const float* q, const float* k, const float* v, int32_t seq, int32_t n_heads,
+                        int32_t n_kv, int32_t hd, float* out);
 
 /* sample_greedy (sampler.cpp:8-13): index of the first maximum. */
 int tf_hip_argmax(int device, const float* x, int32_t n, int32_t* out);

@@ -42,6 +42,65 @@ def test_decode_path_selection(pkg, gguf, preset, want):
     big.close()
 
 
+TOKENS, MFMA = 0, 1  # HipModel.PREFILL_TOKENS, HipModel.PREFILL_MFMA
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("preset", ["tiny_q8", "tiny_qwen", "small_q8"])
+def test_small_models_token_prefill(pkg, gguf, preset, layout):
+    """The per-token prefill path on the models whose prompts otherwise take the matrix cores."""
+    info = pkg.synth_preset_info(preset)
+    prompt = pkg.synth_prompt(info["seed"], 6, info["n_vocab"])
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 8, 64, layout, prefill_path=TOKENS)
+    print(f"{preset} layout {layout}: ids {ids} logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
+
+
+@pytest.mark.parametrize("preset,want", [("tiny_q8", MFMA), ("tiny_qwen", MFMA), ("small_q8", MFMA),
+                                         ("tiny_f32", TOKENS), ("tiny_mixq4", TOKENS)])
+def test_prefill_path_selection(pkg, gguf, preset, want):
+    """Prompts run on the matrix cores when every layer matrix is Q8_0 with tileable
+    shapes; F32 and Q4 models keep the per-token path; PREFILL_TOKENS forces it."""
+    hip = pkg.HipModel(gguf(preset), max_seq=64)
+    assert hip.prefill_path() == want
+    hip.set_prefill_path(TOKENS)
+    assert hip.prefill_path() == TOKENS
+    hip.close()
+
+
+def test_prefill_paths_agree(pkg, gguf):
+    """A 150-token prompt through the matrix cores and token by token: logits within 1e-4,
+    same argmax, same per-layer activations and KV cache within 1e-4, same greedy stream."""
+    path = gguf("small_q8")
+    info = pkg.synth_preset_info("small_q8")
+    prompt = pkg.synth_prompt(info["seed"] + 1, 150, info["n_vocab"])
+    res = []
+    for pf in (TOKENS, MFMA):
+        hip = pkg.HipModel(path, max_seq=256)
+        hip.set_prefill_path(pf)
+        lg, am = hip.prefill(prompt)
+        taps = [hip.layer_act(layer) for layer in range(5)]
+        kv = [hip.read_kv(layer, w, 0, 150) for layer in (0, 3) for w in (0, 1)]
+        ids = hip.generate(8)
+        res.append((lg, am, taps, kv, ids))
+        hip.close()
+    (l0, a0, t0, k0, i0), (l1, a1, t1, k1, i1) = res
+    assert a0 == a1 and np.array_equal(i0, i1)
+    assert rel_err(l1, l0) <= 1e-4
+    for a, b in zip(t1, t0):
+        assert rel_err(a, b) <= 1e-4
+    for a, b in zip(k1, k0):
+        assert rel_err(a, b) <= 1e-4
+
+
+def test_long_prompt_runs_in_chunks(pkg, gguf):
+    """A prompt longer than one prefill chunk (2048 rows): later chunks attend to the earlier
+    ones through the cache, as one attn_prefill over the whole prompt does."""
+    info = pkg.synth_preset_info("tiny_q8")
+    prompt = pkg.synth_prompt(info["seed"] + 2, 2100, info["n_vocab"])
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf("tiny_q8"), prompt, 4, 2176, 1)
+    print(f"tiny_q8 2100-token prompt: ids {ids} logits {worst:.2e} taps {worst_tap:.2e}")
+
+
 def test_step_and_graph_agree(pkg, gguf):
     """Both decode paths give the same greedy stream and logits within 1e-5 from the same state."""
     path = gguf("small_q8")
@@ -113,6 +172,7 @@ def test_errors_and_reset(pkg, gguf):
     ("qwen05b_q8", 16, 128, 512, 0),    # Qwen2.5-0.5B shape with QKV bias
     ("llama1b_mixq4", 6, 64, 512, 0),   # Q4_0 / Q4_1 / Q6_K mix
     ("qwen15b_q8", 64, 16, 8192, 1),    # Qwen2.5-1.5B shape, head-major cache (short prompt)
+    ("llama1b_q8", 512, 4, 1024, 0),    # 512-token prompt on the matrix cores
 ])
 def test_full_size(pkg, gguf, preset, n_prompt, n_gen, max_seq, layout):
     info = pkg.synth_preset_info(preset)

@@ -67,6 +67,96 @@ def test_matmul_several_rows(pkg):
     assert rel_err(got, want) < 1e-5
 
 
+# (M, K, N) of the prefill GEMM: row counts around the 64-row tile, the workloads' K
+PF_GEMM_SHAPES = [(2, 64, 16), (37, 2048, 256), (64, 896, 1152), (100, 8192, 128), (130, 1536, 48),
+                  (512, 2048, 64), (65, 8960, 32), (7, 192, 320)]
+
+
+@pytest.mark.parametrize("m,k,n", PF_GEMM_SHAPES)
+def test_prefill_gemm_matches_oracle(pkg, m, k, n):
+    """Q8_0 rows x M activation rows on the matrix cores: |y - y_oracle| <= 2e-5 * sum_k
+    |x_k w_nk| per output. The fp16 pair of an activation keeps it to 2^-22 of its row's
+    largest element; the rest is fp32 reassociation, as for the GEMV."""
+    rng = np.random.default_rng(2000 + m + k + n)
+    rows = random_rows(rng, 8, k, n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got = pkg.matmul(8, rows, k, n, x)
+    want = oracle_matmul(8, rows, k, x)
+    budget = np.abs(x).astype(np.float64) @ np.abs(oracle_dequant(8, rows, k)).astype(np.float64).T
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= 2e-5 * budget + 1e-30), f"max err/budget {np.max(err / (budget + 1e-30)):.3e}"
+
+
+def test_prefill_gemm_row_scales(pkg):
+    """Rows of very different magnitude keep their relative precision (each row has its own
+    power-of-two scale); a zero row gives zeros; a row with one non-zero x_j gives
+    x_j * w[:, j] bit-exactly (one exact product per output)."""
+    rng = np.random.default_rng(77)
+    k, n = 512, 64
+    rows = random_rows(rng, 8, k, n)
+    deq = oracle_dequant(8, rows, k)
+    x = rng.standard_normal((6, k)).astype(np.float32)
+    x[1] = 0.0
+    x[2] *= 1e4
+    x[3] *= 1e-6
+    x[4] = 0.0
+    x[4, 7] = 3.0
+    x[5, 100] = 6.0e4  # one outlier above fp16's largest finite value
+    got = pkg.matmul(8, rows, k, n, x)
+    want = oracle_matmul(8, rows, k, x)
+    budget = np.abs(x).astype(np.float64) @ np.abs(deq).astype(np.float64).T
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 2e-5 * budget + 1e-30)
+    assert np.all(got[1] == 0.0)
+    assert np.array_equal(got[4], (np.float32(3.0) * deq[:, 7]).astype(np.float32))
+
+
+PF_ATTN_CASES = [  # seq, heads, kv heads, head_dim
+    (1, 4, 2, 64), (5, 4, 2, 32), (16, 32, 8, 64), (17, 14, 2, 64), (100, 12, 2, 128), (70, 6, 1, 32),
+    (512, 32, 8, 64),
+]
+
+
+def oracle_attn_prefill(q, k, v):
+    seq, h, hd = q.shape
+    g = k.shape[1]
+    want = np.zeros_like(q)
+    fp = C.POINTER(C.c_float)
+    scores = np.zeros(seq + 1, np.float32)
+    oracle_lib().orc_attn_prefill(want.ctypes.data_as(fp), q.ctypes.data_as(fp), k.ctypes.data_as(fp),
+                                  v.ctypes.data_as(fp), seq, h, g, hd, scores.ctypes.data_as(fp))
+    return want
+
+
+@pytest.mark.parametrize("seq,h,g,hd", PF_ATTN_CASES)
+def test_attn_prefill_matches_oracle(pkg, seq, h, g, hd):
+    """Causal attention of a chunk over its own rows (attention.cpp:82-111) on fp32 MFMA
+    with an online softmax: within 1e-5 normwise of the oracle."""
+    rng = np.random.default_rng(seq * 100 + h + hd)
+    q = rng.standard_normal((seq, h, hd)).astype(np.float32)
+    k = rng.standard_normal((seq, g, hd)).astype(np.float32)
+    v = rng.standard_normal((seq, g, hd)).astype(np.float32)
+    got = pkg.attn_prefill(q, k, v)
+    want = oracle_attn_prefill(q, k, v)
+    for i in range(seq):
+        assert rel_err(got[i], want[i]) <= 1e-5, f"row {i}: {rel_err(got[i], want[i]):.3e}"
+
+
+def test_attn_prefill_closed_forms(pkg):
+    """Row 0 attends to itself only: its heads are v[0] of their kv head, exactly. With q = 0
+    every score is 0 and row i is the mean of v[0..i]."""
+    rng = np.random.default_rng(8)
+    seq, h, g, hd = 40, 8, 2, 64
+    q = rng.standard_normal((seq, h, hd)).astype(np.float32)
+    k = rng.standard_normal((seq, g, hd)).astype(np.float32)
+    v = rng.standard_normal((seq, g, hd)).astype(np.float32)
+    got = pkg.attn_prefill(q, k, v)
+    assert np.array_equal(got[0], np.repeat(v[0], h // g, axis=0))
+    got = pkg.attn_prefill(np.zeros_like(q), k, v)
+    mean = np.cumsum(v.astype(np.float64), axis=0) / np.arange(1, seq + 1)[:, None, None]
+    want = np.repeat(mean, h // g, axis=1)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(v))
+
+
 @pytest.mark.parametrize("n", [32, 896, 2048, 8960])
 def test_rmsnorm(pkg, n):
     rng = np.random.default_rng(n)
