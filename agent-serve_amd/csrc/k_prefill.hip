@@ -1,8 +1,9 @@
 // Prefill of prompt tokens on the matrix cores: Model::prefill and layer_prefill
 // (model.cpp:144-195) for a chunk of M tokens at once.
 //
+// k_pf_pack_q8   a Q8_0 matrix's integers as fp16 in MFMA fragment order, once per matrix
 // k_pf_split     rmsnorm (layers.cpp:7-12) of each row, or the row as it is, scaled by
-//                a power of two and written as two fp16 planes hi + lo (the A operand)
+//                a power of two and written as fp16 hi + lo in fragment order (the A operand)
 // k_pf_gemm_q8   matmul (matmul.cpp:64-73) of Q8_0 weights on v_mfma_f32_16x16x32_f16,
 //                epilogues: store (+ F32 bias, model.cpp:85-89), residual add
 //                (add_inplace, layers.cpp:21-23), silu(gate) * up (layers.cpp:14-19)
@@ -31,80 +32,13 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
-// ---------------------------------------------------------------- activations -> fp16 pairs
-
-// One workgroup per row. Rows M..Mpad-1 are zeroed so the GEMM tiles past the last
-// token read zeros.
-__global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx, const float* w, float eps, int K,
-                                                     int M, uint16_t* xh, uint16_t* xl, float* rs) {
-    __shared__ double red_d[kWavesPerBlock];
-    __shared__ float red_f[kWavesPerBlock];
-    const int m = blockIdx.x, tid = threadIdx.x;
-    h4_t* hh = (h4_t*)(xh + (int64_t)m * K);
-    h4_t* ll = (h4_t*)(xl + (int64_t)m * K);
-    const int K4 = K / 4;
-    if (m >= M) {
-        const h4_t z = {0, 0, 0, 0};
-        for (int k = tid; k < K4; k += kBlock) {
-            hh[k] = z;
-            ll[k] = z;
-        }
-        if (tid == 0) rs[m] = 0.0f;
-        return;
-    }
-    const float4* xr = (const float4*)(x + (int64_t)m * ldx);
-    const float4* wr = (const float4*)w;
-    float inv = 1.0f;
-    if (w) {
-        double ss = 0;
-        for (int k = tid; k < K4; k += kBlock) {
-            const float4 v = xr[k];
-            ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-        }
-        ss = wave_sum_d(ss);
-        if ((tid & 63) == 0) red_d[tid >> 6] = ss;
-        __syncthreads();
-        ss = (red_d[0] + red_d[1]) + (red_d[2] + red_d[3]);
-        inv = 1.0f / sqrtf((float)(ss / K) + eps);
-    }
-    auto val = [&](int k) {
-        float4 v = xr[k];
-        if (w) {
-            const float4 g = wr[k];
-            v = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
-        }
-        return v;
-    };
-    float amax = 0.0f;
-    for (int k = tid; k < K4; k += kBlock) {
-        const float4 v = val(k);
-        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-    amax = wave_max(amax);
-    if ((tid & 63) == 0) red_f[tid >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
-    int ex = 0;
-    (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
-    int e = amax > 0.0f ? 15 - ex : 0;
-    e = e < -100 ? -100 : (e > 100 ? 100 : e);
-    const float sc = ldexpf(1.0f, e);
-    if (tid == 0) rs[m] = ldexpf(1.0f, -e);
-    for (int k = tid; k < K4; k += kBlock) {
-        const float4 v = val(k);
-        const float t[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
-        h4_t h, l;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            h[j] = (_Float16)t[j];
-            l[j] = (_Float16)(t[j] - (float)h[j]);
-        }
-        hh[k] = h;
-        ll[k] = l;
-    }
-}
-
-// ---------------------------------------------------------------- Q8_0 GEMM
+// ---------------------------------------------------------------- operands in MFMA fragment order
+//
+// v_mfma_f32_16x16x32_f16 takes from lane l the 8 halves (row l % 16, k = 8 (l / 16) + j)
+// of a 16 x 32 operand tile. Both operands are stored so that one tile is 64 lanes x 16
+// bytes, contiguous: a wave fills a fragment with one coalesced 1 KiB load.
+//   activations: xa[row tile][block][hi, lo][lane][8]   (k_pf_split)
+//   weights:     wf[row tile][block][lane][8]            (k_pf_pack_q8, once per matrix)
 
 // Eight offset-binary bytes (q + 128) -> the fp16 values q: 0x64XX is the half 1024 + XX,
 // and 1024 + XX - 1152 = q exactly.
@@ -118,16 +52,111 @@ __device__ __forceinline__ h8_t q8_to_h8(uint2 w) {
     return __builtin_bit_cast(h8_t, p) - off;
 }
 
+// Q8_0 matrix (DevMat q stream, N x K) -> its integers q as fp16 in fragment order.
+__global__ __launch_bounds__(kBlock) void k_pf_pack_q8(const uint8_t* q, int K, int64_t N, h8_t* wf) {
+    const int nblk = K / 32;
+    const int64_t total = N / 16 * nblk * 64;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
+        const int l = (int)(i & 63);
+        const int64_t tb = i >> 6;
+        const int b = (int)(tb % nblk);
+        const int64_t t = tb / nblk;
+        wf[i] = q8_to_h8(*(const uint2*)(q + (16 * t + (l & 15)) * (int64_t)K + 32 * b + 8 * (l >> 4)));
+    }
+}
+
+// Row statistics, one wave per row: the rmsnorm scale inv (when w is given) and a power
+// of two sc putting max |row| in [2^14, 2^15); rs = 1 / sc. Rows M.. get sc = rs = 0.
+__global__ __launch_bounds__(kBlock) void k_pf_rowstats(const float* x, int64_t ldx, const float* w, float eps,
+                                                        int K, int M, float* st /* [Mpad][2]: inv, sc */,
+                                                        float* rs) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int K4 = K / 4;
+    const float4* wr = (const float4*)w;
+    float inv = 1.0f, sc = 0.0f, rsv = 0.0f;
+    if (m < M) {
+        const float4* xr = (const float4*)(x + (int64_t)m * ldx);
+        if (w) {
+            double ss = 0;
+            for (int k = lane; k < K4; k += 64) {
+                const float4 v = xr[k];
+                ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+            }
+            ss = wave_sum_d(ss);
+            inv = 1.0f / sqrtf((float)(ss / K) + eps);
+        }
+        float amax = 0.0f;
+        for (int k = lane; k < K4; k += 64) {
+            float4 v = xr[k];
+            if (w) {
+                const float4 g = wr[k];
+                v = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+            }
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+        amax = wave_max(amax);
+        int ex = 0;
+        (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
+        int e = amax > 0.0f ? 15 - ex : 0;
+        e = e < -100 ? -100 : (e > 100 ? 100 : e);
+        sc = ldexpf(1.0f, e);
+        rsv = ldexpf(1.0f, -e);
+    }
+    if (lane == 0) {
+        st[2 * m] = inv;
+        st[2 * m + 1] = sc;
+        rs[m] = rsv;
+    }
+}
+
+// Every element as hi + lo in fragment order: grid (row tiles, groups of 4 blocks); a
+// thread writes one lane's 16 bytes of a hi and a lo fragment.
+__global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx, const float* w, int K, int M,
+                                                     const float* st, h8_t* xa) {
+    const int T = blockIdx.x, nblk = K / 32;
+    const int b = blockIdx.y * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (b >= nblk) return;
+    const int r = l & 15, m = T * 16 + r;
+    const int k0 = 32 * b + 8 * (l >> 4);
+    h8_t hi = {0, 0, 0, 0, 0, 0, 0, 0}, lo = hi;
+    if (m < M) {
+        const float4* xr = (const float4*)(x + (int64_t)m * ldx + k0);
+        const float4 v0 = xr[0], v1 = xr[1];
+        float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        const float inv = st[2 * m], sc = st[2 * m + 1];
+        if (w) {
+            const float4* wr = (const float4*)(w + k0);
+            const float4 g0 = wr[0], g1 = wr[1];
+            const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = v[j] * inv * g[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float t = v[j] * sc;
+            hi[j] = (_Float16)t;
+            lo[j] = (_Float16)(t - (float)hi[j]);
+        }
+    }
+    h8_t* out = xa + ((int64_t)T * nblk + b) * 128;
+    out[l] = hi;
+    out[64 + l] = lo;
+}
+
+// ---------------------------------------------------------------- Q8_0 GEMM
+
 // Field of the segment holding output subtile u (uniform per wave: scalar selects).
 #define PF_SEL(s, f) ((s) == 0 ? a.seg[0].f : ((s) == 1 ? a.seg[1].f : a.seg[2].f))
 
-// Workgroup: 4 waves as 2 (rows) x 2 (columns); a wave owns 32 rows x 4 column subtiles
-// of 16 (GEMV_SILU: 2 output subtiles, each a gate and an up subtile). Per 32-element
-// block and (row subtile, column subtile): two MFMAs (hi, lo) from zero, then
-// acc += d * block sum. Operands stream from L2 into registers, one stage of two
-// blocks ahead; every load is unconditional (indices clamped) so the compiler waits
-// only for the stage it consumes.
-template <int MODE>
+// Workgroup: 4 waves as 2 (rows) x 2 (columns); a wave owns 32 rows x NI column subtiles
+// of 16 (GEMV_SILU: NI / 2 output subtiles, each a gate and an up subtile). Per 32-element
+// block: for each (row subtile, column subtile) an MFMA of the hi part from zero, then
+// one of the lo part on top (issued after all eight hi MFMAs, so no MFMA waits on the
+// one before it), then acc += d * block sum. Fragments stream from L2 into registers,
+// one stage of two blocks ahead; every load is unconditional (indices clamped) so the
+// compiler waits only for the stage it consumes.
+template <int MODE, int NI>
 __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous range
@@ -142,91 +171,89 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
     const int m0 = mt * kPfTileM + (wave & 1) * 32;
     const int wid = nt * 2 + (wave >> 1);
     const int K = a.K, nblk = K / 32;
-    const int kq = 8 * (lane >> 4);  // this lane's 8 k of a 32-element block
     const int l16 = lane & 15;
 
-    const uint8_t* qp[4];
-    const uint16_t* sp[4];
-    float* yp[4];
-    const float* bp[4];
-    int64_t ldy[4];
-    int col[4];
-    bool ok[4];
+    constexpr int NO = MODE == GEMV_SILU ? NI / 2 : NI;  // output subtiles per wave
+    const TF_GLOBAL h8_t* bp[NI];
+    const uint16_t* sp[NI];
+    float* yp[NI];
+    const float* bsp[NI];
+    int64_t ldy[NI];
+    int col[NI];
+    bool ok[NI];
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
-        int u = MODE == GEMV_SILU ? wid * 2 + (ni & 1) : wid * 4 + ni;
+    for (int ni = 0; ni < NI; ++ni) {
+        int u = wid * NO + ni % NO;
         ok[ni] = u < a.n_sub;
         u = u < a.n_sub ? u : a.n_sub - 1;
         const int s = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
-        const int c = (u - PF_SEL(s, sub0)) * 16 + l16;
-        const bool up = MODE == GEMV_SILU && ni >= 2;
-        const uint8_t* wq = up ? PF_SEL(s, w2.q) : PF_SEL(s, w.q);
+        const int tile = u - PF_SEL(s, sub0);
+        const int c = tile * 16 + l16;
+        const bool up = MODE == GEMV_SILU && ni >= NO;
+        const uint16_t* wf = up ? PF_SEL(s, wf2) : PF_SEL(s, wf);
         const uint8_t* ws = up ? PF_SEL(s, w2.s) : PF_SEL(s, w.s);
-        qp[ni] = wq + (int64_t)c * K + kq;
+        bp[ni] = (const TF_GLOBAL h8_t*)wf + (int64_t)tile * nblk * 64 + lane;
         sp[ni] = (const uint16_t*)ws + (int64_t)c * nblk;
         yp[ni] = PF_SEL(s, y);
-        bp[ni] = PF_SEL(s, bias);
+        bsp[ni] = PF_SEL(s, bias);
         ldy[ni] = PF_SEL(s, ldy);
         col[ni] = c;
     }
-    const _Float16* ah_p[2];
-    const _Float16* al_p[2];
+    const TF_GLOBAL h8_t* ap[2];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi) {
-        const int64_t r = m0 + 16 * mi + l16;
-        ah_p[mi] = (const _Float16*)a.xh + r * K + kq;
-        al_p[mi] = (const _Float16*)a.xl + r * K + kq;
-    }
+    for (int mi = 0; mi < 2; ++mi) ap[mi] = (const TF_GLOBAL h8_t*)a.xa + (int64_t)(m0 / 16 + mi) * nblk * 128 + lane;
 
-    f4_t acc[2][4];
+    f4_t acc[2][NI];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
 
     struct Stage {
         h8_t ah[2][2], al[2][2];  // [row subtile][block]
-        uint2 bq[4][2];           // [column subtile][block]
-        uint32_t d[4];            // the two blocks' fp16 scales
+        h8_t bh[NI][2];           // [column subtile][block]
+        uint32_t d[NI];           // the two blocks' fp16 scales
     };
     const int S = K / 64;
     auto load = [&](int s, Stage& g) {
         s = s < S ? s : S - 1;
-        const int k0 = s * 64;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int j = 0; j < 2; ++j) {
+            const int blk = 2 * s + j;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                g.ah[mi][j] = *(const TF_GLOBAL h8_t*)(ah_p[mi] + k0 + 32 * j);
-                g.al[mi][j] = *(const TF_GLOBAL h8_t*)(al_p[mi] + k0 + 32 * j);
+            for (int mi = 0; mi < 2; ++mi) {
+                g.ah[mi][j] = ap[mi][blk * 128];
+                g.al[mi][j] = ap[mi][blk * 128 + 64];
             }
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) g.bq[ni][j] = gload_u2(qp[ni] + k0 + 32 * j);
-            g.d[ni] = *(const TF_GLOBAL uint32_t*)(sp[ni] + 2 * s);
+            for (int ni = 0; ni < NI; ++ni) g.bh[ni][j] = bp[ni][blk * 64];
         }
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) g.d[ni] = *(const TF_GLOBAL uint32_t*)(sp[ni] + 2 * s);
     };
     auto compute = [&](const Stage& g) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            h8_t bh[4];
-            float dv[4];
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
-                bh[ni] = q8_to_h8(g.bq[ni][j]);
-                dv[ni] = h2f(g.d[ni] >> (16 * j));
-            }
+            f4_t t[2][NI];
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-                for (int ni = 0; ni < 4; ++ni) {
-                    f4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], bh[ni], (f4_t){0.0f, 0.0f, 0.0f, 0.0f},
-                                                                   0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], bh[ni], t, 0, 0, 0);
+                for (int ni = 0; ni < NI; ++ni)
+                    t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], g.bh[ni][j],
+                                                                      (f4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[mi][ni][r] = fmaf(dv[ni], t[r], acc[mi][ni][r]);
-                }
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni)
+                    t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], g.bh[ni][j], t[mi][ni], 0, 0, 0);
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni) {
+                const float dv = h2f(g.d[ni] >> (16 * j));
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[mi][ni][r] = fmaf(dv, t[mi][ni][r], acc[mi][ni][r]);
+            }
         }
     };
     Stage s0, s1;
@@ -252,20 +279,20 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
             if (row >= a.M) continue;
             if (MODE == GEMV_SILU) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < NO; ++j) {
                     if (!ok[j]) continue;
                     const float gv = acc[mi][j][r] * rsa[r];
-                    const float uv = acc[mi][j + 2][r] * rsa[r];
+                    const float uv = acc[mi][j + NO][r] * rsa[r];
                     yp[j][(int64_t)row * ldy[j] + col[j]] = (gv / (1.0f + expf(-gv))) * uv;
                 }
             } else {
 #pragma unroll
-                for (int ni = 0; ni < 4; ++ni) {
+                for (int ni = 0; ni < NI; ++ni) {
                     if (!ok[ni]) continue;
                     const float v = acc[mi][ni][r] * rsa[r];
                     float* p = yp[ni] + (int64_t)row * ldy[ni] + col[ni];
                     if (MODE == GEMV_STORE) {
-                        *p = bp[ni] ? v + bp[ni][col[ni]] : v;
+                        *p = bsp[ni] ? v + bsp[ni][col[ni]] : v;
                     } else {
                         const float nv = *p + v;
                         *p = nv;
@@ -445,9 +472,21 @@ bool pf_gemm_supported(int type, int64_t K, int64_t N) {
 }
 
 hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,
-                           uint16_t* xh, uint16_t* xl, float* rs, hipStream_t st) {
-    if (K % 4 != 0 || ldx % 4 != 0 || Mpad % kPfTileM != 0 || M > Mpad) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_split, dim3(Mpad), dim3(kBlock), 0, st, x, ldx, norm_w, eps, K, M, xh, xl, rs);
+                           uint16_t* xa, float* rs, float* st, hipStream_t s) {
+    if (K % 32 != 0 || ldx % 4 != 0 || Mpad % kPfTileM != 0 || M > Mpad) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_rowstats, dim3(Mpad / kWavesPerBlock), dim3(kBlock), 0, s, x, ldx, norm_w, eps, K, M, st,
+                       rs);
+    hipLaunchKernelGGL(k_pf_split, dim3(Mpad / 16, (K / 32 + 3) / 4), dim3(kBlock), 0, s, x, ldx, norm_w, K, M, st,
+                       (h8_t*)xa);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_pack_q8(const DevMat& m, uint16_t* wf, hipStream_t st) {
+    if (m.type != TF_HIP_TYPE_Q8_0 || m.K % 32 != 0 || m.N % 16 != 0) return hipErrorInvalidValue;
+    const int64_t total = m.N / 16 * (m.K / 32) * 64;
+    int64_t blocks = (total + kBlock - 1) / kBlock;
+    blocks = blocks < 4096 ? blocks : 4096;
+    hipLaunchKernelGGL(k_pf_pack_q8, dim3((unsigned)blocks), dim3(kBlock), 0, st, m.q, (int)m.K, m.N, (h8_t*)wf);
     return hipGetLastError();
 }
 
@@ -457,22 +496,32 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st) {
         return hipErrorInvalidValue;
     for (int s = 0; s < a.n_seg; ++s) {
         const PfSeg& g = a.seg[s];
-        if (g.w.type != TF_HIP_TYPE_Q8_0 || g.w.K != a.K || g.w.N % 16 != 0 || !g.y) return hipErrorInvalidValue;
+        if (g.w.type != TF_HIP_TYPE_Q8_0 || g.w.K != a.K || g.w.N % 16 != 0 || !g.y || !g.wf)
+            return hipErrorInvalidValue;
         const int next = s + 1 < a.n_seg ? a.seg[s + 1].sub0 : a.n_sub;
         if (next - g.sub0 != g.w.N / 16) return hipErrorInvalidValue;
-        if (a.mode == GEMV_SILU && (g.w2.type != TF_HIP_TYPE_Q8_0 || g.w2.K != a.K || g.w2.N != g.w.N))
+        if (a.mode == GEMV_SILU && (g.w2.type != TF_HIP_TYPE_Q8_0 || g.w2.K != a.K || g.w2.N != g.w.N || !g.wf2))
             return hipErrorInvalidValue;
     }
     if (a.seg[0].sub0 != 0 || (a.mode == GEMV_SILU && a.n_seg != 1)) return hipErrorInvalidValue;
-    const int per_wg = a.mode == GEMV_SILU ? 4 : 8;  // output subtiles per workgroup column
-    const int nt = (a.n_sub + per_wg - 1) / per_wg;
-    const dim3 grid((unsigned)(nt * (a.Mpad / kPfTileM)));
-    switch (a.mode) {
-        case GEMV_STORE: hipLaunchKernelGGL(k_pf_gemm_q8<GEMV_STORE>, grid, dim3(256), 0, st, a); break;
-        case GEMV_RESID: hipLaunchKernelGGL(k_pf_gemm_q8<GEMV_RESID>, grid, dim3(256), 0, st, a); break;
-        case GEMV_SILU: hipLaunchKernelGGL(k_pf_gemm_q8<GEMV_SILU>, grid, dim3(256), 0, st, a); break;
+    // 4 column subtiles per wave; 2 when that leaves fewer than two workgroups per CU
+    const int mt = a.Mpad / kPfTileM;
+    const int out4 = a.mode == GEMV_SILU ? 2 : 4;
+    const int wg4 = (a.n_sub + 2 * out4 - 1) / (2 * out4) * mt;
+    const int ni = wg4 >= 2 * device_cu_count() ? 4 : 2;
+    const int per_wg = 2 * (a.mode == GEMV_SILU ? ni / 2 : ni);  // output subtiles per workgroup column
+    const dim3 grid((unsigned)((a.n_sub + per_wg - 1) / per_wg * mt));
+#define PF_LAUNCH(MODE, NI) hipLaunchKernelGGL((k_pf_gemm_q8<MODE, NI>), grid, dim3(256), 0, st, a)
+    switch (a.mode * 8 + ni) {
+        case GEMV_STORE * 8 + 4: PF_LAUNCH(GEMV_STORE, 4); break;
+        case GEMV_STORE * 8 + 2: PF_LAUNCH(GEMV_STORE, 2); break;
+        case GEMV_RESID * 8 + 4: PF_LAUNCH(GEMV_RESID, 4); break;
+        case GEMV_RESID * 8 + 2: PF_LAUNCH(GEMV_RESID, 2); break;
+        case GEMV_SILU * 8 + 4: PF_LAUNCH(GEMV_SILU, 4); break;
+        case GEMV_SILU * 8 + 2: PF_LAUNCH(GEMV_SILU, 2); break;
         default: return hipErrorInvalidValue;
     }
+#undef PF_LAUNCH
     return hipGetLastError();
 }
 

@@ -73,7 +73,8 @@ struct tf_hip_ctx {
     int pf_state = -1;                 // -1 undecided, 0 per-token path, 1 matrix-core path ready
     int pf_cap = 0;                    // rows per prefill chunk (multiple of kPfTileM)
     float *px = nullptr, *pqkv = nullptr, *patt = nullptr, *ph = nullptr, *prs = nullptr;
-    uint16_t *pxh = nullptr, *pxl = nullptr;
+    uint16_t* pxa = nullptr;            // activation fragments (hi, lo) of one chunk
+    std::vector<uint16_t*> pf_wf;       // per slot: the matrix's integers as fp16 fragments
     std::string err;
 };
 
@@ -544,11 +545,24 @@ int ensure_pf(tf_hip_ctx* c) {
         const size_t kmax = std::max({D, F, (size_t)c->H});
         if ((rc = dalloc(c, &c->px, cap * D * 4)) || (rc = dalloc(c, &c->pqkv, cap * NQ * 4)) ||
             (rc = dalloc(c, &c->patt, cap * (size_t)c->H * 4)) || (rc = dalloc(c, &c->ph, cap * F * 4)) ||
-            (rc = dalloc(c, &c->prs, (size_t)cap * 4)) || (rc = dalloc(c, &c->pxh, cap * kmax * 2)) ||
-            (rc = dalloc(c, &c->pxl, cap * kmax * 2)))
+            (rc = dalloc(c, &c->prs, (size_t)cap * 3 * 4)) || (rc = dalloc(c, &c->pxa, cap * kmax * 2 * 2)))
             return rc;
         c->pf_cap = cap;
     }
+    // every layer matrix's integers as fp16 fragments (2 bytes per weight, kept for the
+    // context's life; a re-uploaded matrix is packed again)
+    c->pf_wf.assign(c->mats.size(), nullptr);
+    for (int l = 0; l < p.n_layer; ++l)
+        for (int k : {TF_HIP_LAYER_Q, TF_HIP_LAYER_K, TF_HIP_LAYER_V, TF_HIP_LAYER_O, TF_HIP_LAYER_GATE, TF_HIP_LAYER_UP,
+                      TF_HIP_LAYER_DOWN}) {
+            const int slot = TF_HIP_SLOT_LAYER(l, k);
+            const DevMat& m = mat(c, slot);
+            uint16_t* wf = nullptr;
+            if ((rc = dalloc(c, &wf, (size_t)m.N * m.K * 2))) return rc;
+            HIPCHK(c, launch_pf_pack_q8(m, wf, c->st));
+            c->pf_wf[(size_t)slot] = wf;
+        }
+    HIPCHK(c, hipStreamSynchronize(c->st));
     c->pf_state = 1;
     return 1;
 }
@@ -574,17 +588,18 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
         chk(launch_embed_rows(mat(c, TF_HIP_SLOT_TOKEN_EMBD), c->hist + pos0, nc, c->px, D, c->st));
         auto base = [&](int K) {
             PfGemmArgs a;
-            a.xh = c->pxh;
-            a.xl = c->pxl;
+            a.xa = c->pxa;
             a.rs = c->prs;
             a.K = K;
             a.M = nc;
             a.Mpad = Mpad;
             return a;
         };
-        auto seg = [](PfGemmArgs& a, const DevMat& w, float* y, int64_t ldy, const float* bias) {
+        auto seg = [&](PfGemmArgs& a, int slot, float* y, int64_t ldy, const float* bias) {
             PfSeg& s = a.seg[a.n_seg++];
+            const DevMat& w = mat(c, slot);
             s.w = w;
+            s.wf = c->pf_wf[(size_t)slot];
             s.y = y;
             s.ldy = ldy;
             s.bias = bias;
@@ -592,12 +607,12 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
             a.n_sub += (int)(w.N / 16);
         };
         for (int l = 0; l < p.n_layer && e == hipSuccess; ++l) {
-            auto M = [&](int k) -> const DevMat& { return mat(c, TF_HIP_SLOT_LAYER(l, k)); };
+            auto M = [&](int k) { return TF_HIP_SLOT_LAYER(l, k); };
             auto V = [&](int k) { return vec(c, TF_HIP_SLOT_LAYER(l, k)); };
             float* kc = c->kc + (size_t)l * c->kv_layer;
             float* vc = c->vc + (size_t)l * c->kv_layer;
-            chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_ATTN_NORM), p.rms_eps, D, nc, Mpad, c->pxh, c->pxl, c->prs,
-                                c->st));
+            chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_ATTN_NORM), p.rms_eps, D, nc, Mpad, c->pxa, c->prs,
+                                c->prs + c->pf_cap, c->st));
             {
                 PfGemmArgs a = base(D);
                 a.mode = GEMV_STORE;
@@ -610,23 +625,24 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                                      pos0, kc, vc, p.kv_layout, p.max_seq, c->st));
             chk(launch_pf_attn(c->pqkv, NQ, kc, vc, p.kv_layout, p.n_head, p.n_kv_head, p.head_dim, p.max_seq, nc,
                                pos0, start, c->patt, Hd, c->st));
-            chk(launch_pf_split(c->patt, Hd, nullptr, 0.0f, Hd, nc, Mpad, c->pxh, c->pxl, c->prs, c->st));
+            chk(launch_pf_split(c->patt, Hd, nullptr, 0.0f, Hd, nc, Mpad, c->pxa, c->prs, c->prs + c->pf_cap, c->st));
             {
                 PfGemmArgs a = base(Hd);
                 a.mode = GEMV_RESID;
                 seg(a, M(TF_HIP_LAYER_O), c->px, D, nullptr);
                 chk(launch_pf_gemm(a, c->st));
             }
-            chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_FFN_NORM), p.rms_eps, D, nc, Mpad, c->pxh, c->pxl, c->prs,
-                                c->st));
+            chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_FFN_NORM), p.rms_eps, D, nc, Mpad, c->pxa, c->prs,
+                                c->prs + c->pf_cap, c->st));
             {
                 PfGemmArgs a = base(D);
                 a.mode = GEMV_SILU;
                 seg(a, M(TF_HIP_LAYER_GATE), c->ph, F, nullptr);
-                a.seg[0].w2 = M(TF_HIP_LAYER_UP);
+                a.seg[0].w2 = mat(c, M(TF_HIP_LAYER_UP));
+                a.seg[0].wf2 = c->pf_wf[(size_t)M(TF_HIP_LAYER_UP)];
                 chk(launch_pf_gemm(a, c->st));
             }
-            chk(launch_pf_split(c->ph, F, nullptr, 0.0f, F, nc, Mpad, c->pxh, c->pxl, c->prs, c->st));
+            chk(launch_pf_split(c->ph, F, nullptr, 0.0f, F, nc, Mpad, c->pxa, c->prs, c->prs + c->pf_cap, c->st));
             {
                 PfGemmArgs a = base(F);
                 a.mode = GEMV_RESID;
@@ -1133,15 +1149,15 @@ int tf_hip_matmul(int device, int t, const void* w, int64_t ne0, int64_t ne1, co
     if (n_rows_x >= 2 && pf_gemm_supported(t, ne0, ne1)) {
         // several rows: the prefill GEMM on the matrix cores
         const int Mpad = (n_rows_x + kPfTileM - 1) / kPfTileM * kPfTileM;
-        uint16_t *xh, *xl;
+        uint16_t *xa, *wf;
         float* rs;
-        OPCHK(s.alloc(&xh, (size_t)Mpad * ne0 * 2));
-        OPCHK(s.alloc(&xl, (size_t)Mpad * ne0 * 2));
-        OPCHK(s.alloc(&rs, (size_t)Mpad * 4));
-        OPCHK(launch_pf_split(dx, ne0, nullptr, 0.0f, (int)ne0, n_rows_x, Mpad, xh, xl, rs, s.st));
+        OPCHK(s.alloc(&xa, (size_t)Mpad * ne0 * 2 * 2));
+        OPCHK(s.alloc(&wf, (size_t)ne1 * ne0 * 2));
+        OPCHK(s.alloc(&rs, (size_t)Mpad * 3 * 4));
+        OPCHK(launch_pf_pack_q8(m, wf, s.st));
+        OPCHK(launch_pf_split(dx, ne0, nullptr, 0.0f, (int)ne0, n_rows_x, Mpad, xa, rs, rs + Mpad, s.st));
         PfGemmArgs a;
-        a.xh = xh;
-        a.xl = xl;
+        a.xa = xa;
         a.rs = rs;
         a.K = (int)ne0;
         a.M = n_rows_x;
@@ -1149,6 +1165,7 @@ int tf_hip_matmul(int device, int t, const void* w, int64_t ne0, int64_t ne1, co
         a.mode = GEMV_STORE;
         a.n_seg = 1;
         a.seg[0].w = m;
+        a.seg[0].wf = wf;
         a.seg[0].y = dy;
         a.seg[0].ldy = ne1;
         a.n_sub = (int)(ne1 / 16);

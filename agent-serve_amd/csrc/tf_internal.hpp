@@ -156,19 +156,20 @@ __host__ __device__ inline int64_t kv_offset(int layout, int G, int max_seq, int
 
 // One weight matrix of a prefill GEMM and where its output columns go.
 struct PfSeg {
-    DevMat w;                     // weight (gate for GEMV_SILU)
+    DevMat w;                     // weight (gate for GEMV_SILU): shape and fp16 d stream
     DevMat w2;                    // up matrix for GEMV_SILU
+    const uint16_t* wf = nullptr;   // w's integers as fp16 in fragment order (launch_pf_pack_q8)
+    const uint16_t* wf2 = nullptr;  // the same for w2
     float* y = nullptr;           // output rows of ldy floats
     int64_t ldy = 0;
     const float* bias = nullptr;  // F32 bias added to the output (GEMV_STORE)
     int sub0 = 0;                 // first 16-column output subtile of this segment
 };
 
-// C[M x N] = A[M x K] . W^T over the matrix cores. A arrives as two fp16 planes whose
+// C[M x N] = A[M x K] . W^T over the matrix cores. A arrives as fp16 pairs hi + lo whose
 // sum is each row times a power of two (rs holds the inverse), see launch_pf_split.
 struct PfGemmArgs {
-    const uint16_t* xh = nullptr;  // [Mpad][K] fp16 high part
-    const uint16_t* xl = nullptr;  // [Mpad][K] fp16 low part
+    const uint16_t* xa = nullptr;  // [Mpad/16][K/32][hi, lo][64][8] fp16 (fragment order)
     const float* rs = nullptr;     // [Mpad] row scales
     int K = 0, M = 0, Mpad = 0;
     PfSeg seg[3];
@@ -180,8 +181,11 @@ struct PfGemmArgs {
 };
 
 bool pf_gemm_supported(int type, int64_t K, int64_t N);
+// xa needs Mpad * K * 2 halves, rs Mpad floats, st 2 * Mpad floats (row statistics).
 hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,
-                           uint16_t* xh, uint16_t* xl, float* rs, hipStream_t st);
+                           uint16_t* xa, float* rs, float* st, hipStream_t s);
+// wf needs m.N * m.K halves.
+hipError_t launch_pf_pack_q8(const DevMat& m, uint16_t* wf, hipStream_t st);
 hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st);
 hipError_t launch_embed_rows(const DevMat& emb, const int32_t* tok, int n, float* x, int D, hipStream_t st);
 hipError_t launch_pf_rope_store(float* qkv, int64_t ld, int n, int H, int G, int hd, const float* rope_cos,

@@ -13,7 +13,10 @@ HBM), timed between two synchronisations. `roofline` is that kernel's achieved
 algorithmic GB/s (the K steps' bytes over the HIP-event time of the launch); a second,
 kernel-by-kernel pass over the same steps on the graph path gives the per-class times;
 `cpu_baseline` is the reference --stage v2 path (compiled from its own sources) timed
-on this host's cores over the same prompt and steps.
+on this host's cores over the same prompt and steps. `prefill` is the 512-token prompt
+workload of the same model on the matrix cores: tok/s from HIP events around the call,
+algorithmic TFLOP/s and their fraction of the dense fp16 MFMA peak, the decode rate
+after the prompt, and the reference CPU prefill on a bounded sample.
 """
 from __future__ import annotations
 
@@ -39,6 +42,13 @@ COPY_CALIB_BYTES = 1 << 30
 TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_llama1b_q8_0_traffic.txt"
 STEP_TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_llama1b_q8_0_step_kernel_traffic.txt"
 PUBLISHED_CPU_TOK_S = 10.74  # reference --stage v2, Llama-3.2-1B Q8_0, Ryzen 5 4600H
+# prefill leg: a 512-token prompt of the same model, then 16 decode tokens
+PF_PROMPT_TOKENS = 512
+PF_DECODE_TOKENS = 16
+PF_MAX_SEQ = 1024
+PF_REPS = 5
+PF_CPU_SAMPLE_TOKENS = 64
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X
 
 
 def host_threads() -> int:
@@ -70,6 +80,89 @@ def measured_traffic(kernel_class: str, tokens_per_launch: int = 1):
         except OSError:
             pass
     return None
+
+
+def prefill_flops(info, n):
+    """Algorithmic FLOP of a prefill of n tokens: 2 per weight per token for the layer
+    matrices, the causal attention (q.k and p.v over i + 1 positions for token i), and
+    the lm_head of the last token."""
+    D, F, L, H, G = info["n_embd"], info["n_ff"], info["n_layer"], info["n_head"], info["n_kv_head"]
+    hd = D // H
+    dense = 2.0 * n * L * (D * (H * hd + 2 * G * hd) + H * hd * D + 3 * D * F)
+    attn = 4.0 * hd * (n * (n + 1) / 2) * H * L
+    return dense + attn + 2.0 * D * info["n_vocab"], dense
+
+
+def prefill_leg(pkg, path, info):
+    """The 512-token prompt: PF_REPS timed prefills from a reset (device ms from HIP events
+    around the call's kernels, and wall ms of the synchronous call), then the 16 decode
+    tokens after it."""
+    prompt = pkg.synth_prompt(info["seed"], PF_PROMPT_TOKENS, info["n_vocab"])
+    m = pkg.HipModel(path, max_seq=PF_MAX_SEQ, kv_layout=0)
+    m.prefill(prompt, want_logits=False)  # warm-up
+    dev, wall = [], []
+    for _ in range(PF_REPS):
+        m.reset()
+        t0 = time.perf_counter()
+        _, am = m.prefill(prompt, want_logits=False)
+        wall.append((time.perf_counter() - t0) * 1e3)
+        ms, _, _, name = m.last_timing()
+        dev.append(ms)
+    ids = m.generate(PF_DECODE_TOKENS)
+    dec_ms = m.last_timing()[0]
+    pf_path = m.prefill_path()
+    m.close()
+    flops, dense = prefill_flops(info, PF_PROMPT_TOKENS)
+    d_ms = statistics.median(dev)
+    tflops = flops / (d_ms * 1e-3) / 1e12
+    return {
+        "workload": f"{PF_PROMPT_TOKENS}-token prompt (uniform ids, seed {info['seed']}) of the same model, "
+                    f"max-seq {PF_MAX_SEQ}, then {PF_DECODE_TOKENS} greedy decode tokens",
+        "path": name if pf_path == m.PREFILL_MFMA else "per-token",
+        "tokens": PF_PROMPT_TOKENS,
+        "device_ms": round(d_ms, 3),
+        "wall_ms": round(statistics.median(wall), 3),
+        "tok_s": round(PF_PROMPT_TOKENS / (d_ms * 1e-3), 1),
+        "tflop": round(flops / 1e12, 4),
+        "dense_tflop": round(dense / 1e12, 4),
+        "achieved_tflop_s": round(tflops, 2),
+        "mfma_peak_tflop_s": MFMA_F16_PEAK_TFLOPS,
+        "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+        "mfma_note": "algorithmic FLOP/s over the dense fp16 MFMA peak; the GEMMs issue two fp16 MFMAs "
+                     "(activation hi and lo) per algorithmic product, attention runs on fp32 MFMA",
+        "first_token": int(am),
+        "decode_after_prompt_tok_s": round(PF_DECODE_TOKENS / (dec_ms * 1e-3), 1),
+    }
+
+
+def cpu_prefill_baseline(pkg, path, info):
+    """The reference --stage v2 prefill (oracle/_ref) on this host's cores over the first
+    PF_CPU_SAMPLE_TOKENS tokens of the 512-token prompt (a bounded sample: its cost per
+    token is the dense layers', as at 512 tokens): median of 3 runs after a warm-up."""
+    from oracle.bind import RefModel, ref_available
+
+    if not ref_available():
+        return None
+    threads = host_threads()
+    prompt = pkg.synth_prompt(info["seed"], PF_PROMPT_TOKENS, info["n_vocab"])[:PF_CPU_SAMPLE_TOKENS]
+    ref = RefModel(path, max_seq=PF_MAX_SEQ, kv_layout=0, n_threads=threads)
+    runs = []
+    for i in range(4):
+        ref.reset()
+        t0 = time.perf_counter()
+        ref.prefill(prompt)
+        if i:
+            runs.append(len(prompt) / (time.perf_counter() - t0))
+    ref.close()
+    return {
+        "value": round(statistics.median(runs), 2),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "reference",
+        "sample": f"reference --stage v2 prefill (oracle/_ref, {threads} threads) of the first "
+                  f"{PF_CPU_SAMPLE_TOKENS} tokens of the {PF_PROMPT_TOKENS}-token prompt, median of 3 runs "
+                  "after 1 warm-up",
+    }
 
 
 def cpu_baseline(path, prompt, n_decode, want_ids):
@@ -165,7 +258,10 @@ def main() -> int:
     # known-size copy: the reference dispatch for the HBM byte counters (FETCH_SIZE, WRITE_SIZE)
     copy_best, _ = pkg.copy_stream(COPY_CALIB_BYTES, iters=3)
 
+    pf = prefill_leg(pkg, path, info)
     cpu, match = (None, None) if args.no_cpu else cpu_baseline(path, prompt, K, ids)
+    if not args.no_cpu:
+        pf["cpu_baseline"] = cpu_prefill_baseline(pkg, path, info)
 
     out = {
         "metric": "decode tok/s & % of HBM roofline, Llama-3.2-1B-shape Q8_0, batch 1",
@@ -210,7 +306,8 @@ def main() -> int:
         "step_frac_of_read_stream": round(step_gbs / read_best, 4),
         "bytes_per_step": round(statistics.mean(step_bytes)),
         "device_ms_per_step": round(dev_ms / K, 4),
-        "prefill_tok_s": round(PROMPT_TOKENS / prefill_s, 1),
+        "prefill_6_tokens_wall_ms": round(prefill_s * 1e3, 3),
+        "prefill": pf,
         "decode_path": "persistent step kernel" if dpath == 1 else "graph",
         "graph_kernel_ms_by_class": {k: round(v[0] / K, 4) for k, v in prof.items()},
         "tokens_match_profile_pass": bool(list(ids) == list(ids_prof)),
