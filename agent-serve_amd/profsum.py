@@ -5,6 +5,7 @@
     python3 agent-serve_amd/profsum.py stepcounters <fetch counter_collection.csv> <write counter_collection.csv>
     python3 agent-serve_amd/profsum.py traffic <fetch counter_collection.csv> <write counter_collection.csv>
         --copy-bytes N
+    python3 agent-serve_amd/profsum.py prefill <kernel_trace.csv> --tokens N --dims D,F,L,H,G
 
 `trace` lists each kernel's calls and average / min duration from a --kernel-trace --stats
 run. `traffic` turns the FETCH_SIZE and WRITE_SIZE counters (KiB per dispatch, one
@@ -67,6 +68,49 @@ def step_counters(fetch_csv: str, write_csv: str) -> None:
     print(f"traffic_bytes_per_token k_step {fm * 1024 * 2.0 + wm * 1024 * 1.0:.0f}")
 
 
+def prefill(trace_csv: str, n: int, dims: str) -> None:
+    """Per kernel class of one prompt prefill (the k_pf_* dispatches of the trace): launches,
+    average and total microseconds, algorithmic FLOP per launch and TFLOP/s. Dense GEMM
+    FLOP are 2 per weight per row; attention's are q.k and p.v over i + 1 positions for
+    row i. The attn_output and ffn_down GEMMs share a kernel and alternate in launch order."""
+    D, F, L, H, G = (int(v) for v in dims.split(","))
+    hd = D // H
+    flop = {
+        "qkv_gemm": 2.0 * n * D * (H * hd + 2 * G * hd),
+        "wo_gemm": 2.0 * n * H * hd * D,
+        "gateup_gemm": 2.0 * n * D * 2 * F,
+        "down_gemm": 2.0 * n * F * D,
+        "attention": 4.0 * hd * (n * (n + 1) / 2) * H,
+    }
+    acc: dict[str, list[float]] = collections.defaultdict(list)
+    resid = 0
+    for r in csv.DictReader(open(trace_csv)):
+        k = r["Kernel_Name"]
+        if "k_pf_" not in k and "k_embed_rows" not in k:
+            continue
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if "k_pf_gemm_q8<0" in k:
+            c = "qkv_gemm"
+        elif "k_pf_gemm_q8<1" in k:
+            c = "wo_gemm" if resid % 2 == 0 else "down_gemm"
+            resid += 1
+        elif "k_pf_gemm_q8<2" in k:
+            c = "gateup_gemm"
+        elif "k_pf_attn" in k:
+            c = "attention"
+        else:
+            c = re.sub(r"^_ZN3tfk12_GLOBAL__N_1\d+", "", short(k)).split("(")[0].split("E")[0]
+        acc[c].append(us)
+    total = sum(sum(v) for v in acc.values())
+    print(f"prefill of {n} tokens, {L} layers: {total / 1e3:.3f} ms in k_pf_* kernels")
+    print(f"{'class':16s} {'calls':>6s} {'avg_us':>9s} {'total_ms':>9s} {'share':>6s} {'GFLOP/call':>11s} {'TFLOP/s':>8s}")
+    for c, v in sorted(acc.items(), key=lambda kv: -sum(kv[1])):
+        avg = sum(v) / len(v)
+        f = flop.get(c)
+        fs = f"{f / 1e9:11.2f} {f / (avg * 1e-6) / 1e12:8.1f}" if f else f"{'':11s} {'':8s}"
+        print(f"{c:16s} {len(v):6d} {avg:9.2f} {sum(v) / 1e3:9.3f} {sum(v) / total:6.1%} {fs}")
+
+
 def trace(path: str, steps: int | None) -> None:
     rows = list(csv.DictReader(open(path)))
     print(f"{'kernel':60s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'total_ms':>9s}")
@@ -109,13 +153,17 @@ def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> None:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["trace", "traffic", "steps", "stepcounters"])
+    ap.add_argument("what", choices=["trace", "traffic", "steps", "stepcounters", "prefill"])
     ap.add_argument("files", nargs="+")
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
+    ap.add_argument("--tokens", type=int, default=512)
+    ap.add_argument("--dims", default="2048,8192,16,32,8", help="D,F,L,H,G")
     a = ap.parse_args()
     if a.what == "trace":
         trace(a.files[0], a.steps)
+    elif a.what == "prefill":
+        prefill(a.files[0], a.tokens, a.dims)
     elif a.what == "stepcounters":
         step_counters(a.files[0], a.files[1])
     elif a.what == "steps":
