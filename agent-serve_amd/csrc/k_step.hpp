@@ -279,13 +279,14 @@ __device__ __forceinline__ int64_t kv_at(int layout, int G, int max_seq, int hd,
 
 // Attention of kv head g over positions [start, pos] (attn_decode, attention.cpp:55-80),
 // with the RoPE of its query heads and key (attention.cpp:31-46) and the KV store
-// (kvcache.cpp:31-36). qkv (LDS) holds the head block [n_rep q heads | k | v] as the QKV
-// phase left it; the output heads go to out (LDS, [n_rep][hd]). The same workgroup runs
-// head g for every token of a launch, so the rows it stores are the ones it later reads
-// on this CU.
-template <int HDM>
+// (kvcache.cpp:31-36). fetch() fills qkv (LDS) with the head block [n_rep q heads | k | v]
+// the QKV phase produced; it runs after the first K/V tile's loads are issued (the cached
+// rows do not depend on this token), so the cache latency overlaps the hand-off. The
+// output heads go to out (LDS, [n_rep][hd]). The same workgroup runs head g for every
+// token of a launch, so the rows it stores are the ones it later reads on this CU.
+template <int HDM, class Fetch>
 __device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly, int g, int pos, int start, float* qkv, float* sm,
-                          float* out) {
+                          float* out, Fetch&& fetch) {
     constexpr int kTV = (kTile * HDM / 4 + kT - 1) / kT;  // float4 of a K (or V) tile per thread
     constexpr int kPairs = (kMaxRep * HDM + kT - 1) / kT;  // (head, dim) pairs of P.V per thread
     const int hd = a.hd, d2 = hd / 2, hd4 = hd / 4;
@@ -317,6 +318,7 @@ __device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly
     };
     float4 kr_a[kTV], vr_a[kTV], kr_b[kTV], vr_b[kTV];
     load_tile(start, kr_a, vr_a);
+    fetch();
     // RoPE (rope_one, with the reference build's contractions)
     for (int i = tid; i < (n_rep + 1) * d2; i += kT) {
         const int r = i / d2, j = i % d2;
@@ -435,12 +437,19 @@ __host__ __device__ inline int region_floats(int D, int F, int n_rep, int hd, in
     return 2 * n_wg > r ? 2 * n_wg : r;
 }
 
+// LDS bytes of one wave's staged ffn_down row of K elements (Q8_0): the q bytes padded to
+// whole 1 KiB load instructions, then the fp16 scales padded to 256-byte ones.
+__host__ __device__ inline int down_slot_bytes(int K) {
+    return (K + 1023) / 1024 * 1024 + (K / 16 + 255) / 256 * 256;
+}
+
 // Launch constants, kept in LDS: phases re-read what they need after their barriers
 // instead of holding dozens of kernel-wide values in registers across the whole launch.
 struct StepConst {
     StepArgs a;
     int L, D, F, G, hd, n_rep, Hd, HB, nwg, P, attn_wg0;
     int o_xr, o_xs, o_x16, o_qkv, o_att;  // LDS byte offsets of the arrays below the layer table
+    int o_down, down_slot;                // staged ffn_down rows (o_down 0: not staged), bytes per wave
     uint32_t e0;
     int pos0;
     u64 key0;
@@ -483,6 +492,8 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         c.o_x16 = c.o_xs + 4 * kmax;
         c.o_qkv = c.o_xs + 4 * ((region_floats(c.D, c.F, c.n_rep, c.hd, c.nwg) + 3) / 4 * 4);
         c.o_att = c.o_qkv + 4 * c.HB;
+        c.o_down = args.down_lds ? (c.o_att + 4 * c.n_rep * c.hd + 15) / 16 * 16 : 0;
+        c.down_slot = down_slot_bytes(c.F);
         c.e0 = args.ctl->epoch;
         c.pos0 = args.ctl->pos;
         c.key0 = args.ctl->key;
@@ -509,6 +520,33 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
     auto no_bias = [](int) -> const float* { return nullptr; };
     const int n_tokens = args.n_tokens;
     int tok = 0;
+    // Wave wid's ffn_down row (row wid, when staged) into its LDS slot with direct
+    // global->LDS loads: lane i of a load lands at slot + 16 i (4 i for the scales). Lanes
+    // past the row's end re-read its last bytes; what they write past the row is never read.
+    auto issue_down = [&](const StepLayer& ly) {
+        if constexpr (TL == TF_HIP_TYPE_Q8_0) {
+            const int wid = wg * kNW + wave;
+            if (sc.o_down == 0 || wid >= (int)ly.wd.N) return;
+            const int K = sc.F;
+            const uint8_t* q = ly.wd.q + (int64_t)wid * K;
+            const uint8_t* d = ly.wd.s + (int64_t)wid * (K / 16);
+            unsigned char* slot = smem + sc.o_down + wave * sc.down_slot;
+            const int qsteps = (K + 1023) / 1024, dbytes = K / 16, dsteps = (dbytes + 255) / 256;
+            for (int i = 0; i < qsteps; ++i) {
+                int o = 1024 * i + 16 * lane;
+                o = o < K ? o : K - 16;
+                __builtin_amdgcn_global_load_lds((const TF_GLOBAL void*)(q + o),
+                                                 (__attribute__((address_space(3))) void*)(slot + 1024 * i), 16, 0, 0);
+            }
+            unsigned char* dslot = slot + qsteps * 1024;
+            for (int i = 0; i < dsteps; ++i) {
+                int o = 256 * i + 4 * lane;
+                o = o < dbytes ? o : dbytes - 4;
+                __builtin_amdgcn_global_load_lds((const TF_GLOBAL void*)(d + o),
+                                                 (__attribute__((address_space(3))) void*)(dslot + 256 * i), 4, 0, 0);
+            }
+        }
+    };
 
     for (int t = 0; t < n_tokens; ++t) {
         const bool last = t == n_tokens - 1;
@@ -589,50 +627,66 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 gemv_phase<TL, 1, GEMV_STORE, 2>(3, groups, seg, bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
                                                  prep, epi);
             }
-            // ---- 2: attention (kv head g on workgroup attn_wg0 + g)
-            if (wg >= sc.attn_wg0) {
-                const int g = wg - sc.attn_wg0;
-                const int HB = sc.HB;
-                float* qkv = (float*)(smem + sc.o_qkv);
-                float* att_out = (float*)(smem + sc.o_att);
-                __syncthreads();  // the QKV phase's waves are done with xs
-                gather<kGD, 1>(X(sc.QKV) + par * sc.G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0, sc.a.ctl);
-                __syncthreads();
-                attn_head<HDM>(sc.a, ly, g, sc.pos0 + t, sc.a.att_start, qkv, xs, att_out);
-                const int nh = sc.n_rep * sc.hd;
-                for (int i = tid; i < nh; i += kT) put(X(sc.ATT) + par * sc.Hd + g * nh + i, att_out[i], E(t, l, 2));
-            } else {
-                // ---- 3: wo + residual (workgroups without an attention head)
-                const int Hd = sc.Hd;
-                float wr[1];
-                const int groups[3] = {(int)ly.wo.N, 0, 0};
-                auto seg = [&](int, int) -> const DevMat& { return ly.wo; };
-                auto prep = [&]() {
-                    gather<kGD, 1>(X(sc.ATT) + par * Hd, Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl);
-                    stage(xs, Hd, false, wr, 0.0f, xs, x16, Fmt<TL>::kNeedSums, red);
-                };
-                auto epi = [&](int, int row, float v, float, float) {
-                    put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
-                };
-                gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, Hd, wg * kNW + wave, sc.attn_wg0 * kNW,
-                                                 xs, x16, prep, epi);
-            }
-            // ---- 4: gate/up (ffn_norm fused), SiLU(gate) * up
+            // ---- 2: attention (kv head g on workgroup attn_wg0 + g), then 4: gate/up
+            // ---- 3: wo + residual (workgroups without an attention head), then 4: gate/up
+            // The workgroups without an attention head issue their gate/up tiles and stage
+            // their ffn_down row before they wait for the attention output: cfg1's 50 MB of
+            // gate/up and down stream in while attention runs, instead of after wo. (Giving
+            // the attention workgroups wo rows too makes them the stragglers of wo.)
             {
                 const int D = sc.D;
                 float wr[NWR];
                 load_norm(ly.ffn_norm, D, wr);
-                const int groups[3] = {(int)((ly.wg.N + 1) / 2), 0, 0};
-                auto seg = [&](int, int what) -> const DevMat& { return what == 1 ? ly.wu : ly.wg; };
-                auto prep = [&]() {
+                const int gu_groups[3] = {(int)((ly.wg.N + 1) / 2), 0, 0};
+                auto gu_seg = [&](int, int what) -> const DevMat& { return what == 1 ? ly.wu : ly.wg; };
+                auto gu_epi = [&](int, int row, float v, float up, float) {
+                    put(X(sc.HH) + par * sc.F + row, (v / (1.0f + expf(-v))) * up, E(t, l, 4));
+                };
+                auto gu_input = [&]() {
                     gather<kGD, 1>(X(sc.XB) + par * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl);
                     stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
                 };
-                auto epi = [&](int, int row, float v, float up, float) {
-                    put(X(sc.HH) + par * sc.F + row, (v / (1.0f + expf(-v))) * up, E(t, l, 4));
-                };
-                gemv_phase<TL, 2, GEMV_SILU, 2>(1, groups, seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
-                                                prep, epi);
+                if (wg >= sc.attn_wg0) {
+                    const int g = wg - sc.attn_wg0;
+                    const int HB = sc.HB;
+                    float* qkv = (float*)(smem + sc.o_qkv);
+                    float* att_out = (float*)(smem + sc.o_att);
+                    __syncthreads();  // the QKV phase's waves are done with xs
+                    attn_head<HDM>(sc.a, ly, g, sc.pos0 + t, sc.a.att_start, qkv, xs, att_out, [&]() {
+                        gather<kGD, 1>(X(sc.QKV) + par * sc.G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0,
+                                       sc.a.ctl);
+                        __syncthreads();
+                    });
+                    const int nh = sc.n_rep * sc.hd;
+                    for (int i = tid; i < nh; i += kT) put(X(sc.ATT) + par * sc.Hd + g * nh + i, att_out[i], E(t, l, 2));
+                    auto down_then_input = [&]() {
+                        issue_down(ly);
+                        gu_input();
+                    };
+                    gemv_phase<TL, 2, GEMV_SILU, 2>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                                                    x16, down_then_input, gu_epi);
+                } else {
+                    auto wo_then_input = [&]() {
+                        issue_down(ly);
+                        const int Hd = sc.Hd;
+                        float wo_wr[1];
+                        const int groups[3] = {(int)ly.wo.N, 0, 0};
+                        auto seg = [&](int, int) -> const DevMat& { return ly.wo; };
+                        auto prep = [&]() {
+                            gather<kGD, 1>(X(sc.ATT) + par * Hd, Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl);
+                            stage(xs, Hd, false, wo_wr, 0.0f, xs, x16, Fmt<TL>::kNeedSums, red);
+                        };
+                        auto epi = [&](int, int row, float v, float, float) {
+                            put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
+                        };
+                        gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, Hd, wg * kNW + wave,
+                                                         sc.attn_wg0 * kNW, xs, x16, prep, epi);
+                        __syncthreads();  // every wave's wo rows are read out of xs before the input is staged
+                        gu_input();
+                    };
+                    gemv_phase<TL, 2, GEMV_SILU, 2>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                                                    x16, wo_then_input, gu_epi);
+                }
             }
             // ---- 5: down + residual
             {
@@ -649,8 +703,35 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     put(X(sc.XA) + par * sc.D + row, nv, E(t, l, 5));
                     if (last && sc.a.taps) *gptr(sc.a.taps + (size_t)l * sc.D + row) = nv;
                 };
-                gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, F, wg * kNW + wave, sc.nwg * kNW, xs, x16,
-                                                 prep, epi);
+                bool staged = false;
+                if constexpr (TL == TF_HIP_TYPE_Q8_0) {
+                    if (sc.o_down) {
+                        // the row was staged in LDS during gate/up: the same lane steps and
+                        // order as gemv_phase's, read from the wave's slot
+                        staged = true;
+                        __syncthreads();
+                        prep();
+                        const int wid = wg * kNW + wave;
+                        if (wid < (int)ly.wd.N) {
+                            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS loads have landed
+                            using F8 = Fmt<TL>;
+                            const unsigned char* slot = smem + sc.o_down + wave * sc.down_slot;
+                            const uint16_t* dsl = (const uint16_t*)(slot + (F + 1023) / 1024 * 1024);
+                            float acc = 0.0f;
+                            for (int s = lane; s < F / 16; s += kWave) {
+                                typename F8::Raw w;
+                                w.q = *(const uint4*)(slot + 16 * s);
+                                w.d = dsl[s >> 1];
+                                acc += F8::dot(w, xs, x16, s);
+                            }
+                            acc = wave_sum(acc);
+                            if (lane == 0) epi(0, wid, acc, 0.0f, 0.0f);
+                        }
+                    }
+                }
+                if (!staged)
+                    gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, F, wg * kNW + wave, sc.nwg * kNW, xs,
+                                                     x16, prep, epi);
                 __syncthreads();
                 if (tid == 0) put(X(sc.DONE) + par * sc.nwg + wg, 0.0f, E(t, l, 5));
             }
