@@ -54,15 +54,15 @@ def step_dispatches(trace_csv: str) -> list[float]:
 
 def step_counters(fetch_csv: str, write_csv: str) -> None:
     """HBM bytes per decode token of the persistent step kernel from a run of the CLI
-    (one launch for the prompt, then one launch per decoded token): the median over the
-    single-token launches, FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0 (the factors
-    k_copy_stream of a known size gives these counters on MI355X)."""
+    (the prompt on the matrix cores, then one step-kernel launch per decoded token): the
+    median over the launches after the first, FETCH_SIZE scaled by 2.0 and WRITE_SIZE by
+    1.0 (the factors k_copy_stream of a known size gives these counters on MI355X)."""
     def vals(p, c):
         return [float(r["Counter_Value"]) for r in csv.DictReader(open(p))
                 if r["Counter_Name"] == c and "k_step" in r["Kernel_Name"]]
     f, w = vals(fetch_csv, "FETCH_SIZE"), vals(write_csv, "WRITE_SIZE")
     fm, wm = sorted(f[1:])[len(f[1:]) // 2], sorted(w[1:])[len(w[1:]) // 2]
-    print(f"k_step dispatches: {len(f)} (first = prompt, then one per decoded token)")
+    print(f"k_step dispatches: {len(f)} (one per decoded token; the first, a cold start, is left out of the medians)")
     print(f"decode dispatches: FETCH_SIZE median {fm:.0f} KiB (min {min(f[1:]):.0f}, max {max(f[1:]):.0f}), "
           f"WRITE_SIZE median {wm:.0f} KiB (min {min(w[1:]):.0f}, max {max(w[1:]):.0f})")
     print(f"traffic_bytes_per_token k_step {fm * 1024 * 2.0 + wm * 1024 * 1.0:.0f}")
