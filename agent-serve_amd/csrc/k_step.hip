@@ -12,24 +12,25 @@ size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg) {
                 2 * (size_t)n_wg);
 }
 
-size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg, int down_lds) {
+size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg, int stage_lds) {
     const int n_rep = H / G;
     const int region = step_detail::region_floats(D, F, n_rep, hd, n_wg);
     const size_t table = ((size_t)n_layer * sizeof(StepLayer) + 15) / 16 * 16;
     const size_t floats = (size_t)(D + 3) / 4 * 4 + (size_t)(region + 3) / 4 * 4 + (size_t)(n_rep + 2) * hd +
                           (size_t)n_rep * hd;
-    const size_t down = down_lds ? 16 + (size_t)step_detail::kNW * step_detail::down_slot_bytes(F) : 0;
-    return table + 4 * floats + down;
+    const size_t staged = (stage_lds & 1) ? 16 + (size_t)step_detail::kNW * step_detail::row_slot_bytes(F) : 0;
+    return table + 4 * floats + staged;
 }
 
-bool step_down_lds(int tl, int n_layer, int D, int F, int H, int G, int hd, int n_wg) {
-    if (tl != TF_HIP_TYPE_Q8_0 || D > n_wg * step_detail::kNW || F % 32 != 0) return false;
+int step_stage_lds(int tl, int n_layer, int D, int F, int H, int G, int hd, int n_wg) {
+    if (tl != TF_HIP_TYPE_Q8_0 || F % 32 != 0 || D % 32 != 0 || D < 64 || F < 64) return 0;
     int dev = 0, max_lds = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-        return false;
+        return 0;
+    if (D > n_wg * step_detail::kNW) return 0;
     // the kernel's static LDS (StepConst, reductions) stays under 2 KiB
-    return step_lds_bytes(n_layer, D, F, H, G, hd, n_wg, 1) + 2048 <= (size_t)max_lds;
+    return step_lds_bytes(n_layer, D, F, H, G, hd, n_wg, 1) + 2048 <= (size_t)max_lds ? 1 : 0;
 }
 
 namespace {
@@ -37,7 +38,7 @@ namespace {
 template <int TL, int TO, int HDM>
 hipError_t launch_t(const StepArgs& a, int n_wg, hipStream_t st) {
     const void* fn = (const void*)step_detail::k_step<TL, TO, HDM>;
-    const size_t lds = step_lds_bytes(a.n_layer, a.D, a.F, a.H, a.G, a.hd, n_wg, a.down_lds);
+    const size_t lds = step_lds_bytes(a.n_layer, a.D, a.F, a.H, a.G, a.hd, n_wg, a.stage_lds);
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     int per_cu = 0;

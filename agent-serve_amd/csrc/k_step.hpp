@@ -437,9 +437,9 @@ __host__ __device__ inline int region_floats(int D, int F, int n_rep, int hd, in
     return 2 * n_wg > r ? 2 * n_wg : r;
 }
 
-// LDS bytes of one wave's staged ffn_down row of K elements (Q8_0): the q bytes padded to
-// whole 1 KiB load instructions, then the fp16 scales padded to 256-byte ones.
-__host__ __device__ inline int down_slot_bytes(int K) {
+// LDS bytes of one staged Q8_0 row of K elements: the q bytes padded to whole 1 KiB load
+// instructions, then the fp16 scales padded to 256-byte ones.
+__host__ __device__ inline int row_slot_bytes(int K) {
     return (K + 1023) / 1024 * 1024 + (K / 16 + 255) / 256 * 256;
 }
 
@@ -492,8 +492,8 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         c.o_x16 = c.o_xs + 4 * kmax;
         c.o_qkv = c.o_xs + 4 * ((region_floats(c.D, c.F, c.n_rep, c.hd, c.nwg) + 3) / 4 * 4);
         c.o_att = c.o_qkv + 4 * c.HB;
-        c.o_down = args.down_lds ? (c.o_att + 4 * c.n_rep * c.hd + 15) / 16 * 16 : 0;
-        c.down_slot = down_slot_bytes(c.F);
+        c.down_slot = row_slot_bytes(c.F);
+        c.o_down = (args.stage_lds & 1) ? (c.o_att + 4 * c.n_rep * c.hd + 15) / 16 * 16 : 0;
         c.e0 = args.ctl->epoch;
         c.pos0 = args.ctl->pos;
         c.key0 = args.ctl->key;
@@ -520,31 +520,47 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
     auto no_bias = [](int) -> const float* { return nullptr; };
     const int n_tokens = args.n_tokens;
     int tok = 0;
-    // Wave wid's ffn_down row (row wid, when staged) into its LDS slot with direct
-    // global->LDS loads: lane i of a load lands at slot + 16 i (4 i for the scales). Lanes
-    // past the row's end re-read its last bytes; what they write past the row is never read.
+    // Staged weight rows: a wave copies a Q8_0 row (q bytes, then fp16 scales) into an LDS
+    // slot of its own with direct global->LDS loads, ahead of the phase that reads it: lane
+    // i of a load lands at slot + 16 i (4 i for the scales). Lanes past the row's end re-read
+    // its last bytes; what they write past the row is never read.
+    auto stage_row = [&](const uint8_t* q, const uint8_t* d, int K, unsigned char* slot) {
+        const int qsteps = (K + 1023) / 1024, dbytes = K / 16, dsteps = (dbytes + 255) / 256;
+        for (int i = 0; i < qsteps; ++i) {
+            int o = 1024 * i + 16 * lane;
+            o = o < K ? o : K - 16;
+            __builtin_amdgcn_global_load_lds((const TF_GLOBAL void*)(q + o),
+                                             (__attribute__((address_space(3))) void*)(slot + 1024 * i), 16, 0, 0);
+        }
+        unsigned char* dslot = slot + qsteps * 1024;
+        for (int i = 0; i < dsteps; ++i) {
+            int o = 256 * i + 4 * lane;
+            o = o < dbytes ? o : dbytes - 4;
+            __builtin_amdgcn_global_load_lds((const TF_GLOBAL void*)(d + o),
+                                             (__attribute__((address_space(3))) void*)(dslot + 256 * i), 4, 0, 0);
+        }
+    };
+    // Dot of the staged row in `slot` with xs, in gemv_phase's lane-step order and reduction.
+    auto staged_dot = [&](const unsigned char* slot, int K) -> float {
+        using F8 = Fmt<TF_HIP_TYPE_Q8_0>;
+        const uint16_t* dsl = (const uint16_t*)(slot + (K + 1023) / 1024 * 1024);
+        float acc = 0.0f;
+        for (int s = lane; s < K / 16; s += kWave) {
+            typename F8::Raw w;
+            w.q = *(const uint4*)(slot + 16 * s);
+            w.d = dsl[s >> 1];
+            acc += F8::dot(w, xs, x16, s);
+        }
+        return wave_sum(acc);
+    };
+    // Wave wid's ffn_down row: row wid.
     auto issue_down = [&](const StepLayer& ly) {
         if constexpr (TL == TF_HIP_TYPE_Q8_0) {
             const int wid = wg * kNW + wave;
             if (sc.o_down == 0 || wid >= (int)ly.wd.N) return;
             const int K = sc.F;
-            const uint8_t* q = ly.wd.q + (int64_t)wid * K;
-            const uint8_t* d = ly.wd.s + (int64_t)wid * (K / 16);
-            unsigned char* slot = smem + sc.o_down + wave * sc.down_slot;
-            const int qsteps = (K + 1023) / 1024, dbytes = K / 16, dsteps = (dbytes + 255) / 256;
-            for (int i = 0; i < qsteps; ++i) {
-                int o = 1024 * i + 16 * lane;
-                o = o < K ? o : K - 16;
-                __builtin_amdgcn_global_load_lds((const TF_GLOBAL void*)(q + o),
-                                                 (__attribute__((address_space(3))) void*)(slot + 1024 * i), 16, 0, 0);
-            }
-            unsigned char* dslot = slot + qsteps * 1024;
-            for (int i = 0; i < dsteps; ++i) {
-                int o = 256 * i + 4 * lane;
-                o = o < dbytes ? o : dbytes - 4;
-                __builtin_amdgcn_global_load_lds((const TF_GLOBAL void*)(d + o),
-                                                 (__attribute__((address_space(3))) void*)(dslot + 256 * i), 4, 0, 0);
-            }
+            stage_row(ly.wd.q + (int64_t)wid * K, ly.wd.s + (int64_t)wid * (K / 16), K,
+                      smem + sc.o_down + wave * sc.down_slot);
         }
     };
 
@@ -713,18 +729,10 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         prep();
                         const int wid = wg * kNW + wave;
                         if (wid < (int)ly.wd.N) {
-                            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS loads have landed
-                            using F8 = Fmt<TL>;
-                            const unsigned char* slot = smem + sc.o_down + wave * sc.down_slot;
-                            const uint16_t* dsl = (const uint16_t*)(slot + (F + 1023) / 1024 * 1024);
-                            float acc = 0.0f;
-                            for (int s = lane; s < F / 16; s += kWave) {
-                                typename F8::Raw w;
-                                w.q = *(const uint4*)(slot + 16 * s);
-                                w.d = dsl[s >> 1];
-                                acc += F8::dot(w, xs, x16, s);
-                            }
-                            acc = wave_sum(acc);
+                            // this wave's loads complete in order and the exchange loads of prep
+                            // came after the staged row: this wait is already satisfied
+                            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                            const float acc = staged_dot(smem + sc.o_down + wave * sc.down_slot, F);
                             if (lane == 0) epi(0, wid, acc, 0.0f, 0.0f);
                         }
                     }

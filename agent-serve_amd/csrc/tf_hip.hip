@@ -505,7 +505,7 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
     a.greedy = greedy;
     a.lm_every = lm_every;
     a.att_start = att_start;
-    a.down_lds = step_down_lds(c->step_tl, p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, c->n_wg);
+    a.stage_lds = step_stage_lds(c->step_tl, p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, c->n_wg);
     const hipError_t e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);
     if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("step kernel launch: ") + hipGetErrorString(e));
     c->epoch += (uint32_t)(n * (6 * p.n_layer + 8));

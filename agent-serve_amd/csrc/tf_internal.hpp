@@ -141,7 +141,7 @@ struct StepArgs {
     int greedy;                // 0: tokens from hist (prefill, decode); 1: each token is the previous argmax
     int lm_every;              // 1: lm_head for every token; 0: for the last one only (prefill)
     int att_start;             // first cache position attention covers (0, or the prefill chunk's start)
-    int down_lds;              // 1: each wave's ffn_down row is staged in LDS (see step_down_lds)
+    int stage_lds;             // bit 0: ffn_down rows staged in LDS (step_stage_lds)
 };
 
 // ---------------------------------------------------------------- prefill on the matrix cores
@@ -200,10 +200,12 @@ hipError_t launch_pf_tail(Ctl* ctl, int pos_last, const int32_t* hist, const flo
                           hipStream_t st);
 
 size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg);
-size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg, int down_lds);
-// Whether the step kernel stages ffn_down rows in LDS: Q8_0 layers, one row per wave at
-// most, and the LDS for it.
-bool step_down_lds(int type_layers, int n_layer, int D, int F, int H, int G, int hd, int n_wg);
+size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg, int stage_lds);
+// Which weight rows the step kernel stages in LDS ahead of their phase (bits of
+// StepArgs::stage_lds): the ffn_down rows (bit 0) for Q8_0 layers with at most one row per
+// wave and the LDS for them. (Staging the next layer's QKV rows as well was measured: the
+// exchange that waits behind their loads loses what the QKV phase gains.)
+int step_stage_lds(int type_layers, int n_layer, int D, int F, int H, int G, int hd, int n_wg);
 // true when the model's formats and head size have a compiled step kernel.
 bool step_supported(int type_layers, int type_out, int hd);
 hipError_t launch_step(const StepArgs& a, int type_layers, int type_out, int n_wg, hipStream_t st);

@@ -16,7 +16,8 @@ kernel-by-kernel pass over the same steps on the graph path gives the per-class 
 on this host's cores over the same prompt and steps. `prefill` is the 512-token prompt
 workload of the same model on the matrix cores: tok/s from HIP events around the call,
 algorithmic TFLOP/s and their fraction of the dense fp16 MFMA peak, the decode rate
-after the prompt, and the reference CPU prefill on a bounded sample.
+after the prompt, and the reference CPU prefill on a bounded sample. `context_sweep` is the
+decode rate after prompts of 512..4000 tokens in a 4096-position cache (graph path).
 """
 from __future__ import annotations
 
@@ -49,6 +50,10 @@ PF_MAX_SEQ = 1024
 PF_REPS = 5
 PF_CPU_SAMPLE_TOKENS = 64
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X
+# context sweep: decode after prompts of these lengths, cache of CTX_MAX_SEQ positions
+CTX_PROMPTS = (512, 1024, 2048, 4000)
+CTX_MAX_SEQ = 4096
+CTX_STEPS = 16
 
 
 def host_threads() -> int:
@@ -133,6 +138,29 @@ def prefill_leg(pkg, path, info):
         "first_token": int(am),
         "decode_after_prompt_tok_s": round(PF_DECODE_TOKENS / (dec_ms * 1e-3), 1),
     }
+
+
+def context_sweep(pkg, path, info):
+    """Decode rate by context length (the sweep the reference's roofline.py reads as
+    bench "context" and its runs never produced): per prompt length, a prefill from a
+    reset, then CTX_STEPS greedy tokens timed by HIP events; GB/s counts the weights once
+    and the KV rows of every position read (tf_hip_decode_bytes)."""
+    m = pkg.HipModel(path, max_seq=CTX_MAX_SEQ, kv_layout=0)
+    out = []
+    for n in CTX_PROMPTS:
+        prompt = pkg.synth_prompt(info["seed"] + n, n, info["n_vocab"])
+        m.reset()
+        m.prefill(prompt, want_logits=False)
+        pf_ms = m.last_timing()[0]
+        m.generate(CTX_STEPS)
+        ms, _, _, name = m.last_timing()
+        b = sum(m.decode_bytes(n + i) for i in range(CTX_STEPS))
+        out.append({"context": n, "decode_tok_s": round(CTX_STEPS / (ms * 1e-3), 1),
+                    "decode_gb_s": round(b / (ms * 1e-3) / 1e9, 1), "decode_path": name,
+                    "kv_bytes_per_token": int(m.decode_bytes(n) - m.decode_bytes(0)),
+                    "prefill_tok_s": round(n / (pf_ms * 1e-3), 1)})
+    m.close()
+    return {"max_seq": CTX_MAX_SEQ, "steps": CTX_STEPS, "points": out}
 
 
 def cpu_prefill_baseline(pkg, path, info):
@@ -259,6 +287,7 @@ def main() -> int:
     copy_best, _ = pkg.copy_stream(COPY_CALIB_BYTES, iters=3)
 
     pf = prefill_leg(pkg, path, info)
+    ctx = context_sweep(pkg, path, info)
     cpu, match = (None, None) if args.no_cpu else cpu_baseline(path, prompt, K, ids)
     if not args.no_cpu:
         pf["cpu_baseline"] = cpu_prefill_baseline(pkg, path, info)
@@ -308,6 +337,7 @@ def main() -> int:
         "device_ms_per_step": round(dev_ms / K, 4),
         "prefill_6_tokens_wall_ms": round(prefill_s * 1e3, 3),
         "prefill": pf,
+        "context_sweep": ctx,
         "decode_path": "persistent step kernel" if dpath == 1 else "graph",
         "graph_kernel_ms_by_class": {k: round(v[0] / K, 4) for k, v in prof.items()},
         "tokens_match_profile_pass": bool(list(ids) == list(ids_prof)),
