@@ -65,83 +65,96 @@ __global__ __launch_bounds__(kBlock) void k_pf_pack_q8(const uint8_t* q, int K, 
     }
 }
 
-// Row statistics, one wave per row: the rmsnorm scale inv (when w is given) and a power
-// of two sc putting max |row| in [2^14, 2^15); rs = 1 / sc. Rows M.. get sc = rs = 0.
-__global__ __launch_bounds__(kBlock) void k_pf_rowstats(const float* x, int64_t ldx, const float* w, float eps,
-                                                        int K, int M, float* st /* [Mpad][2]: inv, sc */,
-                                                        float* rs) {
-    const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-    const int K4 = K / 4;
-    const float4* wr = (const float4*)w;
-    float inv = 1.0f, sc = 0.0f, rsv = 0.0f;
-    if (m < M) {
-        const float4* xr = (const float4*)(x + (int64_t)m * ldx);
-        if (w) {
-            double ss = 0;
-            for (int k = lane; k < K4; k += 64) {
-                const float4 v = xr[k];
-                ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-            }
-            ss = wave_sum_d(ss);
-            inv = 1.0f / sqrtf((float)(ss / K) + eps);
-        }
-        float amax = 0.0f;
-        for (int k = lane; k < K4; k += 64) {
-            float4 v = xr[k];
-            if (w) {
-                const float4 g = wr[k];
-                v = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
-            }
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        }
-        amax = wave_max(amax);
-        int ex = 0;
-        (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
-        int e = amax > 0.0f ? 15 - ex : 0;
-        e = e < -100 ? -100 : (e > 100 ? 100 : e);
-        sc = ldexpf(1.0f, e);
-        rsv = ldexpf(1.0f, -e);
-    }
-    if (lane == 0) {
-        st[2 * m] = inv;
-        st[2 * m + 1] = sc;
-        rs[m] = rsv;
-    }
-}
+constexpr int kSplitGroups = 8;  // 8-element groups per thread: rows up to 256 * 8 * 8 = 16384
 
-// Every element as hi + lo in fragment order: grid (row tiles, groups of 4 blocks); a
-// thread writes one lane's 16 bytes of a hi and a lo fragment.
-__global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx, const float* w, int K, int M,
-                                                     const float* st, h8_t* xa) {
-    const int T = blockIdx.x, nblk = K / 32;
-    const int b = blockIdx.y * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
-    if (b >= nblk) return;
-    const int r = l & 15, m = T * 16 + r;
-    const int k0 = 32 * b + 8 * (l >> 4);
-    h8_t hi = {0, 0, 0, 0, 0, 0, 0, 0}, lo = hi;
-    if (m < M) {
-        const float4* xr = (const float4*)(x + (int64_t)m * ldx + k0);
-        const float4 v0 = xr[0], v1 = xr[1];
-        float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        const float inv = st[2 * m], sc = st[2 * m + 1];
-        if (w) {
-            const float4* wr = (const float4*)(w + k0);
-            const float4 g0 = wr[0], g1 = wr[1];
-            const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = v[j] * inv * g[j];
+// One workgroup per row, the row held in registers (thread t owns the 8-element groups
+// t, t + 256, ...): the rmsnorm scale inv (when w is given), a power of two sc putting
+// max |row| in [2^14, 2^15) (rs = 1 / sc), then every element as hi + lo into the
+// fragment layout (16 bytes of a hi and of a lo fragment per group). Rows M.. are zeros
+// with rs = 0.
+__global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx, const float* w, float eps, int K,
+                                                     int M, h8_t* xa, float* rs) {
+    __shared__ double red_d[kWavesPerBlock];
+    __shared__ float red_f[kWavesPerBlock];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const int ng = K / 8, nblk = K / 32;
+    h8_t* tile = xa + (int64_t)(m / 16) * nblk * 128 + (m % 16);
+    if (m >= M) {
+        const h8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int j = tid; j < ng; j += kBlock) {
+            h8_t* o = tile + (j / 4) * 128 + 16 * (j % 4);
+            o[0] = z;
+            o[64] = z;
         }
+        if (tid == 0) rs[m] = 0.0f;
+        return;
+    }
+    const float4* xr = (const float4*)(x + (int64_t)m * ldx);
+    const float4* wr = (const float4*)w;
+    float v[kSplitGroups][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float t = v[j] * sc;
-            hi[j] = (_Float16)t;
-            lo[j] = (_Float16)(t - (float)hi[j]);
+    for (int i = 0; i < kSplitGroups; ++i) {
+        const int j = tid + i * kBlock;
+        const int jj = j < ng ? j : ng - 1;  // a clamped re-read, masked below
+        const float4 a = xr[2 * jj], b = xr[2 * jj + 1];
+        v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+        v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+    }
+    float inv = 1.0f;
+    if (w) {
+        double ss = 0;
+#pragma unroll
+        for (int i = 0; i < kSplitGroups; ++i)
+            if (tid + i * kBlock < ng)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += (double)v[i][e] * v[i][e];
+        ss = wave_sum_d(ss);
+        if ((tid & 63) == 0) red_d[tid >> 6] = ss;
+        __syncthreads();
+        ss = (red_d[0] + red_d[1]) + (red_d[2] + red_d[3]);
+        inv = 1.0f / sqrtf((float)(ss / K) + eps);
+#pragma unroll
+        for (int i = 0; i < kSplitGroups; ++i) {
+            int j = tid + i * kBlock;
+            j = j < ng ? j : ng - 1;
+            const float4 a = wr[2 * j], b = wr[2 * j + 1];
+            const float g[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[i][e] = v[i][e] * inv * g[e];
         }
     }
-    h8_t* out = xa + ((int64_t)T * nblk + b) * 128;
-    out[l] = hi;
-    out[64 + l] = lo;
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSplitGroups; ++i)
+        if (tid + i * kBlock < ng)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+    amax = wave_max(amax);
+    if ((tid & 63) == 0) red_f[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    int ex = 0;
+    (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
+    int e2 = amax > 0.0f ? 15 - ex : 0;
+    e2 = e2 < -100 ? -100 : (e2 > 100 ? 100 : e2);
+    const float sc = ldexpf(1.0f, e2);
+    if (tid == 0) rs[m] = ldexpf(1.0f, -e2);
+#pragma unroll
+    for (int i = 0; i < kSplitGroups; ++i) {
+        const int j = tid + i * kBlock;
+        if (j < ng) {
+            h8_t hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float t = v[i][e] * sc;
+                hi[e] = (_Float16)t;
+                lo[e] = (_Float16)(t - (float)hi[e]);
+            }
+            h8_t* o = tile + (j / 4) * 128 + 16 * (j % 4);
+            o[0] = hi;
+            o[64] = lo;
+        }
+    }
 }
 
 // ---------------------------------------------------------------- Q8_0 GEMM
@@ -384,35 +397,34 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
     for (int d = 0; d < NT; ++d) ot[d] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    for (int kt = att_start; kt <= k_hi; kt += 16) {
-        // K rows: lane's key kt + l16, dims grp*DQ ..
-        float kv[DQ];
-        {
-            int key = kt + l16;
-            key = key <= k_hi ? key : k_hi;
-            const float* kr = kc + kv_offset(layout, G, max_seq, HD, g, key) + grp * DQ;
+    // K rows (lane's key kt + l16, dims grp*DQ ..) and V scalars (MFMA r of dim tile d
+    // needs V[kt + 4 grp + r][16 d + l16]) of the tile at kt; keys past k_hi re-read key
+    // k_hi (masked). The next tile's loads are issued before the current tile's MFMAs.
+    auto load_kv = [&](int kt, float (&kv_)[DQ], float (&vv_)[4][NT]) {
+        int key = kt + l16;
+        key = key <= k_hi ? key : k_hi;
+        const float* kr = kc + kv_offset(layout, G, max_seq, HD, g, key) + grp * DQ;
 #pragma unroll
-            for (int s = 0; s < DQ; s += 4) {
-                const float4 t = gload_f4(kr + s);
-                kv[s] = t.x;
-                kv[s + 1] = t.y;
-                kv[s + 2] = t.z;
-                kv[s + 3] = t.w;
-            }
+        for (int s = 0; s < DQ; s += 4) {
+            const float4 t = gload_f4(kr + s);
+            kv_[s] = t.x;
+            kv_[s + 1] = t.y;
+            kv_[s + 2] = t.z;
+            kv_[s + 3] = t.w;
         }
-        // V scalars: MFMA r of dim tile d needs V[kt + 4 grp + r][16 d + l16]
-        float vv[4][NT];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            int key = kt + 4 * grp + r;
-            key = key <= k_hi ? key : k_hi;
-            const float* vr = vc + kv_offset(layout, G, max_seq, HD, g, key) + l16;
+            int vkey = kt + 4 * grp + r;
+            vkey = vkey <= k_hi ? vkey : k_hi;
+            const float* vr = vc + kv_offset(layout, G, max_seq, HD, g, vkey) + l16;
 #pragma unroll
-            for (int d = 0; d < NT; ++d) vv[r][d] = *gptr(vr + 16 * d);
+            for (int d = 0; d < NT; ++d) vv_[r][d] = *gptr(vr + 16 * d);
         }
+    };
+    auto tile = [&](int kt, const float (&kv_)[DQ], const float (&vv_)[4][NT]) {
         f4_t st = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s = 0; s < DQ; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[s], qv[s], st, 0, 0, 0);
+        for (int s = 0; s < DQ; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kv_[s], qv[s], st, 0, 0, 0);
         float p[4];
         float mt = -INFINITY;
 #pragma unroll
@@ -439,9 +451,20 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
         for (int d = 0; d < NT; ++d) {
             f4_t o = ot[d] * alpha;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r][d], p[r], o, 0, 0, 0);
+            for (int r = 0; r < 4; ++r) o = __builtin_amdgcn_mfma_f32_16x16x4f32(vv_[r][d], p[r], o, 0, 0, 0);
             ot[d] = o;
         }
+    };
+    float kva[DQ], vva[4][NT], kvb[DQ], vvb[4][NT];
+    load_kv(att_start, kva, vva);
+    for (int kt = att_start; kt <= k_hi;) {
+        load_kv(kt + 16, kvb, vvb);
+        tile(kt, kva, vva);
+        kt += 16;
+        if (kt > k_hi) break;
+        load_kv(kt + 16, kva, vva);
+        tile(kt, kvb, vvb);
+        kt += 16;
     }
     // lane holds O[query l16][dims 16 d + 4 grp + 0..3]; the 4 lanes of a query share l_run
     if (qi < n) {
@@ -468,16 +491,14 @@ __global__ __launch_bounds__(kBlock) void k_pf_tail(Ctl* ctl, int pos_last, cons
 }  // namespace
 
 bool pf_gemm_supported(int type, int64_t K, int64_t N) {
-    return type == TF_HIP_TYPE_Q8_0 && K % 64 == 0 && N % 16 == 0 && K <= (1 << 20);
+    return type == TF_HIP_TYPE_Q8_0 && K % 64 == 0 && N % 16 == 0 && K <= kBlock * 8 * kSplitGroups;
 }
 
 hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,
-                           uint16_t* xa, float* rs, float* st, hipStream_t s) {
-    if (K % 32 != 0 || ldx % 4 != 0 || Mpad % kPfTileM != 0 || M > Mpad) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_rowstats, dim3(Mpad / kWavesPerBlock), dim3(kBlock), 0, s, x, ldx, norm_w, eps, K, M, st,
-                       rs);
-    hipLaunchKernelGGL(k_pf_split, dim3(Mpad / 16, (K / 32 + 3) / 4), dim3(kBlock), 0, s, x, ldx, norm_w, K, M, st,
-                       (h8_t*)xa);
+                           uint16_t* xa, float* rs, hipStream_t st) {
+    if (K % 32 != 0 || K > kBlock * 8 * kSplitGroups || ldx % 4 != 0 || Mpad % kPfTileM != 0 || M > Mpad)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_split, dim3(Mpad), dim3(kBlock), 0, st, x, ldx, norm_w, eps, K, M, (h8_t*)xa, rs);
     return hipGetLastError();
 }
 

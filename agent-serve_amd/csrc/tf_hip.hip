@@ -546,7 +546,7 @@ int ensure_pf(tf_hip_ctx* c) {
         const size_t kmax = std::max({D, F, (size_t)c->H});
         if ((rc = dalloc(c, &c->px, cap * D * 4)) || (rc = dalloc(c, &c->pqkv, cap * NQ * 4)) ||
             (rc = dalloc(c, &c->patt, cap * (size_t)c->H * 4)) || (rc = dalloc(c, &c->ph, cap * F * 4)) ||
-            (rc = dalloc(c, &c->prs, (size_t)cap * 3 * 4)) || (rc = dalloc(c, &c->pxa, cap * kmax * 2 * 2)))
+            (rc = dalloc(c, &c->prs, (size_t)cap * 4)) || (rc = dalloc(c, &c->pxa, cap * kmax * 2 * 2)))
             return rc;
         c->pf_cap = cap;
     }
@@ -613,7 +613,7 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
             float* kc = c->kc + (size_t)l * c->kv_layer;
             float* vc = c->vc + (size_t)l * c->kv_layer;
             chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_ATTN_NORM), p.rms_eps, D, nc, Mpad, c->pxa, c->prs,
-                                c->prs + c->pf_cap, c->st));
+                                c->st));
             {
                 PfGemmArgs a = base(D);
                 a.mode = GEMV_STORE;
@@ -626,7 +626,7 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                                      pos0, kc, vc, p.kv_layout, p.max_seq, c->st));
             chk(launch_pf_attn(c->pqkv, NQ, kc, vc, p.kv_layout, p.n_head, p.n_kv_head, p.head_dim, p.max_seq, nc,
                                pos0, start, c->patt, Hd, c->st));
-            chk(launch_pf_split(c->patt, Hd, nullptr, 0.0f, Hd, nc, Mpad, c->pxa, c->prs, c->prs + c->pf_cap, c->st));
+            chk(launch_pf_split(c->patt, Hd, nullptr, 0.0f, Hd, nc, Mpad, c->pxa, c->prs, c->st));
             {
                 PfGemmArgs a = base(Hd);
                 a.mode = GEMV_RESID;
@@ -634,7 +634,7 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                 chk(launch_pf_gemm(a, c->st));
             }
             chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_FFN_NORM), p.rms_eps, D, nc, Mpad, c->pxa, c->prs,
-                                c->prs + c->pf_cap, c->st));
+                                c->st));
             {
                 PfGemmArgs a = base(D);
                 a.mode = GEMV_SILU;
@@ -643,7 +643,7 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                 a.seg[0].wf2 = c->pf_wf[(size_t)M(TF_HIP_LAYER_UP)];
                 chk(launch_pf_gemm(a, c->st));
             }
-            chk(launch_pf_split(c->ph, F, nullptr, 0.0f, F, nc, Mpad, c->pxa, c->prs, c->prs + c->pf_cap, c->st));
+            chk(launch_pf_split(c->ph, F, nullptr, 0.0f, F, nc, Mpad, c->pxa, c->prs, c->st));
             {
                 PfGemmArgs a = base(F);
                 a.mode = GEMV_RESID;
@@ -1154,9 +1154,9 @@ int tf_hip_matmul(int device, int t, const void* w, int64_t ne0, int64_t ne1, co
         float* rs;
         OPCHK(s.alloc(&xa, (size_t)Mpad * ne0 * 2 * 2));
         OPCHK(s.alloc(&wf, (size_t)ne1 * ne0 * 2));
-        OPCHK(s.alloc(&rs, (size_t)Mpad * 3 * 4));
+        OPCHK(s.alloc(&rs, (size_t)Mpad * 4));
         OPCHK(launch_pf_pack_q8(m, wf, s.st));
-        OPCHK(launch_pf_split(dx, ne0, nullptr, 0.0f, (int)ne0, n_rows_x, Mpad, xa, rs, rs + Mpad, s.st));
+        OPCHK(launch_pf_split(dx, ne0, nullptr, 0.0f, (int)ne0, n_rows_x, Mpad, xa, rs, s.st));
         PfGemmArgs a;
         a.xa = xa;
         a.rs = rs;

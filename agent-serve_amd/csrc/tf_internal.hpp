@@ -182,9 +182,9 @@ struct PfGemmArgs {
 };
 
 bool pf_gemm_supported(int type, int64_t K, int64_t N);
-// xa needs Mpad * K * 2 halves, rs Mpad floats, st 2 * Mpad floats (row statistics).
+// xa needs Mpad * K * 2 halves, rs Mpad floats.
 hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,
-                           uint16_t* xa, float* rs, float* st, hipStream_t s);
+                           uint16_t* xa, float* rs, hipStream_t st);
 // wf needs m.N * m.K halves.
 hipError_t launch_pf_pack_q8(const DevMat& m, uint16_t* wf, hipStream_t st);
 hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st);

@@ -125,7 +125,7 @@ int tf_hip_get_decode_path(tf_hip_ctx* ctx);
 /* Prefill path (no counterpart in the reference, whose layer_prefill is the one
  * path, model.cpp:144-195): TF_HIP_PREFILL_MFMA runs a prompt of two or more tokens
  * through the matrix-core GEMMs and the causal chunk attention when every layer
- * matrix is Q8_0 with row lengths divisible by 64 and output lengths by 16 and the head
+ * matrix is Q8_0 with row lengths divisible by 64 (at most 16384) and output lengths by 16 and the head
  * size is 32, 64 or 128 (the default); otherwise, and under TF_HIP_PREFILL_TOKENS,
  * prompt tokens run one at a time through the decode path with attention limited to
  * the prompt. get returns the path a prompt would take (or < 0 on error). */
@@ -173,9 +173,9 @@ int tf_hip_dequant_rows(int device, int ggml_type, const void* w, int64_t ne0, i
                         int64_t nrows, float* out);
 
 /* matmul (matmul.cpp:64-73): y[m][n] = sum_k x[m][k] * W[n][k] for m < n_rows_x.
- * One row runs the decode GEMV. Two or more rows of a Q8_0 matrix with ne0 % 64 == 0 and
- * ne1 % 16 == 0 run the prefill GEMM on the matrix cores; other shapes and formats run
- * the GEMV once per row. */
+ * One row runs the decode GEMV. Two or more rows of a Q8_0 matrix with ne0 % 64 == 0,
+ * ne0 <= 16384 and ne1 % 16 == 0 run the prefill GEMM on the matrix cores; other shapes
+ * and formats run the GEMV once per row. */
 int tf_hip_matmul(int device, int ggml_type, const void* w, int64_t ne0, int64_t ne1, const float* x,
                   int32_t n_rows_x, float* y);
 
