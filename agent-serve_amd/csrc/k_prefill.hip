@@ -317,6 +317,234 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
     }
 }
 
+// Large tiles for GEMMs with enough of them to fill the CUs: a workgroup of 8 waves
+// (2 rows x 4 columns of waves) owns 128 rows x 16 weight-column subtiles (256 weight rows;
+// GEMV_SILU: 8 gate and the 8 matching up subtiles, 128 output columns). A stage (two
+// 32-element blocks) of both operands and the scales is staged in LDS, loaded once per
+// workgroup (8 fragments per wave) through registers one stage ahead of its use; each wave
+// then runs 4 x 4 tiles of 16 x 16 per block, reading its fragments from LDS. The per-block
+// arithmetic and its order are those of k_pf_gemm_q8, so the two give the same bits.
+constexpr int kBigThreads = 512;
+constexpr int kBigRows = 128;
+constexpr int kBigStageH8 = 64 * 64;  // h8 per stage: 32 A fragments + 32 B fragments of 64 lanes
+constexpr int kBigStageBytes = kBigStageH8 * 16 + 256 * 4;
+constexpr size_t kBigLdsBytes = 2 * (size_t)kBigStageBytes;
+
+// SPLIT: the grid also splits K into a.ks slices; slice ks writes its row-scaled partial
+// sums to a.part[ks][row][output column] and k_pf_reduce applies the epilogue.
+template <int MODE, bool SPLIT>
+__global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int b = blockIdx.x;
+    {
+        const int q = (int)gridDim.x / 8;
+        if (b < 8 * q) b = (b % 8) * q + b / 8;
+    }
+    const int kslice = SPLIT ? b % a.ks : 0;
+    if (SPLIT) b /= a.ks;
+    const int MT = a.Mpad / kBigRows;
+    const int mt = b % MT, nt = b / MT;
+    const int K = a.K, nblk = K / 32;
+    const int S = SPLIT ? K / 64 / a.ks : K / 64;  // stages of this slice
+    const int s0 = kslice * S;                      // its first stage
+    const int l16 = lane & 15;
+    constexpr bool SILU = MODE == GEMV_SILU;
+
+    // weight-column subtile q (0..15) of this workgroup: output subtile, matrix, tile row
+    auto resolve = [&](int q, int& u, int& seg, bool& up) {
+        up = SILU && q >= 8;
+        u = SILU ? nt * 8 + (q & 7) : nt * 16 + q;
+        u = u < a.n_sub ? u : a.n_sub - 1;
+        seg = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
+    };
+    // this wave's 8 fragment loads per stage: i < 4 A fragments, i >= 4 B fragments
+    const TF_GLOBAL h8_t* src[8];
+    int step[8];  // h8 per stage
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int f = wave + 8 * i;
+        if (i < 4) {
+            const int T = f / 4, blk = (f / 2) % 2, hl = f % 2;
+            src[i] = (const TF_GLOBAL h8_t*)a.xa + ((int64_t)(mt * 8 + T) * nblk + blk) * 128 + hl * 64 + lane;
+            step[i] = 256;
+        } else {
+            const int g = f - 32, q = g / 2, blk = g % 2;
+            int u, seg;
+            bool up;
+            resolve(q, u, seg, up);
+            const int tile = u - PF_SEL(seg, sub0);
+            const uint16_t* wf = up ? PF_SEL(seg, wf2) : PF_SEL(seg, wf);
+            src[i] = (const TF_GLOBAL h8_t*)wf + ((int64_t)tile * nblk + blk) * 64 + lane;
+            step[i] = 128;
+        }
+    }
+    // the scales: thread t (mod 256) loads column j = t of the 256 weight columns
+    const uint16_t* dsrc;
+    {
+        const int j = tid & 255, q = j / 16;
+        int u, seg;
+        bool up;
+        resolve(q, u, seg, up);
+        const int c = (u - PF_SEL(seg, sub0)) * 16 + (j & 15);
+        const uint8_t* ws = up ? PF_SEL(seg, w2.s) : PF_SEL(seg, w.s);
+        dsrc = (const uint16_t*)ws + (int64_t)c * nblk;
+    }
+    h8_t stg[8];
+    uint32_t dstg;
+    auto gload = [&](int s) {
+        s = s0 + (s < S ? s : S - 1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) stg[i] = src[i][(int64_t)s * step[i]];
+        dstg = *(const TF_GLOBAL uint32_t*)(dsrc + 2 * s);
+    };
+    auto lds_write = [&](int buf) {
+        h8_t* st = (h8_t*)(lds + buf * kBigStageBytes);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st[(wave + 8 * i) * 64 + lane] = stg[i];
+        ((uint32_t*)(lds + buf * kBigStageBytes + kBigStageH8 * 16))[tid & 255] = dstg;
+    };
+    auto barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+    const int wm = wave & 1, wn = wave >> 1;
+    int qb[4];  // this wave's weight-column subtiles
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) qb[ni] = SILU ? (ni < 2 ? wn * 2 + ni : 8 + wn * 2 + ni - 2) : wn * 4 + ni;
+
+    f4_t acc[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](int buf) {
+        const h8_t* st = (const h8_t*)(lds + buf * kBigStageBytes);
+        const uint32_t* sd = (const uint32_t*)(lds + buf * kBigStageBytes + kBigStageH8 * 16);
+        uint32_t dd[4];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) dd[ni] = sd[qb[ni] * 16 + l16];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            h8_t bh[4];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) bh[ni] = st[(32 + qb[ni] * 2 + j) * 64 + lane];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                h8_t ah[2], al[2];
+#pragma unroll
+                for (int mm = 0; mm < 2; ++mm) {
+                    const int T = wm * 4 + half * 2 + mm;
+                    ah[mm] = st[((T * 2 + j) * 2 + 0) * 64 + lane];
+                    al[mm] = st[((T * 2 + j) * 2 + 1) * 64 + lane];
+                }
+                f4_t t[2][4];
+#pragma unroll
+                for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+                    for (int ni = 0; ni < 4; ++ni)
+                        t[mm][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mm], bh[ni],
+                                                                          (f4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+                    for (int ni = 0; ni < 4; ++ni)
+                        t[mm][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mm], bh[ni], t[mm][ni], 0, 0, 0);
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    const float dv = h2f(dd[ni] >> (16 * j));
+#pragma unroll
+                    for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            acc[half * 2 + mm][ni][r] = fmaf(dv, t[mm][ni][r], acc[half * 2 + mm][ni][r]);
+                }
+            }
+        }
+    };
+
+    gload(0);
+    lds_write(0);
+    gload(1);
+    barrier();
+    for (int s = 0; s < S; ++s) {
+        compute(s & 1);
+        lds_write((s + 1) & 1);  // stage s + 1 (the buffer of stage s - 1, read before the last barrier)
+        gload(s + 2);
+        barrier();
+    }
+
+    // epilogue: lane holds rows 16 T + 4 (lane / 16) + r of weight column 16 q + l16
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+        const int r0 = mt * kBigRows + (wm * 4 + mi) * 16 + 4 * (lane >> 4);
+        const float4 rsv = *(const float4*)(a.rs + r0);
+        const float rsa[4] = {rsv.x, rsv.y, rsv.z, rsv.w};
+#pragma unroll
+        for (int ni = 0; ni < (SILU ? 2 : 4); ++ni) {
+            int u, seg;
+            bool up;
+            const int uraw = SILU ? nt * 8 + (qb[ni] & 7) : nt * 16 + qb[ni];
+            resolve(qb[ni], u, seg, up);
+            if (uraw >= a.n_sub) continue;
+            if (SPLIT) {
+                const int ntot = a.n_sub * 16;
+                float* part = a.part + ((int64_t)kslice * a.Mpad) * ntot + u * 16 + l16;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (r0 + r < a.M) part[(int64_t)(r0 + r) * ntot] = acc[mi][ni][r] * rsa[r];
+                continue;
+            }
+            const int c = (u - PF_SEL(seg, sub0)) * 16 + l16;
+            float* y = PF_SEL(seg, y);
+            const int64_t ldy = PF_SEL(seg, ldy);
+            const float* bias = PF_SEL(seg, bias);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = r0 + r;
+                if (row >= a.M) continue;
+                float* p = y + (int64_t)row * ldy + c;
+                if (SILU) {
+                    const float gv = acc[mi][ni][r] * rsa[r];
+                    const float uv = acc[mi][ni + 2][r] * rsa[r];
+                    *p = (gv / (1.0f + expf(-gv))) * uv;
+                } else if (MODE == GEMV_STORE) {
+                    const float v = acc[mi][ni][r] * rsa[r];
+                    *p = bias ? v + bias[c] : v;
+                } else {
+                    const float nv = *p + acc[mi][ni][r] * rsa[r];
+                    *p = nv;
+                    if (row == a.tap_row && a.tap) a.tap[c] = nv;
+                }
+            }
+        }
+    }
+}
+
+// Sums the a.ks partial rows of a split-K GEMM in slice order and applies the epilogue:
+// thread per output column of row blockIdx.y.
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void k_pf_reduce(const PfGemmArgs a) {
+    const int row = blockIdx.y;
+    const int col = blockIdx.x * kBlock + threadIdx.x;
+    const int ntot = a.n_sub * 16;
+    if (col >= ntot) return;
+    const float* p = a.part + (int64_t)row * ntot + col;
+    float v = 0.0f;
+    for (int k = 0; k < a.ks; ++k) v += p[(int64_t)k * a.Mpad * ntot];
+    const int u = col / 16;
+    const int seg = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
+    const int c = col - PF_SEL(seg, sub0) * 16;
+    float* y = PF_SEL(seg, y) + (int64_t)row * PF_SEL(seg, ldy) + c;
+    if (MODE == GEMV_STORE) {
+        const float* bias = PF_SEL(seg, bias);
+        *y = bias ? v + bias[c] : v;
+    } else {
+        const float nv = *y + v;
+        *y = nv;
+        if (row == a.tap_row && a.tap) a.tap[c] = nv;
+    }
+}
+
 #undef PF_SEL
 
 // ---------------------------------------------------------------- RoPE and KV store
@@ -525,6 +753,60 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st) {
             return hipErrorInvalidValue;
     }
     if (a.seg[0].sub0 != 0 || (a.mode == GEMV_SILU && a.n_seg != 1)) return hipErrorInvalidValue;
+    // large tiles when they give every CU a workgroup, directly or with K split in slices
+    if (a.Mpad % kBigRows == 0) {
+        const int per_big = a.mode == GEMV_SILU ? 8 : 16;  // output subtiles per large tile
+        const int n_big = (a.n_sub + per_big - 1) / per_big * (a.Mpad / kBigRows);
+        const int cus = device_cu_count();
+        int ks = 1;
+        if (n_big < cus && a.mode != GEMV_SILU && a.part) {
+            // the fewest slices that fill the CUs, each at least 8 stages long (shorter
+            // slices spend more on filling their pipeline and on the partial rows they
+            // write than they save); worth it from half the CUs on
+            const int S = a.K / 64;
+            const size_t per_slice = (size_t)a.Mpad * a.n_sub * 16;
+            for (int k = 2; k <= 16; k *= 2) {
+                if (S % k != 0 || S / k < 8 || (size_t)k * per_slice > a.part_floats) break;
+                ks = k;
+                if (n_big * k >= cus) break;
+            }
+            if (2 * n_big * ks < cus) ks = 1;
+        }
+        if (n_big >= cus || ks > 1) {
+            static bool attr_set[6] = {false, false, false, false, false, false};
+            const void* fns[6] = {(const void*)k_pf_gemm_big<GEMV_STORE, false>,
+                                  (const void*)k_pf_gemm_big<GEMV_RESID, false>,
+                                  (const void*)k_pf_gemm_big<GEMV_SILU, false>,
+                                  (const void*)k_pf_gemm_big<GEMV_STORE, true>,
+                                  (const void*)k_pf_gemm_big<GEMV_RESID, true>,
+                                  (const void*)k_pf_gemm_big<GEMV_SILU, true>};
+            const int fi = a.mode + (ks > 1 ? 3 : 0);
+            if (!attr_set[fi]) {
+                const hipError_t e =
+                    hipFuncSetAttribute(fns[fi], hipFuncAttributeMaxDynamicSharedMemorySize, (int)kBigLdsBytes);
+                if (e != hipSuccess) return e;
+                attr_set[fi] = true;
+            }
+            PfGemmArgs b = a;
+            b.ks = ks;
+            const dim3 grid((unsigned)(n_big * ks));
+            switch (fi) {
+                case 0: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_STORE, false>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                case 1: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_RESID, false>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                case 2: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_SILU, false>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                case 3: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_STORE, true>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                default: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_RESID, true>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+            }
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess || ks == 1) return e;
+            const dim3 rgrid((unsigned)((a.n_sub * 16 + kBlock - 1) / kBlock), (unsigned)a.M);
+            if (a.mode == GEMV_STORE)
+                hipLaunchKernelGGL(k_pf_reduce<GEMV_STORE>, rgrid, dim3(kBlock), 0, st, b);
+            else
+                hipLaunchKernelGGL(k_pf_reduce<GEMV_RESID>, rgrid, dim3(kBlock), 0, st, b);
+            return hipGetLastError();
+        }
+    }
     // 4 column subtiles per wave; 2 when that leaves fewer than two workgroups per CU
     const int mt = a.Mpad / kPfTileM;
     const int out4 = a.mode == GEMV_SILU ? 2 : 4;

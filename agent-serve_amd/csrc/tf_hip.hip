@@ -74,6 +74,8 @@ struct tf_hip_ctx {
     int pf_cap = 0;                    // rows per prefill chunk (multiple of kPfTileM)
     float *px = nullptr, *pqkv = nullptr, *patt = nullptr, *ph = nullptr, *prs = nullptr;
     uint16_t* pxa = nullptr;            // activation fragments (hi, lo) of one chunk
+    float* ppart = nullptr;             // split-K partial sums of the prefill GEMMs
+    size_t ppart_floats = 0;
     std::vector<uint16_t*> pf_wf;       // per slot: the matrix's integers as fp16 fragments
     std::string err;
 };
@@ -548,6 +550,9 @@ int ensure_pf(tf_hip_ctx* c) {
             (rc = dalloc(c, &c->patt, cap * (size_t)c->H * 4)) || (rc = dalloc(c, &c->ph, cap * F * 4)) ||
             (rc = dalloc(c, &c->prs, (size_t)cap * 4)) || (rc = dalloc(c, &c->pxa, cap * kmax * 2 * 2)))
             return rc;
+        // up to 8 K slices of the widest non-SILU output (QKV or d_model)
+        c->ppart_floats = 8 * (size_t)cap * std::max(NQ, D);
+        if ((rc = dalloc(c, &c->ppart, c->ppart_floats * 4))) return rc;
         c->pf_cap = cap;
     }
     // every layer matrix's integers as fp16 fragments (2 bytes per weight, kept for the
@@ -591,6 +596,8 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
             PfGemmArgs a;
             a.xa = c->pxa;
             a.rs = c->prs;
+            a.part = c->ppart;
+            a.part_floats = c->ppart_floats;
             a.K = K;
             a.M = nc;
             a.Mpad = Mpad;
@@ -1160,6 +1167,10 @@ int tf_hip_matmul(int device, int t, const void* w, int64_t ne0, int64_t ne1, co
         PfGemmArgs a;
         a.xa = xa;
         a.rs = rs;
+        if (Mpad % 128 == 0) {  // workspace for K slices of the large-tile kernel
+            a.part_floats = (size_t)8 * Mpad * ne1;
+            OPCHK(s.alloc(&a.part, a.part_floats * 4));
+        }
         a.K = (int)ne0;
         a.M = n_rows_x;
         a.Mpad = Mpad;

@@ -179,6 +179,9 @@ struct PfGemmArgs {
     int mode = GEMV_STORE;         // GEMV_STORE, GEMV_RESID or GEMV_SILU
     float* tap = nullptr;          // GEMV_RESID: copy of output row tap_row
     int tap_row = -1;
+    float* part = nullptr;         // optional workspace for split-K partial sums (GEMV_STORE, GEMV_RESID)
+    size_t part_floats = 0;
+    int ks = 1;                    // K slices (set by launch_pf_gemm)
 };
 
 bool pf_gemm_supported(int type, int64_t K, int64_t N);

@@ -89,12 +89,14 @@ def prefill(trace_csv: str, n: int, dims: str) -> None:
         if "k_pf_" not in k and "k_embed_rows" not in k:
             continue
         us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-        if "k_pf_gemm_q8<0" in k:
+        if "k_pf_reduce" in k:
+            c = "splitk_reduce"
+        elif re.search(r"k_pf_gemm_(q8|big|split)<0", k):
             c = "qkv_gemm"
-        elif "k_pf_gemm_q8<1" in k:
+        elif re.search(r"k_pf_gemm_(q8|big|split)<1", k):
             c = "wo_gemm" if resid % 2 == 0 else "down_gemm"
             resid += 1
-        elif "k_pf_gemm_q8<2" in k:
+        elif re.search(r"k_pf_gemm_(q8|big|split)<2", k):
             c = "gateup_gemm"
         elif "k_pf_attn" in k:
             c = "attention"
