@@ -7,7 +7,9 @@
 // LDS tiles of K and V rows (one memory round per tile): scores in the reference's
 // 8-lane dot order, an online softmax across tiles, and P.V. With one active split it
 // writes the output heads itself; otherwise it writes (max, sum, o) partials and
-// k_attn_combine merges them in a second launch.
+// k_attn_combine merges them in a second launch. Splits are one tile long until there
+// are kAttnMaxSplits of them, so a long context is read by many workgroups in one memory
+// round each instead of a few walking tiles one after the other.
 // No workgroup waits on another inside a launch: on this multi-XCD part a device-scope
 // fence writes back the XCD's L2, which costs more than the kernel boundary.
 #include "dev_common.hpp"
@@ -242,23 +244,55 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const AttnArgs a) {
     }
 }
 
-// Merges the split partials: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
-__global__ __launch_bounds__(kBlock) void k_attn_combine(const AttnArgs a) {
+// Merges the split partials of head blockIdx.x: out = sum_s o_s e^(m_s - M) / sum_s l_s
+// e^(m_s - M), M = max_s m_s. One workgroup per head: the weights e^(m_s - M) go to LDS
+// once, thread (d, group) sums o_s[d] over the splits s = group, group + groups, ..., and
+// the groups are added in group order (a fixed order for a given split count).
+constexpr int kCombThreads = 1024;
+
+__global__ __launch_bounds__(kCombThreads) void k_attn_combine(const AttnArgs a) {
     const Split sp = split_of(a);
     if (sp.n_act <= 1) return;  // k_attn_decode wrote the output
-    const int i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= a.H * a.hd) return;
-    const int h = i / a.hd, dd = i % a.hd;
+    __shared__ float w[kAttnMaxSplits];
+    __shared__ float red[kCombThreads / kWave];
+    __shared__ float part[kCombThreads];
+    const int h = blockIdx.x, n = sp.n_act, hd = a.hd;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* ml = a.part_ml + (int64_t)h * a.S * 2;
-    float M = -INFINITY;
-    for (int t = 0; t < sp.n_act; ++t) M = fmaxf(M, ml[2 * t]);
-    float L = 0.0f, o = 0.0f;
-    for (int t = 0; t < sp.n_act; ++t) {
-        const float w = expf(ml[2 * t] - M);
-        L = fmaf(ml[2 * t + 1], w, L);
-        o = fmaf(a.part_o[((int64_t)h * a.S + t) * a.hd + dd], w, o);
+    float m = -INFINITY;
+    for (int t = tid; t < n; t += kCombThreads) m = fmaxf(m, ml[2 * t]);
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    float M = red[0];
+    for (int i = 1; i < kCombThreads / kWave; ++i) M = fmaxf(M, red[i]);
+    __syncthreads();  // red is reused below
+    float l = 0.0f;
+    for (int t = tid; t < n; t += kCombThreads) {
+        const float wt = expf(ml[2 * t] - M);
+        w[t] = wt;
+        l = fmaf(ml[2 * t + 1], wt, l);
     }
-    a.out[(int64_t)h * a.hd + dd] = o / L;
+    l = wave_sum(l);
+    if (lane == 0) red[wave] = l;
+    __syncthreads();
+    float L = 0.0f;
+    for (int i = 0; i < kCombThreads / kWave; ++i) L += red[i];
+    const int groups = kCombThreads / hd;
+    const int d = tid % hd, grp = tid / hd;
+    float o = 0.0f;
+    if (grp < groups) {
+        const float* po = a.part_o + (int64_t)h * a.S * hd + d;
+#pragma unroll 8
+        for (int t = grp; t < n; t += groups) o = fmaf(po[(int64_t)t * hd], w[t], o);
+    }
+    part[tid] = o;
+    __syncthreads();
+    if (tid < hd) {
+        float sum = 0.0f;
+        for (int g = 0; g < groups; ++g) sum += part[g * hd + tid];
+        a.out[(int64_t)h * hd + tid] = sum / L;
+    }
 }
 
 }  // namespace
@@ -266,7 +300,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_combine(const AttnArgs a) {
 int attn_splits(int max_seq) {
     if (max_seq <= 512) return 1;
     int s = (max_seq + kAttnMinChunk - 1) / kAttnMinChunk;
-    return s < 2 ? 2 : (s > 64 ? 64 : s);
+    return s < 2 ? 2 : (s > kAttnMaxSplits ? kAttnMaxSplits : s);
 }
 
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
@@ -281,7 +315,8 @@ hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t st) {
         hipLaunchKernelGGL(k_attn_decode<256>, dim3(a.G * a.S), dim3(kBlock), lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.S == 1) return e;
-    hipLaunchKernelGGL(k_attn_combine, dim3((a.H * a.hd + kBlock - 1) / kBlock), dim3(kBlock), 0, st, a);
+    if (a.hd > kCombThreads) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.H), dim3(kCombThreads), 0, st, a);
     return hipGetLastError();
 }
 

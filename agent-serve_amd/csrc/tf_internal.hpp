@@ -103,9 +103,11 @@ struct AttnArgs {
     int fixed_start;
 };
 
-// Attention splits: positions per split at least kAttnMinChunk; one split (no merge
-// launch) when max_seq <= 512.
-constexpr int kAttnMinChunk = 64;
+// Attention splits: positions per split at least kAttnMinChunk (one LDS tile, so a
+// split is one memory round), at most kAttnMaxSplits splits per kv head; one split (no
+// merge launch) when max_seq <= 512.
+constexpr int kAttnMinChunk = 32;
+constexpr int kAttnMaxSplits = 512;
 int attn_splits(int max_seq);
 
 // ---------------------------------------------------------------- persistent step kernel
