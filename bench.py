@@ -18,6 +18,9 @@ workload of the same model on the matrix cores: tok/s from HIP events around the
 algorithmic TFLOP/s and their fraction of the dense fp16 MFMA peak, the decode rate
 after the prompt, and the reference CPU prefill on a bounded sample. `context_sweep` is the
 decode rate after prompts of 512..4000 tokens in a 4096-position cache (graph path).
+`other_configs` runs the other workloads at their own shapes (Qwen2.5-0.5B with QKV bias,
+the mixed Q4 file, Qwen2.5-1.5B after a 4096-token prompt): prefill and decode tok/s and
+decode GB/s.
 """
 from __future__ import annotations
 
@@ -163,6 +166,46 @@ def context_sweep(pkg, path, info):
     return {"max_seq": CTX_MAX_SEQ, "steps": CTX_STEPS, "points": out}
 
 
+# the other configurations of the workload list: (name, preset, prompt tokens, decode tokens,
+# max-seq, KV layout)
+OTHER_CONFIGS = (
+    ("qwen2.5-0.5b-shape q8_0 + qkv bias", "qwen05b_q8", 16, 128, 512, 0),
+    ("llama-3.2-1b-shape mixed q4_0/q4_1/q6_k", "llama1b_mixq4", 6, 64, 512, 0),
+    ("qwen2.5-1.5b-shape q8_0, 4096-token prompt, head-major cache", "qwen15b_q8", 4096, 256, 8192, 1),
+)
+
+
+def configs_leg(pkg):
+    """The other workloads at their own shapes: a prefill of the prompt from a reset, then
+    the decode tokens in one greedy generate call (both timed by the HIP events around
+    the call's kernels); GB/s counts each step's weights once and its KV rows
+    (tf_hip_decode_bytes), as for the headline."""
+    out = []
+    for name, preset, n_prompt, n_dec, max_seq, layout in OTHER_CONFIGS:
+        info = pkg.synth_preset_info(preset)
+        path = str(pathlib.Path(model_path()).parent / f"{preset}-seed{info['seed']}.gguf")
+        if not os.path.exists(path):
+            pkg.synth_write(preset, path, threads=host_threads())
+        prompt = pkg.synth_prompt(info["seed"], n_prompt, info["n_vocab"])
+        m = pkg.HipModel(path, max_seq=max_seq, kv_layout=layout)
+        m.prefill(prompt, want_logits=False)  # warm-up (and one-time weight packing)
+        m.generate(8)
+        m.reset()
+        m.prefill(prompt, want_logits=False)
+        pf_ms, _, _, pf_name = m.last_timing()
+        m.generate(n_dec)
+        ms, _, _, dec_name = m.last_timing()
+        b = sum(m.decode_bytes(n_prompt + i) for i in range(n_dec))
+        gbs = b / (ms * 1e-3) / 1e9
+        out.append({"workload": name, "prompt_tokens": n_prompt, "decode_tokens": n_dec, "max_seq": max_seq,
+                    "prefill_tok_s": round(n_prompt / (pf_ms * 1e-3), 1), "prefill_path": pf_name,
+                    "decode_tok_s": round(n_dec / (ms * 1e-3), 1), "decode_gb_s": round(gbs, 1),
+                    "decode_hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "decode_path": dec_name,
+                    "bytes_per_step": round(b / n_dec)})
+        m.close()
+    return out
+
+
 def cpu_prefill_baseline(pkg, path, info):
     """The reference --stage v2 prefill (oracle/_ref) on this host's cores over the first
     PF_CPU_SAMPLE_TOKENS tokens of the 512-token prompt (a bounded sample: its cost per
@@ -288,6 +331,7 @@ def main() -> int:
 
     pf = prefill_leg(pkg, path, info)
     ctx = context_sweep(pkg, path, info)
+    others = configs_leg(pkg)
     cpu, match = (None, None) if args.no_cpu else cpu_baseline(path, prompt, K, ids)
     if not args.no_cpu:
         pf["cpu_baseline"] = cpu_prefill_baseline(pkg, path, info)
@@ -338,6 +382,7 @@ def main() -> int:
         "prefill_6_tokens_wall_ms": round(prefill_s * 1e3, 3),
         "prefill": pf,
         "context_sweep": ctx,
+        "other_configs": others,
         "decode_path": "persistent step kernel" if dpath == 1 else "graph",
         "graph_kernel_ms_by_class": {k: round(v[0] / K, 4) for k, v in prof.items()},
         "tokens_match_profile_pass": bool(list(ids) == list(ids_prof)),
