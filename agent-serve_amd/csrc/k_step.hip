@@ -6,10 +6,35 @@ namespace tfk {
 
 using step_detail::attn_lds_floats;
 
-size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg) {
+size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg, int split) {
     const size_t n_rep = (size_t)(H / G);
     return 2 * ((size_t)D + (size_t)D + (size_t)G * (n_rep + 2) * hd + (size_t)H * hd + (size_t)F + (size_t)n_wg +
-                2 * (size_t)n_wg);
+                2 * (size_t)n_wg + (size_t)H * split * (hd + 2));
+}
+
+int step_split(int D, int F, int H, int G, int hd, int n_wg) {
+    // A = n_rep * parts splits per kv head on G * A workgroups (at most half of them, the
+    // rest stream the FFN weights meanwhile); parts (a power of two dividing hd) slices of
+    // each head's outputs, one per attention workgroup, for the merge
+    const int n_rep = H / G;
+    int parts = 0;
+    for (int p = 1; p <= hd && hd % p == 0 && H * p <= n_wg / 2; p *= 2) parts = p;
+    if (parts < 1) return 0;
+    const int A = n_rep * parts, sz = hd / parts;
+    if (A < 2 || A * (sz + 2) > 3 * step_detail::kT || A * (sz + 2) > step_detail::region_floats(D, F, n_rep, hd, n_wg))
+        return 0;
+    return A;
+}
+
+int step_split_all(int D, int F, int H, int G, int hd, int n_wg) {
+    // one split of every kv head per workgroup, as far as the merge's gather (3 words per
+    // thread) and the LDS region hold A (sz + 2) words
+    const int n_rep = H / G;
+    const int sz = hd / step_detail::split_all_parts(H, hd, n_wg);
+    int A = n_wg / G;
+    while (A > 1 && (A * (sz + 2) > 3 * step_detail::kT || A * (sz + 2) > step_detail::region_floats(D, F, n_rep, hd, n_wg)))
+        --A;
+    return A < 2 ? 0 : A;
 }
 
 size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg, int stage_lds) {
@@ -17,7 +42,7 @@ size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg,
     const int region = step_detail::region_floats(D, F, n_rep, hd, n_wg);
     const size_t table = ((size_t)n_layer * sizeof(StepLayer) + 15) / 16 * 16;
     const size_t floats = (size_t)(D + 3) / 4 * 4 + (size_t)(region + 3) / 4 * 4 + (size_t)(n_rep + 2) * hd +
-                          (size_t)n_rep * hd;
+                          (size_t)n_rep * (hd + 2);
     const size_t staged = (stage_lds & 1) ? 16 + (size_t)step_detail::kNW * step_detail::row_slot_bytes(F) : 0;
     return table + 4 * floats + staged;
 }

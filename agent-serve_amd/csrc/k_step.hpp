@@ -45,6 +45,18 @@ __device__ __forceinline__ void put(u64* p, float v, uint32_t e) {
 __device__ __forceinline__ u64 get(u64* p) {
     return __hip_atomic_load(gptr(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16 bytes read at agent scope (two 8-byte loads that miss any stale copy in this XCD's L2).
+// c ? a : b on values. (The conditional operator on two float4 lvalues selects between their
+// addresses and copies, which keeps register arrays in scratch.)
+__device__ __forceinline__ float4 sel4(bool c, float4 a, float4 b) {
+    return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
+__device__ __forceinline__ float4 gload_f4_agent(const float* p) {
+    const u64 a = __hip_atomic_load((const TF_GLOBAL u64*)gptr(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const u64 b = __hip_atomic_load((const TF_GLOBAL u64*)gptr(p + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float4(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
+                       __uint_as_float((uint32_t)(b >> 32)));
+}
 __device__ __forceinline__ int get_err(Ctl* c) {
     return __hip_atomic_load(gptr(&c->err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -104,6 +116,45 @@ __device__ __forceinline__ void gather(u64* pa, int na, uint32_t ea, float* da, 
             if (pend & (1u << (NA + i))) {
                 const u64 w = get(pb + tid + i * kT);
                 if ((uint32_t)(w >> 32) == eb) pend &= ~(1u << (NA + i));
+            }
+        }
+    }
+}
+
+// gather() of words base[idx(j)], j < n, of epoch e into d[j] (LDS).
+template <int NA, class Idx>
+__device__ __forceinline__ void gather_idx(u64* base, Idx&& idx, int n, uint32_t e, float* d, Ctl* ctl) {
+    const int tid = threadIdx.x;
+    u64 w[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+        if (tid + i * kT < n) w[i] = get(base + idx(tid + i * kT));
+    uint32_t pend = 0;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int j = tid + i * kT;
+        if (j < n) {
+            if ((uint32_t)(w[i] >> 32) == e)
+                d[j] = __uint_as_float((uint32_t)w[i]);
+            else
+                pend |= 1u << i;
+        }
+    }
+    for (int spin = 0; pend; ++spin) {
+        if (spin >= kSpinLimit || ((spin & 1023) == 1023 && get_err(ctl))) {
+            set_err(ctl, kErrTimeout);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            if (pend & (1u << i)) {
+                const int j = tid + i * kT;
+                const u64 v = get(base + idx(j));
+                if ((uint32_t)(v >> 32) == e) {
+                    d[j] = __uint_as_float((uint32_t)v);
+                    pend &= ~(1u << i);
+                }
             }
         }
     }
@@ -277,22 +328,39 @@ __device__ __forceinline__ int64_t kv_at(int layout, int G, int max_seq, int hd,
     return layout == TF_HIP_KV_HEAD_MAJOR ? ((int64_t)g * max_seq + p) * hd : ((int64_t)p * G + g) * hd;
 }
 
-// Attention of kv head g over positions [start, pos] (attn_decode, attention.cpp:55-80),
-// with the RoPE of its query heads and key (attention.cpp:31-46) and the KV store
-// (kvcache.cpp:31-36). fetch() fills qkv (LDS) with the head block [n_rep q heads | k | v]
-// the QKV phase produced; it runs after the first K/V tile's loads are issued (the cached
-// rows do not depend on this token), so the cache latency overlaps the hand-off. The
-// output heads go to out (LDS, [n_rep][hd]). The same workgroup runs head g for every
-// token of a launch, so the rows it stores are the ones it later reads on this CU.
-template <int HDM, class Fetch>
-__device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly, int g, int pos, int start, float* qkv, float* sm,
-                          float* out, Fetch&& fetch) {
+// Attention of kv head g's n_rep query heads over cache positions [p0, p1) (attn_decode,
+// attention.cpp:55-80), with the RoPE of the query heads and the key (attention.cpp:31-46)
+// and the store of the new K/V row at pos (kvcache.cpp:31-36). fetch() fills qkv (LDS) with
+// the head block [n_rep q heads | k | v] the QKV phase produced; it runs after the first K/V
+// tiles' loads are issued (the cached rows do not depend on this token), so the cache
+// latency overlaps the hand-off. NB = 4 (spans of more than two 32-position tiles): four
+// tiles are in flight at a time, each tile's registers reloaded with the tile four ahead as
+// soon as they are in LDS; NB = 1 or 2 (spans of that many tiles): all of them load up
+// front and nothing is reloaded (a load past the span would delay the hand-off's polls,
+// which wait for every load in flight). The
+// loads past the span re-read row p1 - 1 instead of being skipped: no load sits behind a
+// branch, and every wait for a tile is a fixed count of the loads issued after it.
+//   kPart false (attn_head): [p0, p1) = [start, pos]; out = the normalised heads, [n_rep][hd].
+//     The same workgroup runs head g for every token of a launch, so the rows it stores are
+//     the ones it later reads on this CU.
+//   kPart true (attn_part, caches longer than 512 positions): one split of [start, pos]
+//     (flash-decoding, split over workgroups). out[r * (hd + 2) ...] = the unnormalised o
+//     (P.V with P = e^(s - m)), then m and l (the running max and sum of the online
+//     softmax); the combine phase merges the splits. The split holding pos stores the new
+//     row through at agent scope (later tokens of the launch read it from other XCDs) and
+//     waits for the stores before returning, i.e. before its next puts. The cache is read at
+//     agent scope. An empty split leaves m = -inf, l = 0, o = 0 and does not wait for the
+//     head block.
+template <int HDM, bool kPart, int NB, class Fetch>
+__device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly, int g, int pos, int p0, int p1,
+                                          float* qkv, float* sm, float* out, Fetch&& fetch) {
     constexpr int kTV = (kTile * HDM / 4 + kT - 1) / kT;  // float4 of a K (or V) tile per thread
     constexpr int kPairs = (kMaxRep * HDM + kT - 1) / kT;  // (head, dim) pairs of P.V per thread
     const int hd = a.hd, d2 = hd / 2, hd4 = hd / 4;
     const int n_rep = a.H / a.G;
     const int tid = threadIdx.x;
     const int ks = hd + 4;
+    const int ho = hd + 2;
     float* qs = qkv;                  // [n_rep][hd], rotated in place
     float* kn = qkv + n_rep * hd;     // [hd]
     float* vn = kn + hd;              // [hd]
@@ -300,11 +368,20 @@ __device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly
     float* vt = kt + kTile * ks;      // [kTile][hd]
     float* pr = vt + kTile * hd;      // [n_rep][kTile]
     float* st = pr + n_rep * kTile;   // [n_rep][3]
+    if (kPart && p0 >= p1) {
+        for (int i = tid; i < n_rep * ho; i += kT) {
+            const int d = i % ho;
+            out[i] = d == hd ? -INFINITY : 0.0f;
+        }
+        __syncthreads();
+        return;
+    }
     const TF_GLOBAL float* cs = gptr(a.rope_cos + (int64_t)pos * d2);
     const TF_GLOBAL float* sn = gptr(a.rope_sin + (int64_t)pos * d2);
-    const int p1 = pos + 1;
 
-    auto load_tile = [&](int t0, float4 (&kr)[kTV], float4 (&vr)[kTV]) {
+    // tile i of the span, clamped to its last row
+    auto tile_at = [&](int i) { return min(p0 + i * kTile, p1 - 1); };
+    auto load_tile = [&](int t0, float4 (&kr)[kTV], float4 (&vr)[kTV]) __attribute__((always_inline)) {
         const int tn = min(kTile, p1 - t0);
 #pragma unroll
         for (int k = 0; k < kTV; ++k) {
@@ -312,12 +389,23 @@ __device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly
             i = i < tn * hd4 ? i : tn * hd4 - 1;
             const int j = i / hd4, c = i % hd4;
             const int64_t o = kv_at(a.layout, a.G, a.max_seq, hd, g, t0 + j) + 4 * c;
-            kr[k] = gload_f4(ly.kc + o);
-            vr[k] = gload_f4(ly.vc + o);
+            if constexpr (kPart) {
+                kr[k] = gload_f4_agent(ly.kc + o);
+                vr[k] = gload_f4_agent(ly.vc + o);
+            } else {
+                kr[k] = gload_f4(ly.kc + o);
+                vr[k] = gload_f4(ly.vc + o);
+            }
         }
     };
-    float4 kr_a[kTV], vr_a[kTV], kr_b[kTV], vr_b[kTV];
-    load_tile(start, kr_a, vr_a);
+    // four named buffers (an array of them indexed by an unrolled loop ends up in scratch)
+    float4 kr0[kTV], vr0[kTV], kr1[kTV], vr1[kTV], kr2[kTV], vr2[kTV], kr3[kTV], vr3[kTV];
+    load_tile(tile_at(0), kr0, vr0);
+    if constexpr (NB >= 2) load_tile(tile_at(1), kr1, vr1);
+    if constexpr (NB == 4) {
+        load_tile(tile_at(2), kr2, vr2);
+        load_tile(tile_at(3), kr3, vr3);
+    }
     fetch();
     // RoPE (rope_one, with the reference build's contractions)
     for (int i = tid; i < (n_rep + 1) * d2; i += kT) {
@@ -332,11 +420,17 @@ __device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly
         st[3 * tid + 1] = 0.0f;
     }
     __syncthreads();
-    {
+    const bool stores_row = pos >= p0 && pos < p1;
+    if (stores_row) {
         const int64_t o = kv_at(a.layout, a.G, a.max_seq, hd, g, pos);
         for (int j = tid; j < hd; j += kT) {
-            *gptr(ly.kc + o + j) = kn[j];
-            *gptr(ly.vc + o + j) = vn[j];
+            if constexpr (kPart) {
+                __hip_atomic_store(gptr(ly.kc + o + j), kn[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(gptr(ly.vc + o + j), vn[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                *gptr(ly.kc + o + j) = kn[j];
+                *gptr(ly.vc + o + j) = vn[j];
+            }
         }
     }
     const float scale = 1.0f / sqrtf((float)hd);
@@ -345,81 +439,125 @@ __device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly
     for (int k = 0; k < kPairs; ++k) o_acc[k] = 0.0f;
     const int lane = tid & 63, wave = tid >> 6;
 
-    auto tile = [&](int t0, float4 (&kr)[kTV], float4 (&vr)[kTV], float4 (&kn_r)[kTV], float4 (&vn_r)[kTV]) {
-        const int tn = min(kTile, p1 - t0);
-        if (t0 + kTile < p1) load_tile(t0 + kTile, kn_r, vn_r);
+    auto step = [&](int ti, float4 (&kr)[kTV], float4 (&vr)[kTV]) __attribute__((always_inline)) {
+            const int t0 = p0 + ti * kTile;
+            const int tn = min(kTile, p1 - t0);  // <= 0 past the last tile
 #pragma unroll
-        for (int k = 0; k < kTV; ++k) {
-            const int i = tid + k * kT;
-            if (i < tn * hd4) {
-                const int j = i / hd4, c = i % hd4;
-                const bool is_new = t0 + j == pos;  // the cache row may still be the old one
-                *(float4*)(kt + j * ks + 4 * c) = is_new ? *(const float4*)(kn + 4 * c) : kr[k];
-                *(float4*)(vt + j * hd + 4 * c) = is_new ? *(const float4*)(vn + 4 * c) : vr[k];
+            for (int k = 0; k < kTV; ++k) {
+                const int i = tid + k * kT;
+                if (i < tn * hd4) {
+                    const int j = i / hd4, c = i % hd4;
+                    const bool is_new = t0 + j == pos;  // the cache row may still be the old one
+                    *(float4*)(kt + j * ks + 4 * c) = sel4(is_new, *(const float4*)(kn + 4 * c), kr[k]);
+                    *(float4*)(vt + j * hd + 4 * c) = sel4(is_new, *(const float4*)(vn + 4 * c), vr[k]);
+                }
             }
-        }
-        __syncthreads();
-        // scores in dot_f32's order (8 lanes, then hsum8; quant.cpp:198-214)
-        for (int i = tid; i < n_rep * tn; i += kT) {
-            const int r = i / tn, j = i % tn;
-            const float* qr = qs + r * hd;
-            const float* krow = kt + j * ks;
-            float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            for (int e = 0; e < hd; e += 8) {
-                const float4 q0 = *(const float4*)(qr + e), q1 = *(const float4*)(qr + e + 4);
-                const float4 x0 = *(const float4*)(krow + e), x1 = *(const float4*)(krow + e + 4);
-                c[0] = fmaf(q0.x, x0.x, c[0]);
-                c[1] = fmaf(q0.y, x0.y, c[1]);
-                c[2] = fmaf(q0.z, x0.z, c[2]);
-                c[3] = fmaf(q0.w, x0.w, c[3]);
-                c[4] = fmaf(q1.x, x1.x, c[4]);
-                c[5] = fmaf(q1.y, x1.y, c[5]);
-                c[6] = fmaf(q1.z, x1.z, c[6]);
-                c[7] = fmaf(q1.w, x1.w, c[7]);
+            if constexpr (NB == 4) load_tile(tile_at(ti + 4), kr, vr);
+            if (tn > 0) {
+                __syncthreads();
+                // scores in dot_f32's order (8 lanes, then hsum8; quant.cpp:198-214)
+                for (int i = tid; i < n_rep * tn; i += kT) {
+                    const int r = i / tn, j = i % tn;
+                    const float* qr = qs + r * hd;
+                    const float* krow = kt + j * ks;
+                    float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                    for (int e = 0; e < hd; e += 8) {
+                        const float4 q0 = *(const float4*)(qr + e), q1 = *(const float4*)(qr + e + 4);
+                        const float4 x0 = *(const float4*)(krow + e), x1 = *(const float4*)(krow + e + 4);
+                        c[0] = fmaf(q0.x, x0.x, c[0]);
+                        c[1] = fmaf(q0.y, x0.y, c[1]);
+                        c[2] = fmaf(q0.z, x0.z, c[2]);
+                        c[3] = fmaf(q0.w, x0.w, c[3]);
+                        c[4] = fmaf(q1.x, x1.x, c[4]);
+                        c[5] = fmaf(q1.y, x1.y, c[5]);
+                        c[6] = fmaf(q1.z, x1.z, c[6]);
+                        c[7] = fmaf(q1.w, x1.w, c[7]);
+                    }
+                    pr[r * kTile + j] = scale * (((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7])));
+                }
+                __syncthreads();
+                for (int r = wave; r < n_rep; r += kNW) {
+                    const float v = lane < tn ? pr[r * kTile + lane] : -INFINITY;
+                    const float m_old = st[3 * r];
+                    const float m_new = fmaxf(m_old, wave_max(v));
+                    const float e = lane < tn ? expf(v - m_new) : 0.0f;
+                    if (lane < tn) pr[r * kTile + lane] = e;
+                    const float l_tile = wave_sum(e);
+                    if (lane == 0) {
+                        const float alpha = expf(m_old - m_new);
+                        st[3 * r] = m_new;
+                        st[3 * r + 1] = fmaf(st[3 * r + 1], alpha, l_tile);
+                        st[3 * r + 2] = alpha;
+                    }
+                }
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < kPairs; ++k) {
+                    const int pi = tid + k * kT;
+                    if (pi < n_rep * hd) {
+                        const int r = pi / hd, d = pi % hd;
+                        float o = o_acc[k] * st[3 * r + 2];
+                        for (int j = 0; j < tn; ++j) o = fmaf(pr[r * kTile + j], vt[j * hd + d], o);
+                        o_acc[k] = o;
+                    }
+                }
+                __syncthreads();
             }
-            pr[r * kTile + j] = scale * (((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7])));
+    };
+    if constexpr (NB == 4) {
+        const int n_tiles = (p1 - p0 + kTile - 1) / kTile;
+        for (int it = 0; it < n_tiles; it += 4) {
+            step(it, kr0, vr0);
+            step(it + 1, kr1, vr1);
+            step(it + 2, kr2, vr2);
+            step(it + 3, kr3, vr3);
         }
-        __syncthreads();
-        for (int r = wave; r < n_rep; r += kNW) {
-            const float v = lane < tn ? pr[r * kTile + lane] : -INFINITY;
-            const float m_old = st[3 * r];
-            const float m_new = fmaxf(m_old, wave_max(v));
-            const float e = lane < tn ? expf(v - m_new) : 0.0f;
-            if (lane < tn) pr[r * kTile + lane] = e;
-            const float l_tile = wave_sum(e);
-            if (lane == 0) {
-                const float alpha = expf(m_old - m_new);
-                st[3 * r] = m_new;
-                st[3 * r + 1] = fmaf(st[3 * r + 1], alpha, l_tile);
-                st[3 * r + 2] = alpha;
-            }
-        }
-        __syncthreads();
+    } else {
+        step(0, kr0, vr0);
+        if constexpr (NB == 2) step(1, kr1, vr1);
+    }
+    if constexpr (kPart) {
 #pragma unroll
         for (int k = 0; k < kPairs; ++k) {
             const int pi = tid + k * kT;
-            if (pi < n_rep * hd) {
-                const int r = pi / hd, d = pi % hd;
-                float o = o_acc[k] * st[3 * r + 2];
-                for (int j = 0; j < tn; ++j) o = fmaf(pr[r * kTile + j], vt[j * hd + d], o);
-                o_acc[k] = o;
-            }
+            if (pi < n_rep * hd) out[(pi / hd) * ho + pi % hd] = o_acc[k];
         }
-        __syncthreads();
-    };
-    for (int t0 = start; t0 < p1;) {
-        tile(t0, kr_a, vr_a, kr_b, vr_b);
-        t0 += kTile;
-        if (t0 >= p1) break;
-        tile(t0, kr_b, vr_b, kr_a, vr_a);
-        t0 += kTile;
-    }
+        if (tid < n_rep) {
+            out[tid * ho + hd] = st[3 * tid];
+            out[tid * ho + hd + 1] = st[3 * tid + 1];
+        }
+        if (stores_row) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
 #pragma unroll
-    for (int k = 0; k < kPairs; ++k) {
-        const int pi = tid + k * kT;
-        if (pi < n_rep * hd) out[pi] = o_acc[k] / st[3 * (pi / hd) + 1];
+        for (int k = 0; k < kPairs; ++k) {
+            const int pi = tid + k * kT;
+            if (pi < n_rep * hd) out[pi] = o_acc[k] / st[3 * (pi / hd) + 1];
+        }
     }
     __syncthreads();
+}
+
+template <int HDM, class Fetch>
+__device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly, int g, int pos, int start, float* qkv,
+                                          float* sm, float* out, Fetch&& fetch) {
+    const int n = pos + 1 - start;
+    if (n > 2 * kTile)
+        attn_span<HDM, false, 4>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch);
+    else if (n > kTile)
+        attn_span<HDM, false, 2>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch);
+    else
+        attn_span<HDM, false, 1>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch);
+}
+
+template <int HDM, class Fetch>
+__device__ __forceinline__ void attn_part(const StepArgs& a, const StepLayer& ly, int g, int pos, int p0, int p1,
+                                          float* qkv, float* sm, float* out, Fetch&& fetch) {
+    if (p1 - p0 > 2 * kTile)
+        attn_span<HDM, true, 4>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch);
+    else if (p1 - p0 > kTile)
+        attn_span<HDM, true, 2>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch);
+    else
+        attn_span<HDM, true, 1>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch);
 }
 
 // Floats of LDS the attention scratch needs.
@@ -437,6 +575,14 @@ __host__ __device__ inline int region_floats(int D, int F, int n_rep, int hd, in
     return 2 * n_wg > r ? 2 * n_wg : r;
 }
 
+// Slices per query head in the layout where every workgroup splits: the largest power of
+// two dividing hd with one workgroup per (head, slice) pair.
+__host__ __device__ inline int split_all_parts(int H, int hd, int n_wg) {
+    int parts = 1;
+    while (2 * parts <= hd && hd % (2 * parts) == 0 && H * 2 * parts <= n_wg) parts *= 2;
+    return parts;
+}
+
 // LDS bytes of one staged Q8_0 row of K elements: the q bytes padded to whole 1 KiB load
 // instructions, then the fp16 scales padded to 256-byte ones.
 __host__ __device__ inline int row_slot_bytes(int K) {
@@ -448,13 +594,14 @@ __host__ __device__ inline int row_slot_bytes(int K) {
 struct StepConst {
     StepArgs a;
     int L, D, F, G, hd, n_rep, Hd, HB, nwg, P, attn_wg0;
+    int A, parts, A_all, parts_all, PW;  // split attention: splits per kv head and slices per head of both layouts
     int o_xr, o_xs, o_x16, o_qkv, o_att;  // LDS byte offsets of the arrays below the layer table
     int o_down, down_slot;                // staged ffn_down rows (o_down 0: not staged), bytes per wave
     uint32_t e0;
     int pos0;
     u64 key0;
     // exchange buffers (word offsets into a.ex), each twice (layer or token parity)
-    int XA, XB, QKV, ATT, HH, DONE, BEST;
+    int XA, XB, QKV, ATT, HH, DONE, BEST, PART;
 };
 
 template <int TL, int TO, int HDM>
@@ -485,7 +632,12 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         c.HB = (c.n_rep + 2) * args.hd;  // words of one kv head block [q heads | k | v]
         c.nwg = gridDim.x;
         c.P = 6 * c.L + 8;               // epochs per token
-        c.attn_wg0 = c.nwg - c.G;        // workgroups attn_wg0.. run the attention heads
+        c.A = args.split;                // > 0: splits per kv head of the long-cache attention (trailing layout)
+        c.attn_wg0 = c.nwg - c.G * (c.A ? c.A : 1);  // workgroups attn_wg0.. run the attention
+        c.parts = c.A ? c.A / c.n_rep : 1;  // each attention workgroup then merges hd / parts outputs of one head
+        c.A_all = args.split_all;        // > 0: splits per kv head when every workgroup splits
+        c.parts_all = split_all_parts(args.H, c.hd, c.nwg);
+        c.PW = args.H * (c.A > c.A_all ? c.A : c.A_all) * (c.hd + 2);  // words of one parity of PART
         const int kmax = c.D > c.F ? c.D : c.F;
         c.o_xr = (int)(((size_t)c.L * sizeof(StepLayer) + 15) / 16 * 16);
         c.o_xs = c.o_xr + 4 * ((c.D + 3) / 4 * 4);
@@ -493,7 +645,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         c.o_qkv = c.o_xs + 4 * ((region_floats(c.D, c.F, c.n_rep, c.hd, c.nwg) + 3) / 4 * 4);
         c.o_att = c.o_qkv + 4 * c.HB;
         c.down_slot = row_slot_bytes(c.F);
-        c.o_down = (args.stage_lds & 1) ? (c.o_att + 4 * c.n_rep * c.hd + 15) / 16 * 16 : 0;
+        c.o_down = (args.stage_lds & 1) ? (c.o_att + 4 * c.n_rep * (c.hd + 2) + 15) / 16 * 16 : 0;
         c.e0 = args.ctl->epoch;
         c.pos0 = args.ctl->pos;
         c.key0 = args.ctl->key;
@@ -504,6 +656,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         c.HH = c.ATT + 2 * c.Hd;
         c.DONE = c.HH + 2 * c.F;
         c.BEST = c.DONE + 2 * c.nwg;
+        c.PART = c.BEST + 4 * c.nwg;
     }
     {
         const u64* src = (const u64*)args.layers;
@@ -646,8 +799,8 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             // ---- 2: attention (kv head g on workgroup attn_wg0 + g), then 4: gate/up
             // ---- 3: wo + residual (workgroups without an attention head), then 4: gate/up
             // The workgroups without an attention head issue their gate/up tiles and stage
-            // their ffn_down row before they wait for the attention output: cfg1's 50 MB of
-            // gate/up and down stream in while attention runs, instead of after wo. (Giving
+            // their ffn_down row before they wait for the attention output: a 1B model's 53 MB
+            // of gate/up and down per layer stream in while attention runs, not after wo. (Giving
             // the attention workgroups wo rows too makes them the stragglers of wo.)
             {
                 const int D = sc.D;
@@ -662,7 +815,75 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     gather<kGD, 1>(X(sc.XB) + par * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl);
                     stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
                 };
-                if (wg >= sc.attn_wg0) {
+                // ---- 2 (caches longer than 512 positions): kv head g's positions split over
+                // A workgroups, then each (query head, slice of hd / parts outputs) merged
+                // from the A partials by one workgroup. Two layouts, chosen per token from
+                // the span's length (the same on every workgroup):
+                //   trailing: the G * A workgroups from attn_wg0 on split and merge while the
+                //     others start wo's and ffn_down's loads; best while a split is at most
+                //     two tiles;
+                //   all: workgroups 0.. split (A_all per kv head) and merge, then every
+                //     workgroup runs wo; more splits, shorter ones, for long spans.
+                // The partials carry epoch slot 6 of the layer (unused by the other phases;
+                // the argmax words use it only past the last layer; never 0).
+                const int span = sc.pos0 + t + 1 - sc.a.att_start;
+                const bool all = sc.A_all && span > 2 * kTile * sc.A;
+                if (sc.A && (all || wg >= sc.attn_wg0)) {
+                    const int A = all ? sc.A_all : sc.A, parts = all ? sc.parts_all : sc.parts;
+                    const int G = sc.G, HB = sc.HB, n_rep = sc.n_rep, hd = sc.hd, ho = hd + 2;
+                    const int aw = all ? wg : wg - sc.attn_wg0;
+                    u64* pb = X(sc.PART) + par * sc.PW;
+                    float* qkv = (float*)(smem + sc.o_qkv);
+                    float* part = (float*)(smem + sc.o_att);
+                    __syncthreads();  // the QKV phase's waves are done with xs
+                    if (aw < G * A) {
+                        const int g = aw % G, s = aw / G;
+                        const int pos = sc.pos0 + t, start = sc.a.att_start;
+                        const int chunk = (pos + 1 - start + A - 1) / A;
+                        const int p0 = start + s * chunk, p1 = min(pos + 1, p0 + chunk);
+                        attn_part<HDM>(sc.a, ly, g, pos, p0, p1, qkv, xs, part, [&]() {
+                            gather<kGD, 1>(X(sc.QKV) + par * G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0,
+                                           sc.a.ctl);
+                            __syncthreads();
+                        });
+                        u64* pw_base = pb + (size_t)(g * A + s) * n_rep * ho;
+                        for (int i = tid; i < n_rep * ho; i += kT) put(pw_base + i, part[i], E(t, l, 6));
+                    }
+                    if (aw < sc.a.H * parts) {
+                        const int sz = hd / parts;
+                        const int h = aw / parts, d0 = (aw % parts) * sz;
+                        const int g = h / n_rep, r = h % n_rep, w = sz + 2;
+                        float* buf = xs;  // [A][sz, m, l]
+                        __syncthreads();
+                        gather_idx<3>(pb, [&](int j) {
+                            const int s = j / w, k = j % w;
+                            return (size_t)((g * A + s) * n_rep + r) * ho + (k < sz ? d0 + k : hd + k - sz);
+                        }, A * w, E(t, l, 6), buf, sc.a.ctl);
+                        __syncthreads();
+                        for (int k = wave; k < sz; k += kNW) {
+                            float m = -INFINITY;
+                            for (int s = lane; s < A; s += kWave) m = fmaxf(m, buf[s * w + sz]);
+                            m = wave_max(m);
+                            float lsum = 0.0f, osum = 0.0f;
+                            for (int s = lane; s < A; s += kWave) {
+                                const float wt = expf(buf[s * w + sz] - m);
+                                lsum = fmaf(buf[s * w + sz + 1], wt, lsum);
+                                osum = fmaf(buf[s * w + k], wt, osum);
+                            }
+                            lsum = wave_sum(lsum);
+                            osum = wave_sum(osum);
+                            if (lane == 0) put(X(sc.ATT) + par * sc.Hd + h * hd + d0 + k, osum / lsum, E(t, l, 2));
+                        }
+                    }
+                }
+                if (sc.A && !all && wg >= sc.attn_wg0) {
+                    auto down_then_input = [&]() {
+                        issue_down(ly);
+                        gu_input();
+                    };
+                    gemv_phase<TL, 2, GEMV_SILU, 2>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                                                    x16, down_then_input, gu_epi);
+                } else if (!sc.A && wg >= sc.attn_wg0) {
                     const int g = wg - sc.attn_wg0;
                     const int HB = sc.HB;
                     float* qkv = (float*)(smem + sc.o_qkv);
@@ -696,7 +917,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                             put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
                         };
                         gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, Hd, wg * kNW + wave,
-                                                         sc.attn_wg0 * kNW, xs, x16, prep, epi);
+                                                         (all ? sc.nwg : sc.attn_wg0) * kNW, xs, x16, prep, epi);
                         __syncthreads();  // every wave's wo rows are read out of xs before the input is staged
                         gu_input();
                     };

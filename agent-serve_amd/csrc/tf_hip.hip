@@ -65,6 +65,7 @@ struct tf_hip_ctx {
     int path_opt = TF_HIP_PATH_STEP;  // requested decode path
     int step_state = -1;              // -1 undecided, 0 graph path, 1 step kernel ready
     int step_tl = -1, step_to = -1, n_wg = 0;
+    int step_split = 0, step_split_all = 0;  // the step kernel's attention splits (step_split*)
     StepLayer* d_layers = nullptr;
     unsigned long long* ex = nullptr;
     uint32_t epoch = 0;               // exchange epochs consumed (mirrors ctl->epoch)
@@ -421,9 +422,10 @@ int ensure_graph(tf_hip_ctx* c) {
 
 // Decides once, after every tensor is uploaded, whether the persistent step kernel runs
 // this model: one format for all layer matrices, the embedding in the lm_head's format, a
-// compiled (format, head size) combination, one attention split (max_seq <= 512: longer
-// caches keep the split attention of the graph path), cooperative launch, and inputs
-// within the kernel's per-thread capacities. Returns 1 (step kernel), 0 (graph) or < 0.
+// compiled (format, head size) combination, cooperative launch, and inputs within the
+// kernel's per-thread capacities. Caches longer than 512 positions split each layer's
+// attention over workgroups (step_split, step_split_all). Returns 1 (step kernel), 0
+// (graph) or < 0.
 int ensure_step(tf_hip_ctx* c) {
     if (c->path_opt != TF_HIP_PATH_STEP) return 0;
     if (c->step_state >= 0) return c->step_state;
@@ -439,7 +441,6 @@ int ensure_step(tf_hip_ctx* c) {
             if (mat(c, TF_HIP_SLOT_LAYER(l, k)).type != tl) return 0;
     const DevMat& out = output_mat(c);
     if (mat(c, TF_HIP_SLOT_TOKEN_EMBD).type != out.type || !step_supported(tl, out.type, p.head_dim)) return 0;
-    if (c->S != 1) return 0;
     int coop = 0;
     if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device) != hipSuccess || !coop) return 0;
     const int n_wg = device_cu_count();
@@ -447,6 +448,9 @@ int ensure_step(tf_hip_ctx* c) {
     if (n_wg < 2 * p.n_kv_head || p.n_embd + n_wg > 4096 || p.n_ff > 10240 || 2 * n_wg > 1024 ||
         (n_rep + 2) * p.head_dim > 4096 || p.n_head * p.head_dim > 4096)
         return 0;
+    // caches longer than 512 positions: attention split over workgroups
+    const int split = p.max_seq > 512 ? step_split(p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, n_wg) : 0;
+    if (p.max_seq > 512 && !split) return 0;
     std::vector<StepLayer> tab((size_t)p.n_layer);
     for (int l = 0; l < p.n_layer; ++l) {
         auto M = [&](int k) -> const DevMat& { return mat(c, TF_HIP_SLOT_LAYER(l, k)); };
@@ -467,7 +471,11 @@ int ensure_step(tf_hip_ctx* c) {
         t.kc = c->kc + (size_t)l * c->kv_layer;
         t.vc = c->vc + (size_t)l * c->kv_layer;
     }
-    const size_t words = step_exchange_words(p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, n_wg);
+    const int split_all =
+        split ? step_split_all(p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, n_wg) : 0;
+    c->step_split_all = split_all;
+    const size_t words = step_exchange_words(p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, n_wg,
+                                             split > split_all ? split : split_all);
     if ((rc = dalloc(c, &c->d_layers, tab.size() * sizeof(StepLayer))) || (rc = dalloc(c, &c->ex, words * 8)))
         return rc;
     HIPCHK(c, hipMemcpy(c->d_layers, tab.data(), tab.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
@@ -475,6 +483,7 @@ int ensure_step(tf_hip_ctx* c) {
     c->step_tl = tl;
     c->step_to = out.type;
     c->n_wg = n_wg;
+    c->step_split = split;
     c->step_state = 1;
     return 1;
 }
@@ -508,6 +517,8 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
     a.lm_every = lm_every;
     a.att_start = att_start;
     a.stage_lds = step_stage_lds(c->step_tl, p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, c->n_wg);
+    a.split = c->step_split;
+    a.split_all = c->step_split_all;
     const hipError_t e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);
     if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("step kernel launch: ") + hipGetErrorString(e));
     c->epoch += (uint32_t)(n * (6 * p.n_layer + 8));

@@ -144,6 +144,8 @@ struct StepArgs {
     int lm_every;              // 1: lm_head for every token; 0: for the last one only (prefill)
     int att_start;             // first cache position attention covers (0, or the prefill chunk's start)
     int stage_lds;             // bit 0: ffn_down rows staged in LDS (step_stage_lds)
+    int split;                 // > 0: split attention on the trailing workgroups, splits per kv head (step_split)
+    int split_all;             // > 0: splits per kv head when every workgroup splits (step_split_all)
 };
 
 // ---------------------------------------------------------------- prefill on the matrix cores
@@ -204,7 +206,14 @@ hipError_t launch_pf_attn(const float* q, int64_t ldq, const float* kc, const fl
 hipError_t launch_pf_tail(Ctl* ctl, int pos_last, const int32_t* hist, const float* xrow, float* x, int D,
                           hipStream_t st);
 
-size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg);
+// Exchange words of the step kernel; split: the larger of its two splits per kv head.
+size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg, int split);
+// Splits per kv head of the step kernel's attention for caches longer than 512 positions,
+// or 0 when the model's shape does not allow it: step_split on the trailing workgroups
+// (the others stream wo's and the FFN's weights meanwhile), step_split_all on every
+// workgroup (for long spans).
+int step_split(int D, int F, int H, int G, int hd, int n_wg);
+int step_split_all(int D, int F, int H, int G, int hd, int n_wg);
 size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg, int stage_lds);
 // Which weight rows the step kernel stages in LDS ahead of their phase (bits of
 // StepArgs::stage_lds): the ffn_down rows (bit 0) for Q8_0 layers with at most one row per

@@ -48,6 +48,7 @@ void usage() {
                  "  --max-seq N          KV cache length (default 4096)\n"
                  "  --kv-layout seq|head override KV layout\n"
                  "  --device N           HIP device (default 0)\n"
+                 "  --decode-path P      step (persistent kernel, the default) | graph\n"
                  "  --profile            print the per-kernel-class breakdown of one greedy pass\n");
 }
 
@@ -105,7 +106,7 @@ int sample_logits(const float* logits, int n, float temperature, float top_p, st
 }  // namespace
 
 int main(int argc, char** argv) {
-    std::string model_path, prompt, token_str, stage = "v2", kv_layout;
+    std::string model_path, prompt, token_str, stage = "v2", kv_layout, decode_path = "step";
     int n_predict = 64, seed = 42, max_seq = 4096, device = 0;
     float temp = 0, topp = 0.9f;
     bool profile = false;
@@ -127,6 +128,7 @@ int main(int argc, char** argv) {
         else if (a == "--max-seq") max_seq = std::stoi(next());
         else if (a == "--kv-layout") kv_layout = next();
         else if (a == "--device") device = std::stoi(next());
+        else if (a == "--decode-path") decode_path = next();
         else if (a == "--pin" || a == "--no-bos") {
         } else if (a == "--profile") profile = true;
         else if (a == "-h" || a == "--help") {
@@ -155,6 +157,12 @@ int main(int argc, char** argv) {
         if (token_str.empty())
             die(prompt.empty() ? "empty prompt" : "--prompt needs the reference tokenizer; pass --tokens");
         Model model(model_path, cfg);
+        if (decode_path == "graph" || decode_path == "step") {
+            if (tf_hip_set_decode_path(model.ctx(), decode_path == "graph" ? TF_HIP_PATH_GRAPH : TF_HIP_PATH_STEP))
+                die("tf_hip_set_decode_path failed");
+        } else {
+            die("--decode-path takes step or graph");
+        }
         std::fprintf(stderr, "%s\n", model.describe().c_str());
         std::vector<int> ids = parse_tokens(token_str);
         if (ids.empty()) die("empty prompt");

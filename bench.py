@@ -149,6 +149,9 @@ def context_sweep(pkg, path, info):
     reset, then CTX_STEPS greedy tokens timed by HIP events; GB/s counts the weights once
     and the KV rows of every position read (tf_hip_decode_bytes)."""
     m = pkg.HipModel(path, max_seq=CTX_MAX_SEQ, kv_layout=0)
+    # warm-up: the step kernel's one-time set-up and first launches stay out of the points
+    m.prefill(pkg.synth_prompt(info["seed"], 8, info["n_vocab"]), want_logits=False)
+    m.generate(4)
     out = []
     for n in CTX_PROMPTS:
         prompt = pkg.synth_prompt(info["seed"] + n, n, info["n_vocab"])

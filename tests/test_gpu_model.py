@@ -30,16 +30,45 @@ def test_small_models(pkg, gguf, preset, layout, path):
 @pytest.mark.parametrize("preset,want", [("tiny_q8", STEP), ("tiny_f32", STEP), ("small_q8", STEP),
                                          ("tiny_mixq4", GRAPH)])
 def test_decode_path_selection(pkg, gguf, preset, want):
-    """The persistent step kernel runs models whose layer matrices share a compiled format;
+    """The persistent step kernel runs models whose layer matrices share a compiled format,
+    also with caches longer than 512 positions (attention split over workgroups);
     mixed-format models keep the graph path; PATH_GRAPH forces the graph."""
     hip = pkg.HipModel(gguf(preset), max_seq=64)
     assert hip.decode_path() == want
     hip.set_decode_path(GRAPH)
     assert hip.decode_path() == GRAPH
     hip.close()
-    big = pkg.HipModel(gguf("tiny_q8"), max_seq=1024)  # split attention: graph path
-    assert big.decode_path() == GRAPH
+    big = pkg.HipModel(gguf(preset), max_seq=1024)
+    assert big.decode_path() == want
     big.close()
+
+
+@pytest.mark.parametrize("path", [GRAPH, STEP], ids=["graph", "step"])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("preset", ["tiny_q8", "tiny_f32", "tiny_qwen", "small_q8"])
+def test_long_cache_split_attention(pkg, gguf, preset, layout, path):
+    """A 600-token prompt in a 1024-position cache: the step kernel's attention splits the
+    positions over its trailing workgroups and merges the splits there, the graph path's
+    over split workgroups and a combine launch; both against the oracle while decoding
+    past it."""
+    info = pkg.synth_preset_info(preset)
+    prompt = pkg.synth_prompt(info["seed"] + 7, 600, info["n_vocab"])
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, 1024, layout, decode_path=path)
+    print(f"{preset} layout {layout} path {path}: logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
+
+
+# (preset, prompt tokens, cache positions): the step kernel's splits move from its trailing
+# workgroups to every workgroup once the span passes 64 positions per trailing split
+# (tiny_f32: 16 splits per kv head, so past 1024; tiny_q8: 64, past 4096). The prompts end
+# a few positions short of that, so the per-token decodes and the one-launch greedy loop
+# both cross it.
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("preset,n_prompt,max_seq", [("tiny_f32", 1018, 2048), ("tiny_q8", 4090, 4200)])
+def test_long_cache_split_layout_switch(pkg, gguf, preset, n_prompt, max_seq, layout):
+    info = pkg.synth_preset_info(preset)
+    prompt = pkg.synth_prompt(info["seed"] + 11, n_prompt, info["n_vocab"])
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, max_seq, layout, decode_path=STEP)
+    print(f"{preset} {n_prompt} layout {layout}: logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
 
 
 TOKENS, MFMA = 0, 1  # HipModel.PREFILL_TOKENS, HipModel.PREFILL_MFMA
