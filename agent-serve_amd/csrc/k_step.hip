@@ -77,8 +77,8 @@ hipError_t launch_t(const StepArgs& a, int n_wg, hipStream_t st) {
 
 }  // namespace
 
-bool step_supported(int tl, int to, int hd) {
-    if (hd > 128) return false;
+bool step_supported(int tl, int to, int hd, int n_rep) {
+    if (hd > 128 || n_rep > step_detail::kMaxRep) return false;
     return (tl == TF_HIP_TYPE_Q8_0 && to == TF_HIP_TYPE_Q8_0) || (tl == TF_HIP_TYPE_F32 && to == TF_HIP_TYPE_F32 && hd <= 64);
 }
 

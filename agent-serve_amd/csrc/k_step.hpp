@@ -314,14 +314,18 @@ __device__ __forceinline__ void gemv_phase(int nseg, const int (&groups)[3], Seg
     }
     __syncthreads();
     prep();
+    // the last one or two tiles are consumed without loading past them: a load issued there
+    // (clamped, so a re-read) would sit in front of the next phase's exchange reads, which
+    // complete after it
     int k = 0;
-    for (; k + 2 <= n_tiles; k += 2) {
+    for (; k + 2 < n_tiles; k += 2) {
         consume(k, wa, ea);
         load_k(k + 2, wa, ea);
         consume(k + 1, wb, eb);
         load_k(k + 3, wb, eb);
     }
     if (k < n_tiles) consume(k, wa, ea);
+    if (k + 1 < n_tiles) consume(k + 1, wb, eb);
 }
 
 __device__ __forceinline__ int64_t kv_at(int layout, int G, int max_seq, int hd, int g, int p) {
@@ -406,14 +410,28 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
         load_tile(tile_at(2), kr2, vr2);
         load_tile(tile_at(3), kr3, vr3);
     }
+    // this thread's RoPE cos/sin, read before the hand-off (after it they would cost another
+    // memory round trip on the attention's critical path)
+    constexpr int kRope = ((kMaxRep + 1) * HDM / 2 + kT - 1) / kT;
+    float rc[kRope], rs[kRope];
+#pragma unroll
+    for (int k = 0; k < kRope; ++k) {
+        const int j = (tid + k * kT) % d2;
+        rc[k] = cs[j];
+        rs[k] = sn[j];
+    }
     fetch();
     // RoPE (rope_one, with the reference build's contractions)
-    for (int i = tid; i < (n_rep + 1) * d2; i += kT) {
-        const int r = i / d2, j = i % d2;
-        float* v = qs + r * hd;  // r == n_rep is the key
-        const float x0 = v[j], x1 = v[j + d2], c = cs[j], s = sn[j];
-        v[j] = fmaf(x0, c, -(x1 * s));
-        v[j + d2] = fmaf(x0, s, x1 * c);
+#pragma unroll
+    for (int k = 0; k < kRope; ++k) {
+        const int i = tid + k * kT;
+        if (i < (n_rep + 1) * d2) {
+            const int r = i / d2, j = i % d2;
+            float* v = qs + r * hd;  // r == n_rep is the key
+            const float x0 = v[j], x1 = v[j + d2], c = rc[k], s = rs[k];
+            v[j] = fmaf(x0, c, -(x1 * s));
+            v[j + d2] = fmaf(x0, s, x1 * c);
+        }
     }
     if (tid < n_rep) {
         st[3 * tid] = -INFINITY;
@@ -722,6 +740,9 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         for (int l = 0; l < sc.L; ++l) {
             const StepLayer& ly = lay[l];
             const int par = l & 1;
+            // split attention layout of this token (caches longer than 512 positions), see phase 2
+            const int span = sc.pos0 + t + 1 - sc.a.att_start;
+            const bool all = sc.A_all && span > 2 * kTile * sc.A;
             // ---- 1: QKV (attn_norm fused)
             {
                 const int D = sc.D;
@@ -800,8 +821,9 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             // ---- 3: wo + residual (workgroups without an attention head), then 4: gate/up
             // The workgroups without an attention head issue their gate/up tiles and stage
             // their ffn_down row before they wait for the attention output: a 1B model's 53 MB
-            // of gate/up and down per layer stream in while attention runs, not after wo. (Giving
-            // the attention workgroups wo rows too makes them the stragglers of wo.)
+            // of gate/up and down per layer stream in while attention runs, not after wo. (The
+            // attention workgroups take no wo rows: with their gate/up and ffn_down loads issued
+            // before wo they are wo's stragglers, after it gate/up's.)
             {
                 const int D = sc.D;
                 float wr[NWR];
@@ -815,6 +837,22 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     gather<kGD, 1>(X(sc.XB) + par * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl);
                     stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
                 };
+                // ---- 3: wo + residual, rows dealt over nw waves from wave 0
+                auto wo_phase = [&](int nw) {
+                    const int Hd = sc.Hd;
+                    float wo_wr[1];
+                    const int groups[3] = {(int)ly.wo.N, 0, 0};
+                    auto seg = [&](int, int) -> const DevMat& { return ly.wo; };
+                    auto prep = [&]() {
+                        gather<kGD, 1>(X(sc.ATT) + par * Hd, Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl);
+                        stage(xs, Hd, false, wo_wr, 0.0f, xs, x16, Fmt<TL>::kNeedSums, red);
+                    };
+                    auto epi = [&](int, int row, float v, float, float) {
+                        put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
+                    };
+                    gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, Hd, wg * kNW + wave, nw, xs, x16, prep,
+                                                     epi);
+                };
                 // ---- 2 (caches longer than 512 positions): kv head g's positions split over
                 // A workgroups, then each (query head, slice of hd / parts outputs) merged
                 // from the A partials by one workgroup. Two layouts, chosen per token from
@@ -826,8 +864,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 //     workgroup runs wo; more splits, shorter ones, for long spans.
                 // The partials carry epoch slot 6 of the layer (unused by the other phases;
                 // the argmax words use it only past the last layer; never 0).
-                const int span = sc.pos0 + t + 1 - sc.a.att_start;
-                const bool all = sc.A_all && span > 2 * kTile * sc.A;
                 if (sc.A && (all || wg >= sc.attn_wg0)) {
                     const int A = all ? sc.A_all : sc.A, parts = all ? sc.parts_all : sc.parts;
                     const int G = sc.G, HB = sc.HB, n_rep = sc.n_rep, hd = sc.hd, ho = hd + 2;
@@ -905,19 +941,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 } else {
                     auto wo_then_input = [&]() {
                         issue_down(ly);
-                        const int Hd = sc.Hd;
-                        float wo_wr[1];
-                        const int groups[3] = {(int)ly.wo.N, 0, 0};
-                        auto seg = [&](int, int) -> const DevMat& { return ly.wo; };
-                        auto prep = [&]() {
-                            gather<kGD, 1>(X(sc.ATT) + par * Hd, Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl);
-                            stage(xs, Hd, false, wo_wr, 0.0f, xs, x16, Fmt<TL>::kNeedSums, red);
-                        };
-                        auto epi = [&](int, int row, float v, float, float) {
-                            put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
-                        };
-                        gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, Hd, wg * kNW + wave,
-                                                         (all ? sc.nwg : sc.attn_wg0) * kNW, xs, x16, prep, epi);
+                        wo_phase((all ? sc.nwg : sc.attn_wg0) * kNW);
                         __syncthreads();  // every wave's wo rows are read out of xs before the input is staged
                         gu_input();
                     };

@@ -440,7 +440,9 @@ int ensure_step(tf_hip_ctx* c) {
         for (int k : kinds)
             if (mat(c, TF_HIP_SLOT_LAYER(l, k)).type != tl) return 0;
     const DevMat& out = output_mat(c);
-    if (mat(c, TF_HIP_SLOT_TOKEN_EMBD).type != out.type || !step_supported(tl, out.type, p.head_dim)) return 0;
+    if (mat(c, TF_HIP_SLOT_TOKEN_EMBD).type != out.type ||
+        !step_supported(tl, out.type, p.head_dim, p.n_head / p.n_kv_head))
+        return 0;
     int coop = 0;
     if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device) != hipSuccess || !coop) return 0;
     const int n_wg = device_cu_count();

@@ -220,8 +220,9 @@ size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg,
 // wave and the LDS for them. (Staging the next layer's QKV rows as well was measured: the
 // exchange that waits behind their loads loses what the QKV phase gains.)
 int step_stage_lds(int type_layers, int n_layer, int D, int F, int H, int G, int hd, int n_wg);
-// true when the model's formats and head size have a compiled step kernel.
-bool step_supported(int type_layers, int type_out, int hd);
+// true when the model's formats, head size and query heads per kv head (n_rep) have a
+// compiled step kernel.
+bool step_supported(int type_layers, int type_out, int hd, int n_rep);
 hipError_t launch_step(const StepArgs& a, int type_layers, int type_out, int n_wg, hipStream_t st);
 
 // Launchers (k_*.hip).
