@@ -60,9 +60,9 @@ int step_stage_lds(int tl, int n_layer, int D, int F, int H, int G, int hd, int 
 
 namespace {
 
-template <int TL, int TO, int HDM>
+template <int TL, int TO, int HDM, int TA = TL>
 hipError_t launch_t(const StepArgs& a, int n_wg, hipStream_t st) {
-    const void* fn = (const void*)step_detail::k_step<TL, TO, HDM>;
+    const void* fn = (const void*)step_detail::k_step<TL, TO, HDM, TA>;
     const size_t lds = step_lds_bytes(a.n_layer, a.D, a.F, a.H, a.G, a.hd, n_wg, a.stage_lds);
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
@@ -77,9 +77,13 @@ hipError_t launch_t(const StepArgs& a, int n_wg, hipStream_t st) {
 
 }  // namespace
 
+int step_alt_type(int tl) { return tl == TF_HIP_TYPE_Q4_0 ? TF_HIP_TYPE_Q4_1 : tl; }
+
 bool step_supported(int tl, int to, int hd, int n_rep) {
     if (hd > 128 || n_rep > step_detail::kMaxRep) return false;
-    return (tl == TF_HIP_TYPE_Q8_0 && to == TF_HIP_TYPE_Q8_0) || (tl == TF_HIP_TYPE_F32 && to == TF_HIP_TYPE_F32 && hd <= 64);
+    return (tl == TF_HIP_TYPE_Q8_0 && to == TF_HIP_TYPE_Q8_0) ||
+           (tl == TF_HIP_TYPE_F32 && to == TF_HIP_TYPE_F32 && hd <= 64) ||
+           (tl == TF_HIP_TYPE_Q4_0 && to == TF_HIP_TYPE_Q6_K && hd <= 64);
 }
 
 hipError_t launch_step(const StepArgs& a, int tl, int to, int n_wg, hipStream_t st) {
@@ -88,6 +92,8 @@ hipError_t launch_step(const StepArgs& a, int tl, int to, int n_wg, hipStream_t 
                           : launch_t<TF_HIP_TYPE_Q8_0, TF_HIP_TYPE_Q8_0, 128>(a, n_wg, st);
     if (tl == TF_HIP_TYPE_F32 && to == TF_HIP_TYPE_F32 && a.hd <= 64)
         return launch_t<TF_HIP_TYPE_F32, TF_HIP_TYPE_F32, 64>(a, n_wg, st);
+    if (tl == TF_HIP_TYPE_Q4_0 && to == TF_HIP_TYPE_Q6_K && a.hd <= 64)
+        return launch_t<TF_HIP_TYPE_Q4_0, TF_HIP_TYPE_Q6_K, 64, TF_HIP_TYPE_Q4_1>(a, n_wg, st);
     return hipErrorInvalidValue;
 }
 

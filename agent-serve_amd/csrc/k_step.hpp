@@ -622,9 +622,16 @@ struct StepConst {
     int XA, XB, QKV, ATT, HH, DONE, BEST, PART;
 };
 
-template <int TL, int TO, int HDM>
+// TL: the layer matrices' format; TA: a second format wo and ffn_down may have, layer by
+// layer (the runtime type picks the instantiation); TO: the lm_head's (and embedding's).
+template <int TL, int TO, int HDM, int TA>
 __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
     using FE = Fmt<TO>;  // the embedding table has the lm_head's format (checked by the host)
+    constexpr bool kSums = Fmt<TL>::kNeedSums || Fmt<TA>::kNeedSums;  // inputs of wo and ffn_down
+    // lane steps per tile of the d_model-long rows (QKV, wo, gate/up, lm_head): one for the
+    // 32-element formats, whose 2048-element rows are 64 steps (a second would be masked
+    // out on every lane); ffn_down's n_ff-long rows keep two
+    constexpr int UL = Fmt<TL>::E >= 32 ? 1 : 2, UA = Fmt<TA>::E >= 32 ? 1 : 2, UO = Fmt<TO>::E >= 32 ? 1 : 2;
     constexpr int NWR = 8;  // norm weights per thread: d_model <= 4096
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ __align__(16) unsigned char sc_raw[sizeof(StepConst)];  // StepConst is not trivially constructible
@@ -814,7 +821,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     }
                     put(X(sc.QKV) + par * sc.G * HB + idx, bias(si) ? v + extra : v, E(t, l, 1));
                 };
-                gemv_phase<TL, 1, GEMV_STORE, 2>(3, groups, seg, bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
+                gemv_phase<TL, 1, GEMV_STORE, UL>(3, groups, seg, bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
                                                  prep, epi);
             }
             // ---- 2: attention (kv head g on workgroup attn_wg0 + g), then 4: gate/up
@@ -845,13 +852,17 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     auto seg = [&](int, int) -> const DevMat& { return ly.wo; };
                     auto prep = [&]() {
                         gather<kGD, 1>(X(sc.ATT) + par * Hd, Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl);
-                        stage(xs, Hd, false, wo_wr, 0.0f, xs, x16, Fmt<TL>::kNeedSums, red);
+                        stage(xs, Hd, false, wo_wr, 0.0f, xs, x16, kSums, red);
                     };
                     auto epi = [&](int, int row, float v, float, float) {
                         put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
                     };
-                    gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, Hd, wg * kNW + wave, nw, xs, x16, prep,
-                                                     epi);
+                    if (TA != TL && ly.wo.type == TA)
+                        gemv_phase<TA, 1, GEMV_RESID, UA>(1, groups, seg, no_bias, Hd, wg * kNW + wave, nw, xs, x16,
+                                                         prep, epi);
+                    else
+                        gemv_phase<TL, 1, GEMV_RESID, UL>(1, groups, seg, no_bias, Hd, wg * kNW + wave, nw, xs, x16,
+                                                         prep, epi);
                 };
                 // ---- 2 (caches longer than 512 positions): kv head g's positions split over
                 // A workgroups, then each (query head, slice of hd / parts outputs) merged
@@ -917,7 +928,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         issue_down(ly);
                         gu_input();
                     };
-                    gemv_phase<TL, 2, GEMV_SILU, 2>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                    gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, down_then_input, gu_epi);
                 } else if (!sc.A && wg >= sc.attn_wg0) {
                     const int g = wg - sc.attn_wg0;
@@ -936,7 +947,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         issue_down(ly);
                         gu_input();
                     };
-                    gemv_phase<TL, 2, GEMV_SILU, 2>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                    gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, down_then_input, gu_epi);
                 } else {
                     auto wo_then_input = [&]() {
@@ -945,7 +956,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         __syncthreads();  // every wave's wo rows are read out of xs before the input is staged
                         gu_input();
                     };
-                    gemv_phase<TL, 2, GEMV_SILU, 2>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                    gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, wo_then_input, gu_epi);
                 }
             }
@@ -957,7 +968,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 auto seg = [&](int, int) -> const DevMat& { return ly.wd; };
                 auto prep = [&]() {
                     gather<kGF, 1>(X(sc.HH) + par * F, F, E(t, l, 4), xs, nullptr, 0, 0, sc.a.ctl);
-                    stage(xs, F, false, wr, 0.0f, xs, x16, Fmt<TL>::kNeedSums, red);
+                    stage(xs, F, false, wr, 0.0f, xs, x16, kSums, red);
                 };
                 auto epi = [&](int, int row, float v, float, float) {
                     const float nv = xr[row] + v;
@@ -982,9 +993,14 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         }
                     }
                 }
-                if (!staged)
-                    gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, F, wg * kNW + wave, sc.nwg * kNW, xs,
-                                                     x16, prep, epi);
+                if (!staged) {
+                    if (TA != TL && ly.wd.type == TA)
+                        gemv_phase<TA, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, F, wg * kNW + wave, sc.nwg * kNW,
+                                                         xs, x16, prep, epi);
+                    else
+                        gemv_phase<TL, 1, GEMV_RESID, 2>(1, groups, seg, no_bias, F, wg * kNW + wave, sc.nwg * kNW,
+                                                         xs, x16, prep, epi);
+                }
                 __syncthreads();
                 if (tid == 0) put(X(sc.DONE) + par * sc.nwg + wg, 0.0f, E(t, l, 5));
             }
@@ -1010,7 +1026,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 const u64 k = argmax_key(v, row);
                 best = k > best ? k : best;
             };
-            gemv_phase<TO, 2, GEMV_LOGITS, 2>(1, groups, seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
+            gemv_phase<TO, 2, GEMV_LOGITS, UO>(1, groups, seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
                                               prep, epi);
             best = wave_max_u64(best);
             if (lane == 0) wbest[wave] = best;

@@ -421,8 +421,9 @@ int ensure_graph(tf_hip_ctx* c) {
 }
 
 // Decides once, after every tensor is uploaded, whether the persistent step kernel runs
-// this model: one format for all layer matrices, the embedding in the lm_head's format, a
-// compiled (format, head size) combination, cooperative launch, and inputs within the
+// this model: one format for all layer matrices (wo and ffn_down may also have the
+// kernel's second format, step_alt_type: Q4_1 beside Q4_0), the embedding in the lm_head's
+// format, a compiled (format, head size) combination, cooperative launch, and inputs within the
 // kernel's per-thread capacities. Caches longer than 512 positions split each layer's
 // attention over workgroups (step_split, step_split_all). Returns 1 (step kernel), 0
 // (graph) or < 0.
@@ -436,9 +437,13 @@ int ensure_step(tf_hip_ctx* c) {
     const int tl = mat(c, TF_HIP_SLOT_LAYER(0, TF_HIP_LAYER_Q)).type;
     const int kinds[7] = {TF_HIP_LAYER_Q,    TF_HIP_LAYER_K,  TF_HIP_LAYER_V,   TF_HIP_LAYER_O,
                           TF_HIP_LAYER_GATE, TF_HIP_LAYER_UP, TF_HIP_LAYER_DOWN};
+    const int ta = step_alt_type(tl);  // wo and ffn_down may also have this format
     for (int l = 0; l < p.n_layer; ++l)
-        for (int k : kinds)
-            if (mat(c, TF_HIP_SLOT_LAYER(l, k)).type != tl) return 0;
+        for (int k : kinds) {
+            const int t = mat(c, TF_HIP_SLOT_LAYER(l, k)).type;
+            const bool alt_ok = k == TF_HIP_LAYER_O || k == TF_HIP_LAYER_DOWN;
+            if (t != tl && !(alt_ok && t == ta)) return 0;
+        }
     const DevMat& out = output_mat(c);
     if (mat(c, TF_HIP_SLOT_TOKEN_EMBD).type != out.type ||
         !step_supported(tl, out.type, p.head_dim, p.n_head / p.n_kv_head))

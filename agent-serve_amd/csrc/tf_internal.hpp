@@ -223,6 +223,9 @@ int step_stage_lds(int type_layers, int n_layer, int D, int F, int H, int G, int
 // true when the model's formats, head size and query heads per kv head (n_rep) have a
 // compiled step kernel.
 bool step_supported(int type_layers, int type_out, int hd, int n_rep);
+// The second format the step kernel for layer format tl takes for wo and ffn_down (tl when
+// there is none).
+int step_alt_type(int tl);
 hipError_t launch_step(const StepArgs& a, int type_layers, int type_out, int n_wg, hipStream_t st);
 
 // Launchers (k_*.hip).

@@ -111,9 +111,10 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
 
 /* Decode path of prefill / decode / generate. TF_HIP_PATH_STEP (the default): one
  * persistent cooperative kernel per call runs every token of the call, for models whose
- * layer matrices share one format the kernel is compiled for (others use the graph path;
- * caches longer than 512 positions split each layer's attention over workgroups).
- * TF_HIP_PATH_GRAPH: one captured graph of per-layer kernels replayed per token. Both compute the same function; neither has a
+ * layer matrices share one format the kernel is compiled for (Q8_0, F32, or Q4_0 with
+ * Q4_1 wo / ffn_down allowed; others use the graph path; caches longer than 512 positions
+ * split each layer's attention over workgroups). TF_HIP_PATH_GRAPH: one captured graph of
+ * per-layer kernels replayed per token. Both compute the same function; neither has a
  * counterpart in the reference (a backend choice below Model::decode, model.cpp:197-208).
  * tf_hip_get_decode_path returns the path the next call will take (needs every tensor
  * uploaded). */
