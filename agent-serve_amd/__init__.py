@@ -57,6 +57,7 @@ def hip_lib() -> C.CDLL:
         "tf_hip_reset": (C.c_int, [vp]),
         "tf_hip_set_decode_path": (C.c_int, [vp, C.c_int32]),
         "tf_hip_get_decode_path": (C.c_int, [vp]),
+        "tf_hip_set_split_all_from": (C.c_int, [vp, C.c_int32]),
         "tf_hip_set_prefill_path": (C.c_int, [vp, C.c_int32]),
         "tf_hip_get_prefill_path": (C.c_int, [vp]),
         "tf_hip_get_pos": (C.c_int, [vp]),
@@ -247,6 +248,13 @@ class HipModel:
         rc = H.tf_hip_set_decode_path(self._L.tfh_ctx(self._h), int(path))
         if rc != 0:
             raise RuntimeError(f"tf_hip_set_decode_path({path}) failed: {rc}")
+
+    def set_split_all_from(self, span: int):
+        """Step kernel, caches longer than 512 positions: spans of more than `span` positions
+        split attention over every workgroup (span < 0: the model-derived default)."""
+        rc = hip_lib().tf_hip_set_split_all_from(self._L.tfh_ctx(self._h), int(span))
+        if rc != 0:
+            raise RuntimeError(f"tf_hip_set_split_all_from({span}) failed: {rc}")
 
     def decode_path(self) -> int:
         H = hip_lib()

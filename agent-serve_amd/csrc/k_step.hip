@@ -26,6 +26,16 @@ int step_split(int D, int F, int H, int G, int hd, int n_wg) {
     return A;
 }
 
+int step_split_all_from(int H, int G, int hd, int split) {
+    // Every workgroup splitting gives up the trailing layout's overlap of attention with the
+    // FFN's weight loads; it pays once a trailing split's share of the scores and P.V,
+    // span / split * n_rep * hd, passes about 25,600 (measured on MI355X: the crossover is
+    // near 1,500 positions for the Llama-3.2-1B shape, 16 splits of 4 heads x 64, and near
+    // 1,750 for the Qwen2.5-1.5B shape, 48 splits of 6 heads x 128; both give 1,600 here)
+    const int64_t w = (int64_t)(H / G) * hd;
+    return split > 0 ? (int)((25600LL * split + w - 1) / w) : 0;
+}
+
 int step_split_all(int D, int F, int H, int G, int hd, int n_wg) {
     // one split of every kv head per workgroup, as far as the merge's gather (3 words per
     // thread) and the LDS region hold A (sz + 2) words

@@ -749,7 +749,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             const int par = l & 1;
             // split attention layout of this token (caches longer than 512 positions), see phase 2
             const int span = sc.pos0 + t + 1 - sc.a.att_start;
-            const bool all = sc.A_all && span > 2 * kTile * sc.A;
+            const bool all = sc.A_all && span > sc.a.split_all_from;
             // ---- 1: QKV (attn_norm fused)
             {
                 const int D = sc.D;
@@ -869,8 +869,8 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 // from the A partials by one workgroup. Two layouts, chosen per token from
                 // the span's length (the same on every workgroup):
                 //   trailing: the G * A workgroups from attn_wg0 on split and merge while the
-                //     others start wo's and ffn_down's loads; best while a split is at most
-                //     two tiles;
+                //     others start the FFN's and wo's loads; best while a split's share of the
+                //     scores and P.V is small (spans up to split_all_from);
                 //   all: workgroups 0.. split (A_all per kv head) and merge, then every
                 //     workgroup runs wo; more splits, shorter ones, for long spans.
                 // The partials carry epoch slot 6 of the layer (unused by the other phases;

@@ -66,6 +66,7 @@ struct tf_hip_ctx {
     int step_state = -1;              // -1 undecided, 0 graph path, 1 step kernel ready
     int step_tl = -1, step_to = -1, n_wg = 0;
     int step_split = 0, step_split_all = 0;  // the step kernel's attention splits (step_split*)
+    int split_all_from = -1;                  // tf_hip_set_split_all_from (< 0: step_split_all_from)
     StepLayer* d_layers = nullptr;
     unsigned long long* ex = nullptr;
     uint32_t epoch = 0;               // exchange epochs consumed (mirrors ctl->epoch)
@@ -526,6 +527,8 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
     a.stage_lds = step_stage_lds(c->step_tl, p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, c->n_wg);
     a.split = c->step_split;
     a.split_all = c->step_split_all;
+    a.split_all_from = c->split_all_from >= 0 ? c->split_all_from
+                                              : step_split_all_from(p.n_head, p.n_kv_head, p.head_dim, c->step_split);
     const hipError_t e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);
     if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("step kernel launch: ") + hipGetErrorString(e));
     c->epoch += (uint32_t)(n * (6 * p.n_layer + 8));
@@ -990,6 +993,12 @@ int tf_hip_set_decode_path(tf_hip_ctx* c, int32_t path) {
     if (!c || (path != TF_HIP_PATH_GRAPH && path != TF_HIP_PATH_STEP)) return TF_HIP_EINVAL;
     c->path_opt = path;
     if (path == TF_HIP_PATH_STEP && c->step_state == 0) c->step_state = -1;  // decide again
+    return 0;
+}
+
+int tf_hip_set_split_all_from(tf_hip_ctx* c, int32_t span) {
+    if (!c) return TF_HIP_EINVAL;
+    c->split_all_from = span < 0 ? -1 : span;
     return 0;
 }
 

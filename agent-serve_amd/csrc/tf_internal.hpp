@@ -146,6 +146,7 @@ struct StepArgs {
     int stage_lds;             // bit 0: ffn_down rows staged in LDS (step_stage_lds)
     int split;                 // > 0: split attention on the trailing workgroups, splits per kv head (step_split)
     int split_all;             // > 0: splits per kv head when every workgroup splits (step_split_all)
+    int split_all_from;        // spans longer than this use split_all (step_split_all_from)
 };
 
 // ---------------------------------------------------------------- prefill on the matrix cores
@@ -214,6 +215,8 @@ size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg, int spl
 // workgroup (for long spans).
 int step_split(int D, int F, int H, int G, int hd, int n_wg);
 int step_split_all(int D, int F, int H, int G, int hd, int n_wg);
+// The span (cache positions attended) past which every workgroup splits instead.
+int step_split_all_from(int H, int G, int hd, int split);
 size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg, int stage_lds);
 // Which weight rows the step kernel stages in LDS ahead of their phase (bits of
 // StepArgs::stage_lds): the ffn_down rows (bit 0) for Q8_0 layers with at most one row per

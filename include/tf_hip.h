@@ -123,6 +123,13 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
 int tf_hip_set_decode_path(tf_hip_ctx* ctx, int32_t path);
 int tf_hip_get_decode_path(tf_hip_ctx* ctx);
 
+/* Tuning knob of the step kernel's split attention (caches longer than 512 positions; no
+ * counterpart in the reference): spans of more than `span` attended positions split over
+ * every workgroup, shorter ones over the trailing workgroups only. span < 0 restores the
+ * model-derived default. Results are the same function either way; used by the tests to
+ * place the switch inside a short decode. */
+int tf_hip_set_split_all_from(tf_hip_ctx* ctx, int32_t span);
+
 /* Prefill path (no counterpart in the reference, whose layer_prefill is the one
  * path, model.cpp:144-195): TF_HIP_PREFILL_MFMA runs a prompt of two or more tokens
  * through the matrix-core GEMMs and the causal chunk attention when every layer

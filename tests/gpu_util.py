@@ -29,11 +29,12 @@ def oracle_matmul(t: int, rows: np.ndarray, k: int, x: np.ndarray) -> np.ndarray
     return y
 
 
-def model_parity(pkg, path, prompt, n, max_seq, layout, tol=1e-3, taps=True, decode_path=None, prefill_path=None):
+def model_parity(pkg, path, prompt, n, max_seq, layout, tol=1e-3, taps=True, decode_path=None, prefill_path=None,
+                 setup=None):
     """Decode the oracle's greedy stream on both sides, comparing logits, argmax and
     per-layer activations at every step; then the device greedy loop from a reset.
     decode_path: HipModel.PATH_GRAPH / PATH_STEP; prefill_path: HipModel.PREFILL_TOKENS /
-    PREFILL_MFMA; None for the defaults.
+    PREFILL_MFMA; None for the defaults. setup(hip): called once on the model before use.
     Returns (oracle ids, max logits rel err, max tap rel err, min top-2 margin)."""
     orc = OracleModel(path, max_seq=max_seq, kv_layout=layout, n_threads=n_threads())
     hip = pkg.HipModel(path, max_seq=max_seq, kv_layout=layout)
@@ -41,6 +42,8 @@ def model_parity(pkg, path, prompt, n, max_seq, layout, tol=1e-3, taps=True, dec
         hip.set_decode_path(decode_path)
     if prefill_path is not None:
         hip.set_prefill_path(prefill_path)
+    if setup is not None:
+        setup(hip)
     try:
         lo = orc.prefill(prompt)
         lh, am = hip.prefill(prompt)

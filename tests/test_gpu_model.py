@@ -58,17 +58,20 @@ def test_long_cache_split_attention(pkg, gguf, preset, layout, path):
     print(f"{preset} layout {layout} path {path}: logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
 
 
-# (preset, prompt tokens, cache positions): the step kernel's splits move from its trailing
-# workgroups to every workgroup once the span passes 64 positions per trailing split
-# (tiny_f32: 16 splits per kv head, so past 1024; tiny_q8: 64, past 4096). The prompts end
-# a few positions short of that, so the per-token decodes and the one-launch greedy loop
-# both cross it.
+# (preset, prompt tokens, cache positions, switch span): the step kernel's splits move from
+# its trailing workgroups to every workgroup once the span passes the switch
+# (tf_hip_set_split_all_from). The prompts end a few positions short of it, so the
+# per-token decodes and the one-launch greedy loop both cross it; with 1024 and 4096 the
+# trailing splits hold 64 positions each at the switch (16 and 64 splits per kv head).
 @pytest.mark.parametrize("layout", [0, 1])
-@pytest.mark.parametrize("preset,n_prompt,max_seq", [("tiny_f32", 1018, 2048), ("tiny_q8", 4090, 4200)])
-def test_long_cache_split_layout_switch(pkg, gguf, preset, n_prompt, max_seq, layout):
+@pytest.mark.parametrize("preset,n_prompt,max_seq,switch", [("tiny_f32", 1018, 2048, 1024),
+                                                            ("tiny_q8", 4090, 4200, 4096),
+                                                            ("tiny_qwen", 700, 1024, 705)])
+def test_long_cache_split_layout_switch(pkg, gguf, preset, n_prompt, max_seq, switch, layout):
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"] + 11, n_prompt, info["n_vocab"])
-    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, max_seq, layout, decode_path=STEP)
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, max_seq, layout, decode_path=STEP,
+                                                 setup=lambda hip: hip.set_split_all_from(switch))
     print(f"{preset} {n_prompt} layout {layout}: logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
 
 
