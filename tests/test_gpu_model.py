@@ -46,7 +46,7 @@ def test_decode_path_selection(pkg, gguf, preset, want):
 
 @pytest.mark.parametrize("path", [GRAPH, STEP], ids=["graph", "step"])
 @pytest.mark.parametrize("layout", [0, 1])
-@pytest.mark.parametrize("preset", ["tiny_q8", "tiny_f32", "tiny_qwen", "small_q8"])
+@pytest.mark.parametrize("preset", ["tiny_q8", "tiny_f32", "tiny_qwen", "small_q8", "tiny_mixq4"])
 def test_long_cache_split_attention(pkg, gguf, preset, layout, path):
     """A 600-token prompt in a 1024-position cache: the step kernel's attention splits the
     positions over its trailing workgroups and merges the splits there, the graph path's
