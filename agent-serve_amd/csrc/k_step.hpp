@@ -847,6 +847,10 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 // ---- 3: wo + residual, rows dealt over nw waves from wave 0
                 auto wo_phase = [&](int nw) {
                     const int Hd = sc.Hd;
+                    // rows dealt round the waves starting where the QKV rows ended, so that a
+                    // wave with a QKV row more than the rest does not also get one more wo row
+                    const int rot = (int)((ly.wq.N + ly.wk.N + ly.wv.N) % (sc.nwg * kNW)) % nw;
+                    const int wid = (wg * kNW + wave + nw - rot) % nw;
                     float wo_wr[1];
                     const int groups[3] = {(int)ly.wo.N, 0, 0};
                     auto seg = [&](int, int) -> const DevMat& { return ly.wo; };
@@ -858,11 +862,9 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
                     };
                     if (TA != TL && ly.wo.type == TA)
-                        gemv_phase<TA, 1, GEMV_RESID, UA>(1, groups, seg, no_bias, Hd, wg * kNW + wave, nw, xs, x16,
-                                                         prep, epi);
+                        gemv_phase<TA, 1, GEMV_RESID, UA>(1, groups, seg, no_bias, Hd, wid, nw, xs, x16, prep, epi);
                     else
-                        gemv_phase<TL, 1, GEMV_RESID, UL>(1, groups, seg, no_bias, Hd, wg * kNW + wave, nw, xs, x16,
-                                                         prep, epi);
+                        gemv_phase<TL, 1, GEMV_RESID, UL>(1, groups, seg, no_bias, Hd, wid, nw, xs, x16, prep, epi);
                 };
                 // ---- 2 (caches longer than 512 positions): kv head g's positions split over
                 // A workgroups, then each (query head, slice of hd / parts outputs) merged
