@@ -45,7 +45,7 @@ HBM_PEAK_GBS = 8000.0
 COPY_CALIB_BYTES = 1 << 30
 TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_llama1b_q8_0_traffic.txt"
 STEP_TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_llama1b_q8_0_step_kernel_traffic.txt"
-PUBLISHED_CPU_TOK_S = 10.74  # reference --stage v2, Llama-3.2-1B Q8_0, Ryzen 5 4600H
+PUBLISHED_CPU_TOK_S = 10.74  # reference --stage v2, Llama-3.2-1B Q8_0, Ryzen 5 4600H 6c/12t (its published figure)
 # prefill leg: a 512-token prompt of the same model, then 16 decode tokens
 PF_PROMPT_TOKENS = 512
 PF_DECODE_TOKENS = 16
@@ -275,7 +275,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs the token loop on one GPU; --gpus {args.gpus} is not supported "
+        print(f"bench.py: the token loop runs on one GPU; --gpus {args.gpus} is not supported "
               "(batch-1 decode of a 1.3 GB model fits one MI355X; multi-GPU sharding is design-only)",
               file=sys.stderr)
         return 2

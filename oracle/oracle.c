@@ -1,8 +1,8 @@
 /*
  * oracle.c - CPU restatement of tinferno's --stage v2 token loop.
  *
- * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker for the HIP backend and
- * the CPU baseline's restated form; never linked into the product.
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the oracle the HIP backend is checked
+ * against, and the CPU baseline's restated form; never linked into the product.
  *
  * Built with -O3 -mavx2 -mfma -mf16c -ffp-contract=off: the only fused
  * multiply-adds are the explicit fmaf() calls, placed where g++ -O3 -mfma fuses

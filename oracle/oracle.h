@@ -1,7 +1,7 @@
 /*
  * oracle.h - CPU restatement of tinferno's --stage v2 token loop.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker that the HIP backend is
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle that the HIP backend is
  * compared against. Only tests/, __graft_entry__.smoke() and bench.py's CPU
  * baseline leg load it; the product (libtf_hip.so, libtinferno.so, the CLI)
  * never links, loads or calls it.

@@ -1,4 +1,4 @@
-"""Pins the oracle (oracle/oracle.c) before it is trusted as the checker.
+"""Pins the oracle (oracle/oracle.c) before the HIP backend is compared against it.
 
 Three independent pins:
   * bit-for-bit equality with the reference compiled from its own sources (oracle/_ref),
