@@ -344,17 +344,16 @@ __device__ __forceinline__ int64_t kv_at(int layout, int G, int max_seq, int hd,
 // which wait for every load in flight). The
 // loads past the span re-read row p1 - 1 instead of being skipped: no load sits behind a
 // branch, and every wait for a tile is a fixed count of the loads issued after it.
-//   kPart false (attn_head): [p0, p1) = [start, pos]; out = the normalised heads, [n_rep][hd].
-//     The same workgroup runs head g for every token of a launch, so the rows it stores are
-//     the ones it later reads on this CU.
-//   kPart true (attn_part, caches longer than 512 positions): one split of [start, pos]
-//     (flash-decoding, split over workgroups). out[r * (hd + 2) ...] = the unnormalised o
-//     (P.V with P = e^(s - m)), then m and l (the running max and sum of the online
-//     softmax); the combine phase merges the splits. The split holding pos stores the new
-//     row through at agent scope (later tokens of the launch read it from other XCDs) and
-//     waits for the stores before returning, i.e. before its next puts. The cache is read at
-//     agent scope. An empty split leaves m = -inf, l = 0, o = 0 and does not wait for the
-//     head block.
+//   kPart false (attn_head, spans up to StepArgs::split_from): [p0, p1) = [start, pos]; out =
+//     the normalised heads, [n_rep][hd]. The same workgroup runs head g for every such
+//     token of a launch, so the rows it reads are its own or written before the launch.
+//   kPart true (attn_part, longer spans): one split of [start, pos] (flash-decoding, split
+//     over workgroups). out[r * (hd + 2) ...] = the unnormalised o (P.V with P = e^(s - m)),
+//     then m and l (the running max and sum of the online softmax); the combine phase
+//     merges the splits. The cache is read at agent scope. An empty split leaves m = -inf,
+//     l = 0, o = 0 and does not wait for the head block.
+//   Both store the new row at agent scope (a later, split token of the launch reads it from
+//   other XCDs) and wait for the stores before returning, i.e. before their next puts.
 template <int HDM, bool kPart, int NB, class Fetch>
 __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly, int g, int pos, int p0, int p1,
                                           float* qkv, float* sm, float* out, Fetch&& fetch) {
@@ -441,14 +440,11 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
     const bool stores_row = pos >= p0 && pos < p1;
     if (stores_row) {
         const int64_t o = kv_at(a.layout, a.G, a.max_seq, hd, g, pos);
+        // agent scope in both layouts: a launch whose later tokens split reads this row from
+        // workgroups on other XCDs
         for (int j = tid; j < hd; j += kT) {
-            if constexpr (kPart) {
-                __hip_atomic_store(gptr(ly.kc + o + j), kn[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(gptr(ly.vc + o + j), vn[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-                *gptr(ly.kc + o + j) = kn[j];
-                *gptr(ly.vc + o + j) = vn[j];
-            }
+            __hip_atomic_store(gptr(ly.kc + o + j), kn[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(gptr(ly.vc + o + j), vn[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     const float scale = 1.0f / sqrtf((float)hd);
@@ -544,7 +540,6 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
             out[tid * ho + hd] = st[3 * tid];
             out[tid * ho + hd + 1] = st[3 * tid + 1];
         }
-        if (stores_row) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else {
 #pragma unroll
         for (int k = 0; k < kPairs; ++k) {
@@ -552,6 +547,8 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
             if (pi < n_rep * hd) out[pi] = o_acc[k] / st[3 * (pi / hd) + 1];
         }
     }
+    // the row's stores are done before this workgroup's next puts
+    if (stores_row) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 }
 
@@ -658,7 +655,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         c.nwg = gridDim.x;
         c.P = 6 * c.L + 8;               // epochs per token
         c.A = args.split;                // > 0: splits per kv head of the long-cache attention (trailing layout)
-        c.attn_wg0 = c.nwg - c.G * (c.A ? c.A : 1);  // workgroups attn_wg0.. run the attention
+        c.attn_wg0 = c.nwg - c.G * (c.A ? c.A : 1);  // workgroups attn_wg0.. run a split token's attention
         c.parts = c.A ? c.A / c.n_rep : 1;  // each attention workgroup then merges hd / parts outputs of one head
         c.A_all = args.split_all;        // > 0: splits per kv head when every workgroup splits
         c.parts_all = split_all_parts(args.H, c.hd, c.nwg);
@@ -750,6 +747,9 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             // split attention layout of this token (caches longer than 512 positions), see phase 2
             const int span = sc.pos0 + t + 1 - sc.a.att_start;
             const bool all = sc.A_all && span > sc.a.split_all_from;
+            // short spans attend on one workgroup per kv head (attn_head), longer ones split
+            const bool split = sc.A && (all || span > sc.a.split_from);
+            const int attn_wg0 = split ? sc.attn_wg0 : sc.nwg - sc.G;
             // ---- 1: QKV (attn_norm fused)
             {
                 const int D = sc.D;
@@ -877,10 +877,10 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 //     workgroup runs wo; more splits, shorter ones, for long spans.
                 // The partials carry epoch slot 6 of the layer (unused by the other phases;
                 // the argmax words use it only past the last layer; never 0).
-                if (sc.A && (all || wg >= sc.attn_wg0)) {
+                if (split && (all || wg >= attn_wg0)) {
                     const int A = all ? sc.A_all : sc.A, parts = all ? sc.parts_all : sc.parts;
                     const int G = sc.G, HB = sc.HB, n_rep = sc.n_rep, hd = sc.hd, ho = hd + 2;
-                    const int aw = all ? wg : wg - sc.attn_wg0;
+                    const int aw = all ? wg : wg - attn_wg0;
                     u64* pb = X(sc.PART) + par * sc.PW;
                     float* qkv = (float*)(smem + sc.o_qkv);
                     float* part = (float*)(smem + sc.o_att);
@@ -925,15 +925,15 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         }
                     }
                 }
-                if (sc.A && !all && wg >= sc.attn_wg0) {
+                if (split && !all && wg >= attn_wg0) {
                     auto down_then_input = [&]() {
                         issue_down(ly);
                         gu_input();
                     };
                     gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, down_then_input, gu_epi);
-                } else if (!sc.A && wg >= sc.attn_wg0) {
-                    const int g = wg - sc.attn_wg0;
+                } else if (!split && wg >= attn_wg0) {
+                    const int g = wg - attn_wg0;
                     const int HB = sc.HB;
                     float* qkv = (float*)(smem + sc.o_qkv);
                     float* att_out = (float*)(smem + sc.o_att);
@@ -954,7 +954,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 } else {
                     auto wo_then_input = [&]() {
                         issue_down(ly);
-                        wo_phase((all ? sc.nwg : sc.attn_wg0) * kNW);
+                        wo_phase((all ? sc.nwg : attn_wg0) * kNW);
                         __syncthreads();  // every wave's wo rows are read out of xs before the input is staged
                         gu_input();
                     };

@@ -8,6 +8,7 @@
 // does) and the greedy loop (token = previous argmax, no host round trip).
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -456,8 +457,9 @@ int ensure_step(tf_hip_ctx* c) {
     if (n_wg < 2 * p.n_kv_head || p.n_embd + n_wg > 4096 || p.n_ff > 10240 || 2 * n_wg > 1024 ||
         (n_rep + 2) * p.head_dim > 4096 || p.n_head * p.head_dim > 4096)
         return 0;
-    // caches longer than 512 positions: attention split over workgroups
-    const int split = p.max_seq > 512 ? step_split(p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, n_wg) : 0;
+    // attention split over workgroups for tokens past StepArgs::split_from positions
+    // (required past 512: one workgroup per kv head attends at most that many)
+    const int split = step_split(p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, n_wg);
     if (p.max_seq > 512 && !split) return 0;
     std::vector<StepLayer> tab((size_t)p.n_layer);
     for (int l = 0; l < p.n_layer; ++l) {
@@ -527,6 +529,12 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
     a.stage_lds = step_stage_lds(c->step_tl, p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, c->n_wg);
     a.split = c->step_split;
     a.split_all = c->step_split_all;
+    // one workgroup per kv head attends two 32-position tiles faster than the split's extra
+    // merge hand-off; past that its tiles cost more (Llama-3.2-1B shape on MI355X: 0.533 vs
+    // 0.544 ms per token at spans 7-38, 1.015 vs 0.557 at spans 301-428)
+    const char* sf = std::getenv("TF_HIP_SPLIT_FROM");
+    a.split_from = sf ? std::atoi(sf) : 64;
+    if (a.split_from > 512) a.split_from = 512;
     a.split_all_from = c->split_all_from >= 0 ? c->split_all_from
                                               : step_split_all_from(p.n_head, p.n_kv_head, p.head_dim, c->step_split);
     const hipError_t e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);

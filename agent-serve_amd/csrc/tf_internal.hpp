@@ -147,6 +147,7 @@ struct StepArgs {
     int split;                 // > 0: split attention on the trailing workgroups, splits per kv head (step_split)
     int split_all;             // > 0: splits per kv head when every workgroup splits (step_split_all)
     int split_all_from;        // spans longer than this use split_all (step_split_all_from)
+    int split_from;            // spans (positions attended) up to this attend on one workgroup per kv head
 };
 
 // ---------------------------------------------------------------- prefill on the matrix cores

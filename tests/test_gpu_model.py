@@ -75,6 +75,19 @@ def test_long_cache_split_layout_switch(pkg, gguf, preset, n_prompt, max_seq, sw
     print(f"{preset} {n_prompt} layout {layout}: logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
 
 
+# Caches of at most 512 positions: tokens attending up to 64 positions run attention on one
+# workgroup per kv head, longer spans split it. Prompts of 60 tokens put the switch inside
+# the per-token decodes and inside the one-launch greedy loop, whose later, split tokens
+# read the rows the earlier ones stored from other workgroups.
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("preset", ["tiny_f32", "tiny_q8", "tiny_qwen"])
+def test_short_cache_split_switch(pkg, gguf, preset, layout):
+    info = pkg.synth_preset_info(preset)
+    prompt = pkg.synth_prompt(info["seed"] + 5, 60, info["n_vocab"])
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, 512, layout, decode_path=STEP)
+    print(f"{preset} layout {layout}: logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
+
+
 TOKENS, MFMA = 0, 1  # HipModel.PREFILL_TOKENS, HipModel.PREFILL_MFMA
 
 
