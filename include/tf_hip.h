@@ -112,8 +112,10 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
 /* Decode path of prefill / decode / generate. TF_HIP_PATH_STEP (the default): one
  * persistent cooperative kernel per call runs every token of the call, for models whose
  * layer matrices share one format the kernel is compiled for (Q8_0, F32, or Q4_0 with
- * Q4_1 wo / ffn_down allowed; others use the graph path; caches longer than 512 positions
- * split each layer's attention over workgroups). TF_HIP_PATH_GRAPH: one captured graph of
+ * Q4_1 wo / ffn_down allowed; others use the graph path; tokens attending more than 64
+ * positions split each layer's attention over workgroups, shorter spans run it on one
+ * workgroup per kv head; the environment variable TF_HIP_SPLIT_FROM moves that span, at
+ * most 512). TF_HIP_PATH_GRAPH: one captured graph of
  * per-layer kernels replayed per token. Both compute the same function; neither has a
  * counterpart in the reference (a backend choice below Model::decode, model.cpp:197-208).
  * tf_hip_get_decode_path returns the path the next call will take (needs every tensor
@@ -123,9 +125,9 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
 int tf_hip_set_decode_path(tf_hip_ctx* ctx, int32_t path);
 int tf_hip_get_decode_path(tf_hip_ctx* ctx);
 
-/* Tuning knob of the step kernel's split attention (caches longer than 512 positions; no
- * counterpart in the reference): spans of more than `span` attended positions split over
- * every workgroup, shorter ones over the trailing workgroups only. span < 0 restores the
+/* Tuning knob of the step kernel's split attention (no counterpart in the reference):
+ * spans of more than `span` attended positions split over every workgroup, shorter split
+ * ones over the trailing workgroups only. span < 0 restores the
  * model-derived default. Results are the same function either way; used by the tests to
  * place the switch inside a short decode. */
 int tf_hip_set_split_all_from(tf_hip_ctx* ctx, int32_t span);
