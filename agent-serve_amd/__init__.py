@@ -58,6 +58,9 @@ def hip_lib() -> C.CDLL:
         "tf_hip_set_decode_path": (C.c_int, [vp, C.c_int32]),
         "tf_hip_get_decode_path": (C.c_int, [vp]),
         "tf_hip_set_split_all_from": (C.c_int, [vp, C.c_int32]),
+        "tf_hip_set_split_from": (C.c_int, [vp, C.c_int32]),
+        "tf_hip_get_step_config": (C.c_int, [vp, _i32p, C.c_int32]),
+        "tf_hip_set_exchange_epoch": (C.c_int, [vp, C.c_uint32]),
         "tf_hip_set_prefill_path": (C.c_int, [vp, C.c_int32]),
         "tf_hip_get_prefill_path": (C.c_int, [vp]),
         "tf_hip_get_pos": (C.c_int, [vp]),
@@ -111,6 +114,8 @@ def host_lib() -> C.CDLL:
         "tfh_synth_preset_info": (C.c_int, [C.c_char_p, _i32p]),
         "tfh_synth_prompt": (C.c_int, [C.c_int64, C.c_int32, C.c_int32, _i32p]),
         "tfh_rope_tables": (C.c_int, [C.c_float, C.c_int32, C.c_int32, _f32p, _f32p]),
+        "tfh_file_decode_bytes": (C.c_double, [C.c_char_p, C.c_int32]),
+        "tfh_file_rope_tables": (C.c_int, [C.c_char_p, C.c_int32, _f32p, _f32p]),
         "tfh_quantize_row": (C.c_int, [C.c_int32, _f32p, C.c_int64, vp]),
         "tfh_gguf_summary": (C.c_int, [C.c_char_p, _u64p, C.c_char_p, C.c_int32]),
     }
@@ -177,6 +182,24 @@ def rope_tables(theta: float, n_rot: int, n_pos: int):
     c = np.zeros((n_pos, n_rot // 2), np.float32)
     s = np.zeros((n_pos, n_rot // 2), np.float32)
     if host_lib().tfh_rope_tables(theta, n_rot, n_pos, _f(c), _f(s)) != 0:
+        raise RuntimeError(host_lib().tfh_global_error().decode())
+    return c, s
+
+
+def file_decode_bytes(path: str, pos: int) -> float:
+    """Algorithmic bytes of one decode step at position pos of the GGUF at path (the
+    roofline's numerator, Model::decode_bytes), computed on the host."""
+    v = host_lib().tfh_file_decode_bytes(str(path).encode(), int(pos))
+    if v < 0:
+        raise RuntimeError(host_lib().tfh_global_error().decode())
+    return float(v)
+
+
+def file_rope_tables(path: str, n_pos: int, half_dim: int):
+    """The host RoPE cos/sin tables the Model uploads for the GGUF at path."""
+    c = np.zeros((n_pos, half_dim), np.float32)
+    s = np.zeros((n_pos, half_dim), np.float32)
+    if host_lib().tfh_file_rope_tables(str(path).encode(), n_pos, _f(c), _f(s)) != 0:
         raise RuntimeError(host_lib().tfh_global_error().decode())
     return c, s
 
@@ -255,6 +278,31 @@ class HipModel:
         rc = hip_lib().tf_hip_set_split_all_from(self._L.tfh_ctx(self._h), int(span))
         if rc != 0:
             raise RuntimeError(f"tf_hip_set_split_all_from({span}) failed: {rc}")
+
+    def set_split_from(self, span: int):
+        """Step kernel: spans of at most `span` positions attend on one workgroup per kv
+        head, longer ones split (span < 0: the default, 64; at most 512)."""
+        H = hip_lib()
+        rc = H.tf_hip_set_split_from(self._L.tfh_ctx(self._h), int(span))
+        if rc != 0:
+            raise RuntimeError(H.tf_hip_last_error(self._L.tfh_ctx(self._h)).decode())
+
+    def step_config(self) -> dict:
+        """The step kernel's attention configuration (raises when the step kernel does not
+        run this model)."""
+        H = hip_lib()
+        out = np.zeros(5, np.int32)
+        rc = H.tf_hip_get_step_config(self._L.tfh_ctx(self._h), _i(out), 5)
+        if rc != 0:
+            raise RuntimeError(H.tf_hip_last_error(self._L.tfh_ctx(self._h)).decode())
+        keys = ("n_wg", "split", "split_all", "split_from", "split_all_from")
+        return dict(zip(keys, (int(v) for v in out)))
+
+    def set_exchange_epoch(self, epoch: int):
+        """Test hook: the step kernel's exchange epoch counter."""
+        rc = hip_lib().tf_hip_set_exchange_epoch(self._L.tfh_ctx(self._h), int(epoch) & 0xFFFFFFFF)
+        if rc != 0:
+            raise RuntimeError(f"tf_hip_set_exchange_epoch failed: {rc}")
 
     def decode_path(self) -> int:
         H = hip_lib()

@@ -51,6 +51,11 @@ __device__ __forceinline__ float ub0(uint32_t w) { return (float)(w & 0xFFu); }
 __device__ __forceinline__ float ub1(uint32_t w) { return (float)((w >> 8) & 0xFFu); }
 __device__ __forceinline__ float ub2(uint32_t w) { return (float)((w >> 16) & 0xFFu); }
 __device__ __forceinline__ float ub3(uint32_t w) { return (float)(w >> 24); }
+// Signed byte n of a dword as float (one v_cvt_f32_i32 with an SDWA sign-extended byte).
+__device__ __forceinline__ float sb0(uint32_t w) { return (float)(int8_t)w; }
+__device__ __forceinline__ float sb1(uint32_t w) { return (float)(int8_t)(w >> 8); }
+__device__ __forceinline__ float sb2(uint32_t w) { return (float)(int8_t)(w >> 16); }
+__device__ __forceinline__ float sb3(uint32_t w) { return (float)((int32_t)w >> 24); }
 
 // DPP lane permutes within a row of 16 lanes (no LDS round trip).
 template <int CTRL>

@@ -5,10 +5,12 @@
 // load() fetches a step of one row; dot() returns its contribution to x . w with x
 // (and its 16-element partial sums x16) in LDS; dequant() writes the step's values.
 //
-// Offset-binary trick: quantised values are decoded as unsigned bytes u = q + c with
-// one v_cvt_f32_ubyte each, and sum_j x_j q_j = sum_j x_j u_j - c * sum_j x_j, where
-// the per-16 sums of x come from the prologue. dequant() produces d * (float)q
-// exactly as the reference does (quant.cpp:66-131: all those products are exact).
+// Q8_0 bytes stay signed: each converts with one v_cvt_f32_i32 (SDWA byte select with
+// sign extension), so the dot is sum_j x_j q_j directly and its rounding scales with
+// sum |x_j q_j|. The 4- and 6-bit formats decode unsigned codes u = q + c with one
+// v_cvt_f32_ubyte each, and sum_j x_j q_j = sum_j x_j u_j - c * sum_j x_j, where the
+// per-16 sums of x come from the prologue. dequant() produces d * (float)q exactly as
+// the reference does (quant.cpp:66-131: all those products are exact).
 #pragma once
 
 #include "dev_common.hpp"
@@ -30,7 +32,7 @@ struct Fmt;
 template <>
 struct Fmt<TF_HIP_TYPE_Q8_0> {
     static constexpr int E = 16;
-    static constexpr bool kNeedSums = true;
+    static constexpr bool kNeedSums = false;
     struct Raw {
         uint4 q;
         uint32_t d;
@@ -44,17 +46,19 @@ struct Fmt<TF_HIP_TYPE_Q8_0> {
         w.d = *gptr((const uint16_t*)(p.s + 2 * (s >> 1)));
         return w;
     }
-    __device__ static float dot(const Raw& w, const float* xs, const float* x16, int s) {
+    // sum_j x_j q_j of the step's 16 elements, then times d (dot_q8_0_f32 scales each
+    // block's sum by d, quant.cpp:266-321)
+    __device__ static float dot(const Raw& w, const float* xs, const float*, int s) {
         const float4* x4 = (const float4*)(xs + 16 * s);
-        float t = -128.0f * x16[s];
+        float t = 0.0f;
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float4 xv = x4[i];
-            t = fmaf(xv.x, ub0(q[i]), t);
-            t = fmaf(xv.y, ub1(q[i]), t);
-            t = fmaf(xv.z, ub2(q[i]), t);
-            t = fmaf(xv.w, ub3(q[i]), t);
+            t = fmaf(xv.x, sb0(q[i]), t);
+            t = fmaf(xv.y, sb1(q[i]), t);
+            t = fmaf(xv.z, sb2(q[i]), t);
+            t = fmaf(xv.w, sb3(q[i]), t);
         }
         return h2f(w.d) * t;
     }
@@ -62,10 +66,7 @@ struct Fmt<TF_HIP_TYPE_Q8_0> {
         const float d = h2f(w.d);
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int u = (int)((q[i >> 2] >> (8 * (i & 3))) & 0xFFu);
-            out[i] = d * (float)(u - 128);
-        }
+        for (int i = 0; i < 16; ++i) out[i] = d * (float)(int8_t)(q[i >> 2] >> (8 * (i & 3)));
     }
 };
 

@@ -94,8 +94,11 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const AttnArgs a) {
     // one memory round for everything the first tile needs
     const int nq = n_rep * d2;
     float qa[kQPairs], qb[kQPairs], ca[kQPairs], sa[kQPairs];
-    const float* cs = a.rope_cos + (int64_t)pos * d2;
-    const float* sn = a.rope_sin + (int64_t)pos * d2;
+    // without RoPE the angles are loaded but unused: row 0 of the table then, so that a
+    // stand-in table of d2 floats (the op-level entry points pass q) is never read past
+    const int64_t ro = a.rope ? (int64_t)pos * d2 : 0;
+    const float* cs = a.rope_cos + ro;
+    const float* sn = a.rope_sin + ro;
 #pragma unroll
     for (int k = 0; k < kQPairs; ++k) {
         int i = tid + k * kBlock;
@@ -108,10 +111,13 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const AttnArgs a) {
         sa[k] = sn[j];
     }
     const int jk = tid < d2 ? tid : d2 - 1;
-    const float* kh = a.knew + (int64_t)g * hd;
+    // the new row: knew / vnew, or (null) the cache's row at pos, already stored
+    const int64_t o_new = kv_index(a.layout, a.G, a.max_seq, hd, g, pos);
+    const float* kh = a.knew ? a.knew + (int64_t)g * hd : a.kc + o_new;
+    const float* vh = a.vnew ? a.vnew + (int64_t)g * hd : a.vc + o_new;
     const float k0 = kh[jk], k1 = kh[jk + d2], kc0 = cs[jk], ks0 = sn[jk];
     const int jv = tid < hd ? tid : hd - 1;
-    const float v0 = a.vnew[(int64_t)g * hd + jv];
+    const float v0 = vh[jv];
     float4 kr_a[kTileVec], vr_a[kTileVec], kr_b[kTileVec], vr_b[kTileVec];
     load_tile(p0, kr_a, vr_a);
 

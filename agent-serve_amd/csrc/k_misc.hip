@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kBlock) void k_repack(int type, const uint8_t* raw,
         if (type == TF_HIP_TYPE_Q8_0) {
             const uint8_t* src = raw + r * nb * 34 + b * 34;
             uint8_t* q = m.q + r * K + b * 32;
-            for (int j = 0; j < 32; ++j) q[j] = (uint8_t)(src[2 + j] ^ 0x80u);  // q + 128
+            for (int j = 0; j < 32; ++j) q[j] = src[2 + j];  // int8 q
             ((uint16_t*)m.s)[r * nb + b] = (uint16_t)(src[0] | (src[1] << 8));
         } else if (type == TF_HIP_TYPE_Q4_0) {
             const uint8_t* src = raw + r * nb * 18 + b * 18;

@@ -40,9 +40,11 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 //   activations: xa[row tile][block][hi, lo][lane][8]   (k_pf_split)
 //   weights:     wf[row tile][block][lane][8]            (k_pf_pack_q8, once per matrix)
 
-// Eight offset-binary bytes (q + 128) -> the fp16 values q: 0x64XX is the half 1024 + XX,
-// and 1024 + XX - 1152 = q exactly.
+// Eight int8 bytes q -> their fp16 values: with u = q + 128 (the byte with its top bit
+// flipped), 0x64UU is the half 1024 + u, and 1024 + u - 1152 = q exactly.
 __device__ __forceinline__ h8_t q8_to_h8(uint2 w) {
+    w.x ^= 0x80808080u;
+    w.y ^= 0x80808080u;
     const uint32_t p0 = (w.x & 0xFFu) | ((w.x & 0xFF00u) << 8) | 0x64006400u;
     const uint32_t p1 = ((w.x >> 16) & 0xFFu) | ((w.x >> 8) & 0xFF0000u) | 0x64006400u;
     const uint32_t p2 = (w.y & 0xFFu) | ((w.y & 0xFF00u) << 8) | 0x64006400u;

@@ -24,6 +24,13 @@ constexpr int kNumClasses = 7;  // embed, qkv, attention, wo, gate/up, down, lm_
 const char* const kClassNames[kNumClasses] = {"embed", "qkv_gemv", "attention", "wo_gemv",
                                               "gateup_gemv", "down_gemv", "lmhead_gemv"};
 
+// One workgroup per kv head attends two 32-position tiles faster than a split's extra merge
+// hand-off; past that its tiles cost more (Llama-3.2-1B shape on MI355X: 0.533 vs 0.544 ms
+// per token at spans 7-38, 1.015 vs 0.557 at spans 301-428). One workgroup per kv head
+// attends at most 512 positions.
+constexpr int kSplitFromDefault = 64;
+constexpr int kSplitFromMax = 512;
+
 struct Prof {
     std::vector<hipEvent_t> ev;  // pairs per launch
     std::vector<int> cls;
@@ -68,8 +75,10 @@ struct tf_hip_ctx {
     int step_tl = -1, step_to = -1, n_wg = 0;
     int step_split = 0, step_split_all = 0;  // the step kernel's attention splits (step_split*)
     int split_all_from = -1;                  // tf_hip_set_split_all_from (< 0: step_split_all_from)
+    int split_from = kSplitFromDefault;       // tf_hip_set_split_from: spans up to this attend unsplit
     StepLayer* d_layers = nullptr;
     unsigned long long* ex = nullptr;
+    size_t ex_words = 0;
     uint32_t epoch = 0;               // exchange epochs consumed (mirrors ctl->epoch)
     // prefill on the matrix cores (k_prefill.hip)
     int pf_opt = TF_HIP_PREFILL_MFMA;  // requested prefill path
@@ -490,6 +499,7 @@ int ensure_step(tf_hip_ctx* c) {
         return rc;
     HIPCHK(c, hipMemcpy(c->d_layers, tab.data(), tab.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
     HIPCHK(c, hipMemset(c->ex, 0, words * 8));  // epoch 0 is never used
+    c->ex_words = words;
     c->step_tl = tl;
     c->step_to = out.type;
     c->n_wg = n_wg;
@@ -529,17 +539,25 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
     a.stage_lds = step_stage_lds(c->step_tl, p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, c->n_wg);
     a.split = c->step_split;
     a.split_all = c->step_split_all;
-    // one workgroup per kv head attends two 32-position tiles faster than the split's extra
-    // merge hand-off; past that its tiles cost more (Llama-3.2-1B shape on MI355X: 0.533 vs
-    // 0.544 ms per token at spans 7-38, 1.015 vs 0.557 at spans 301-428)
-    const char* sf = std::getenv("TF_HIP_SPLIT_FROM");
-    a.split_from = sf ? std::atoi(sf) : 64;
-    if (a.split_from > 512) a.split_from = 512;
+    a.split_from = c->split_from;
     a.split_all_from = c->split_all_from >= 0 ? c->split_all_from
                                               : step_split_all_from(p.n_head, p.n_kv_head, p.head_dim, c->step_split);
+    // Exchange words carry 32-bit epochs, P per token, and the launch uses c->epoch + 1 ..
+    // c->epoch + n P. Before that range would pass 2^32 (about 40 M tokens of the 1B shape)
+    // the words are cleared and the count starts again at 0, so no word left from before
+    // can carry an epoch a reader expects.
+    const uint64_t P = 6ull * (uint64_t)p.n_layer + 8ull;
+    if ((uint64_t)c->epoch + (uint64_t)n * P >= 0xFFFFFFFFull) {
+        HIPCHK(c, hipStreamSynchronize(c->st));
+        HIPCHK(c, hipMemsetAsync(c->ex, 0, c->ex_words * 8, c->st));
+        c->epoch = 0;
+        c->ctl_host->epoch = 0;
+        HIPCHK(c, hipMemcpyAsync((char*)c->ctl + offsetof(Ctl, epoch), (char*)c->ctl_host + offsetof(Ctl, epoch),
+                                 sizeof(uint32_t), hipMemcpyHostToDevice, c->st));
+    }
     const hipError_t e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);
     if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("step kernel launch: ") + hipGetErrorString(e));
-    c->epoch += (uint32_t)(n * (6 * p.n_layer + 8));
+    c->epoch += (uint32_t)((uint64_t)n * P);
     return 0;
 }
 
@@ -730,6 +748,13 @@ int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out) {
 
     tf_hip_ctx* c = new tf_hip_ctx();
     c->device = device;
+    // TF_HIP_SPLIT_FROM: an override of the split-from span, read once here; ignored unless
+    // it is a whole number in [0, 512]
+    if (const char* sf = std::getenv("TF_HIP_SPLIT_FROM")) {
+        char* end = nullptr;
+        const long v = std::strtol(sf, &end, 10);
+        if (end != sf && *end == 0 && v >= 0 && v <= kSplitFromMax) c->split_from = (int)v;
+    }
     c->hp = p;
     c->H = p.n_head * p.head_dim;
     c->KVd = p.n_kv_head * p.head_dim;
@@ -908,7 +933,7 @@ int tf_hip_get_pos(const tf_hip_ctx* c) { return c ? c->pos : TF_HIP_EINVAL; }
 int tf_hip_decode(tf_hip_ctx* c, int32_t token, float* logits, int32_t* argmax) {
     if (!c) return TF_HIP_EINVAL;
     HIPCHK(c, hipSetDevice(c->device));
-    if (c->pos + 1 > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
+    if (c->pos >= c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
     if (token < 0 || token >= mat(c, TF_HIP_SLOT_TOKEN_EMBD).N)
         return fail(c, TF_HIP_ERANGE, "token " + std::to_string(token) + " out of range");
     const int use_step = ensure_step(c);
@@ -934,7 +959,7 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
     if (!c || (n > 0 && !tokens)) return TF_HIP_EINVAL;
     if (n <= 0) return 0;
     HIPCHK(c, hipSetDevice(c->device));
-    if (c->pos + n > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "prefill exceeds max_seq");
+    if (n > c->hp.max_seq - c->pos) return fail(c, TF_HIP_ERANGE, "prefill exceeds max_seq");
     const int64_t V = mat(c, TF_HIP_SLOT_TOKEN_EMBD).N;
     for (int i = 0; i < n; ++i)
         if (tokens[i] < 0 || tokens[i] >= V)
@@ -972,7 +997,7 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     if (n <= 0) return 0;
     HIPCHK(c, hipSetDevice(c->device));
     if (!c->have_logits) return fail(c, TF_HIP_ESTATE, "generate needs a prior prefill or decode");
-    if (c->pos + n > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
+    if (n > c->hp.max_seq - c->pos) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
     const int use_step = ensure_step(c);
     if (use_step < 0) return use_step;
     int rc = use_step ? 0 : ensure_graph(c);
@@ -1007,6 +1032,45 @@ int tf_hip_set_decode_path(tf_hip_ctx* c, int32_t path) {
 int tf_hip_set_split_all_from(tf_hip_ctx* c, int32_t span) {
     if (!c) return TF_HIP_EINVAL;
     c->split_all_from = span < 0 ? -1 : span;
+    return 0;
+}
+
+int tf_hip_set_split_from(tf_hip_ctx* c, int32_t span) {
+    if (!c) return TF_HIP_EINVAL;
+    if (span < 0) {
+        c->split_from = kSplitFromDefault;
+        return 0;
+    }
+    if (span > kSplitFromMax)
+        return fail(c, TF_HIP_EINVAL, "split_from " + std::to_string(span) + " above " + std::to_string(kSplitFromMax));
+    c->split_from = span;
+    return 0;
+}
+
+int tf_hip_get_step_config(tf_hip_ctx* c, int32_t* out, int32_t n) {
+    if (!c || !out || n < 5) return TF_HIP_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    const int s = ensure_step(c);
+    if (s < 0) return s;
+    if (s == 0) return fail(c, TF_HIP_ESTATE, "the step kernel does not run this model");
+    const tf_hip_hparams& p = c->hp;
+    out[0] = c->n_wg;
+    out[1] = c->step_split;
+    out[2] = c->step_split_all;
+    out[3] = c->split_from;
+    out[4] = c->split_all_from >= 0 ? c->split_all_from
+                                    : step_split_all_from(p.n_head, p.n_kv_head, p.head_dim, c->step_split);
+    return 0;
+}
+
+int tf_hip_set_exchange_epoch(tf_hip_ctx* c, uint32_t epoch) {
+    if (!c) return TF_HIP_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    c->epoch = epoch;
+    c->ctl_host->epoch = epoch;
+    HIPCHK(c, hipMemcpy((char*)c->ctl + offsetof(Ctl, epoch), (char*)c->ctl_host + offsetof(Ctl, epoch),
+                        sizeof(uint32_t), hipMemcpyHostToDevice));
     return 0;
 }
 
@@ -1075,7 +1139,7 @@ int tf_hip_profile_generate(tf_hip_ctx* c, int32_t n, int32_t* out, float* ms_by
     if (!c || n <= 0 || !out) return TF_HIP_EINVAL;
     HIPCHK(c, hipSetDevice(c->device));
     if (!c->have_logits) return fail(c, TF_HIP_ESTATE, "generate needs a prior prefill or decode");
-    if (c->pos + n > c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
+    if (n > c->hp.max_seq - c->pos) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
     int rc = check_ready(c);
     if (rc) return rc;
     const int pos0 = c->pos;

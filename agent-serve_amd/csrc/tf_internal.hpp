@@ -17,7 +17,7 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 
 // One weight matrix [N rows x K] in the backend's HBM layout. The GGUF bytes are
 // split into streams so that every lane step is one aligned 16-byte load:
-//   Q8_0: q  = u8 [N][K]    q+128 (offset binary), s = f16 d [N][K/32]
+//   Q8_0: q  = i8 [N][K]    the GGUF quants, s = f16 d [N][K/32]
 //   Q4_0: q  = u8 [N][K/2]  the GGUF nibble bytes (element j low, j+16 high), s = f16 d [N][K/32]
 //   Q4_1: q  = as Q4_0,     s = f16 pairs (d, m) [N][K/32]
 //   Q6_K: q  = u8 [N][K/2]  low nibbles of each 32-element group (element j low, j+16 high)
@@ -88,8 +88,8 @@ struct GemvArgs {
 
 struct AttnArgs {
     const float* q;         // [H][hd] raw (bias added, not rotated)
-    const float* knew;      // [G][hd] raw
-    const float* vnew;      // [G][hd]
+    const float* knew;      // [G][hd] raw, or nullptr: the cache already holds the row at pos
+    const float* vnew;      // [G][hd], or nullptr as knew
     float* kc;              // this layer's K cache
     float* vc;              // this layer's V cache
     const float* rope_cos;  // [max_seq][hd/2]

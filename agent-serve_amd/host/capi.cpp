@@ -167,6 +167,30 @@ int tfh_gguf_summary(const char* path, uint64_t* out, char* arch, int32_t arch_l
     });
 }
 
+// Model::decode_bytes(pos) of the GGUF at path, without a device: the algorithmic bytes of
+// one decode step at position pos.
+double tfh_file_decode_bytes(const char* path, int32_t pos) {
+    double v = -1.0;
+    guard(nullptr, [&] {
+        tfh::GgufFile g(path);
+        v = tfh::decode_traffic(g, tfh::read_hparams(g)).at(pos);
+    });
+    return v;
+}
+
+// The host RoPE tables of the GGUF at path (the Model's hyperparameter rules, llama3
+// scaling included): [n_pos][head_dim / 2] cosines and sines.
+int tfh_file_rope_tables(const char* path, int32_t n_pos, float* cos_out, float* sin_out) {
+    return guard(nullptr, [&] {
+        tfh::GgufFile g(path);
+        const tfh::HParams h = tfh::read_hparams(g);
+        std::vector<float> c, s;
+        tfh::rope_tables(tfh::rope_freqs(h.rope), n_pos, c, s);
+        std::memcpy(cos_out, c.data(), c.size() * 4);
+        std::memcpy(sin_out, s.data(), s.size() * 4);
+    });
+}
+
 int tfh_rope_tables(float theta, int32_t n_rot, int32_t n_pos, float* cos_out, float* sin_out) {
     return guard(nullptr, [&] {
         tfh::RopeParams rp;

@@ -75,37 +75,82 @@ void Model::check(int rc, const char* what) const {
     }
 }
 
-Model::Model(const std::string& path, const RunConfig& cfg) : gguf_(path), cfg_(cfg) {
-    // hyperparameters exactly as model.cpp:9-41 derives them
-    const std::string a = gguf_.arch();
+namespace {
+
+const char* const kLayerNames[TF_HIP_LAYER_COUNT] = {
+    "attn_norm.weight", "attn_q.weight",   "attn_k.weight", "attn_v.weight",   "attn_output.weight",
+    "attn_q.bias",      "attn_k.bias",     "attn_v.bias",   "ffn_norm.weight", "ffn_gate.weight",
+    "ffn_up.weight",    "ffn_down.weight"};
+
+bool optional_kind(int k) { return k == TF_HIP_LAYER_BQ || k == TF_HIP_LAYER_BK || k == TF_HIP_LAYER_BV; }
+
+}  // namespace
+
+HParams read_hparams(const GgufFile& g) {
+    HParams h;
+    const std::string a = g.arch();
     auto key = [&](const char* f) { return a + "." + f; };
-    n_vocab_ = (int)gguf_.u64(key("vocab_size"), 0);
-    if (!n_vocab_) n_vocab_ = (int)gguf_.arr_len("tokenizer.ggml.tokens");
-    n_embd_ = (int)gguf_.u64(key("embedding_length"));
-    n_ff_ = (int)gguf_.u64(key("feed_forward_length"));
-    n_layer_ = (int)gguf_.u64(key("block_count"));
-    n_head_ = (int)gguf_.u64(key("attention.head_count"));
-    n_kv_head_ = (int)gguf_.u64(key("attention.head_count_kv"), (uint64_t)n_head_);
-    head_dim_ = n_head_ ? n_embd_ / n_head_ : 0;  // n_embd / n_head wins over rope.dimension_count
-    rms_eps_ = gguf_.f32(key("attention.layer_norm_rms_epsilon"), 1e-5f);
-    RopeParams rp;
-    rp.theta = gguf_.f32(key("rope.freq_base"), 10000.0f);
-    rp.n_rot = head_dim_;
-    if (gguf_.str(key("rope.scaling.type"), "") == "llama3") {
+    h.n_vocab = (int)g.u64(key("vocab_size"), 0);
+    if (!h.n_vocab) h.n_vocab = (int)g.arr_len("tokenizer.ggml.tokens");
+    h.n_embd = (int)g.u64(key("embedding_length"));
+    h.n_ff = (int)g.u64(key("feed_forward_length"));
+    h.n_layer = (int)g.u64(key("block_count"));
+    h.n_head = (int)g.u64(key("attention.head_count"));
+    h.n_kv_head = (int)g.u64(key("attention.head_count_kv"), (uint64_t)h.n_head);
+    h.head_dim = h.n_head ? h.n_embd / h.n_head : 0;  // n_embd / n_head wins over rope.dimension_count
+    h.rms_eps = g.f32(key("attention.layer_norm_rms_epsilon"), 1e-5f);
+    RopeParams& rp = h.rope;
+    rp.theta = g.f32(key("rope.freq_base"), 10000.0f);
+    rp.n_rot = h.head_dim;
+    if (g.str(key("rope.scaling.type"), "") == "llama3") {
         rp.llama3 = true;
-        rp.scale = gguf_.f32(key("rope.scaling.factor"), 32.0f);
-        rp.low_freq_f = gguf_.f32(key("rope.scaling.low_freq_factor"), 1.0f);
-        rp.high_freq_f = gguf_.f32(key("rope.scaling.high_freq_factor"), 4.0f);
-        rp.orig_ctx = (float)gguf_.u64(key("rope.scaling.original_context_length"), 8192);
+        rp.scale = g.f32(key("rope.scaling.factor"), 32.0f);
+        rp.low_freq_f = g.f32(key("rope.scaling.low_freq_factor"), 1.0f);
+        rp.high_freq_f = g.f32(key("rope.scaling.high_freq_factor"), 4.0f);
+        rp.orig_ctx = (float)g.u64(key("rope.scaling.original_context_length"), 8192);
     }
-    bos_ = (int)gguf_.u64("tokenizer.ggml.bos_token_id", 1);
-    eos_ = (int)gguf_.u64("tokenizer.ggml.eos_token_id", 2);
+    h.bos = (int)g.u64("tokenizer.ggml.bos_token_id", 1);
+    h.eos = (int)g.u64("tokenizer.ggml.eos_token_id", 2);
+    if (!h.n_vocab) h.n_vocab = (int)g.must("token_embd.weight").rows();
+    if (h.n_layer <= 0 || h.n_embd <= 0 || h.n_head <= 0) throw std::runtime_error("bad hyperparameters");
+    return h;
+}
+
+DecodeTraffic decode_traffic(const GgufFile& g, const HParams& hp) {
+    DecodeTraffic t;
+    const TensorInfo& tok = g.must("token_embd.weight");
+    const TensorInfo* out = g.find("output.weight");
+    // tied: token_embd is the lm_head and read whole; untied: output is, and one row of token_embd
+    t.tensor_bytes = out ? out->nbytes : tok.nbytes;
+    t.tensor_bytes += g.must("output_norm.weight").nbytes;
+    for (int l = 0; l < hp.n_layer; ++l)
+        for (int k = 0; k < TF_HIP_LAYER_COUNT; ++k) {
+            const std::string name = "blk." + std::to_string(l) + "." + kLayerNames[k];
+            const TensorInfo* ti = optional_kind(k) ? g.find(name) : &g.must(name);
+            if (ti) t.tensor_bytes += ti->nbytes;
+        }
+    t.embd_row_bytes = ggml_row_nbytes(tok.type, tok.ne[0]);
+    t.kv_bytes_per_pos = (double)hp.n_layer * hp.n_kv_head * hp.head_dim * 4.0 * 2.0;
+    return t;
+}
+
+Model::Model(const std::string& path, const RunConfig& cfg) : gguf_(path), cfg_(cfg) {
+    const HParams h = read_hparams(gguf_);
+    n_vocab_ = h.n_vocab;
+    n_embd_ = h.n_embd;
+    n_ff_ = h.n_ff;
+    n_layer_ = h.n_layer;
+    n_head_ = h.n_head;
+    n_kv_head_ = h.n_kv_head;
+    head_dim_ = h.head_dim;
+    rms_eps_ = h.rms_eps;
+    bos_ = h.bos;
+    eos_ = h.eos;
+    traffic_ = decode_traffic(gguf_, h);
 
     const TensorInfo& tok = gguf_.must("token_embd.weight");
     const TensorInfo& onorm = gguf_.must("output_norm.weight");
     const TensorInfo* out = gguf_.find("output.weight");
-    if (!n_vocab_) n_vocab_ = (int)tok.rows();
-    if (n_layer_ <= 0 || n_embd_ <= 0 || n_head_ <= 0) throw std::runtime_error("bad hyperparameters");
 
     tf_hip_hparams hp{};
     hp.n_vocab = n_vocab_;
@@ -123,29 +168,19 @@ Model::Model(const std::string& path, const RunConfig& cfg) : gguf_(path), cfg_(
 
     auto up = [&](int slot, const TensorInfo& t) {
         check(tf_hip_upload_tensor(ctx_, slot, t.type, t.ne[0], t.rows(), t.data, t.nbytes), t.name.c_str());
-        tensor_bytes_read_ += t.nbytes;
     };
     up(TF_HIP_SLOT_TOKEN_EMBD, tok);
-    embd_row_bytes_ = ggml_row_nbytes(tok.type, tok.ne[0]);
     up(TF_HIP_SLOT_OUTPUT_NORM, onorm);
-    if (out) {
-        up(TF_HIP_SLOT_OUTPUT, *out);
-        tensor_bytes_read_ -= tok.nbytes;  // untied: only one embedding row is read per token
-    }
-    static const char* kNames[TF_HIP_LAYER_COUNT] = {
-        "attn_norm.weight", "attn_q.weight",   "attn_k.weight", "attn_v.weight",   "attn_output.weight",
-        "attn_q.bias",      "attn_k.bias",     "attn_v.bias",   "ffn_norm.weight", "ffn_gate.weight",
-        "ffn_up.weight",    "ffn_down.weight"};
+    if (out) up(TF_HIP_SLOT_OUTPUT, *out);
     for (int l = 0; l < n_layer_; ++l) {
         const std::string p = "blk." + std::to_string(l) + ".";
         for (int k = 0; k < TF_HIP_LAYER_COUNT; ++k) {
-            const bool optional = k == TF_HIP_LAYER_BQ || k == TF_HIP_LAYER_BK || k == TF_HIP_LAYER_BV;
-            const TensorInfo* t = optional ? gguf_.find(p + kNames[k]) : &gguf_.must(p + kNames[k]);
+            const TensorInfo* t = optional_kind(k) ? gguf_.find(p + kLayerNames[k]) : &gguf_.must(p + kLayerNames[k]);
             if (t) up(TF_HIP_SLOT_LAYER(l, k), *t);
         }
     }
     std::vector<float> ct, st;
-    rope_tables(rope_freqs(rp), cfg_.max_seq, ct, st);
+    rope_tables(rope_freqs(h.rope), cfg_.max_seq, ct, st);
     check(tf_hip_set_rope_table(ctx_, ct.data(), st.data(), cfg_.max_seq, head_dim_ / 2), "rope table");
 }
 
@@ -153,7 +188,7 @@ Model::~Model() { tf_hip_destroy(ctx_); }
 
 void Model::prefill(const int* tokens, int n, float* logits) {
     if (n <= 0) return;
-    if (n_pos_ + n > cfg_.max_seq) throw std::runtime_error("prefill exceeds max_seq");
+    if (n > cfg_.max_seq - n_pos_) throw std::runtime_error("prefill exceeds max_seq");
     std::vector<int32_t> t(tokens, tokens + n);
     int32_t am = -1;
     check(tf_hip_prefill(ctx_, t.data(), n, logits, &am), "prefill");
@@ -162,7 +197,7 @@ void Model::prefill(const int* tokens, int n, float* logits) {
 }
 
 void Model::decode(int token, float* logits) {
-    if (n_pos_ + 1 > cfg_.max_seq) throw std::runtime_error("decode exceeds max_seq");
+    if (n_pos_ >= cfg_.max_seq) throw std::runtime_error("decode exceeds max_seq");
     int32_t am = -1;
     check(tf_hip_decode(ctx_, token, logits, &am), "decode");
     last_argmax_ = am;
@@ -171,7 +206,7 @@ void Model::decode(int token, float* logits) {
 
 void Model::generate(int n, int32_t* out_tokens) {
     if (n <= 0) return;
-    if (n_pos_ + n > cfg_.max_seq) throw std::runtime_error("decode exceeds max_seq");
+    if (n > cfg_.max_seq - n_pos_) throw std::runtime_error("decode exceeds max_seq");
     check(tf_hip_generate(ctx_, n, out_tokens), "generate");
     n_pos_ += n;
 }
@@ -182,10 +217,7 @@ void Model::reset() {
     last_argmax_ = -1;
 }
 
-double Model::decode_bytes(int pos) const {
-    const double kv = (double)n_layer_ * n_kv_head_ * head_dim_ * 4.0 * 2.0;
-    return (double)tensor_bytes_read_ + (double)embd_row_bytes_ + kv * (pos + 1) + kv;
-}
+double Model::decode_bytes(int pos) const { return traffic_.at(pos); }
 
 std::string Model::describe() const {
     std::ostringstream o;

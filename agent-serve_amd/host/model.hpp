@@ -49,6 +49,27 @@ struct RopeParams {
 std::vector<float> rope_freqs(const RopeParams& rp);
 void rope_tables(const std::vector<float>& freq, int n_pos, std::vector<float>& cos_tab, std::vector<float>& sin_tab);
 
+// Hyperparameters exactly as model.cpp:9-41 derives them from the GGUF metadata.
+struct HParams {
+    int n_vocab = 0, n_embd = 0, n_ff = 0, n_layer = 0, n_head = 0, n_kv_head = 0, head_dim = 0;
+    int bos = 1, eos = 2;
+    float rms_eps = 1e-5f;
+    RopeParams rope;
+};
+HParams read_hparams(const GgufFile& g);
+
+// Algorithmic bytes of one decode step (the roofline's numerator): every tensor the step
+// reads once -- the layer matrices, norms and biases, the lm_head (token_embd when tied)
+// -- plus one embedding row, plus K and V rows of every attended position and the new
+// row written. decode_bytes(pos) = tensor_bytes + embd_row_bytes + kv_bytes_per_pos * (pos + 2).
+struct DecodeTraffic {
+    size_t tensor_bytes = 0;
+    size_t embd_row_bytes = 0;
+    double kv_bytes_per_pos = 0;  // n_layer * n_kv_head * head_dim * 4 * 2 (fp32 K and V)
+    double at(int pos) const { return (double)tensor_bytes + (double)embd_row_bytes + kv_bytes_per_pos * (pos + 2); }
+};
+DecodeTraffic decode_traffic(const GgufFile& g, const HParams& hp);
+
 class Model {
 public:
     Model(const std::string& path, const RunConfig& cfg);
@@ -96,8 +117,7 @@ private:
     float rms_eps_ = 1e-5f;
     int n_pos_ = 0;
     int last_argmax_ = -1;
-    size_t embd_row_bytes_ = 0;
-    size_t tensor_bytes_read_ = 0;  // bytes of every tensor a decode step reads
+    DecodeTraffic traffic_;
 };
 
 }  // namespace tfh

@@ -273,6 +273,13 @@ bool synth_preset(const std::string& name, SynthSpec* s) {
         p.rope_theta = 1000000.0f;
         p.rms_eps = 1e-6f;
         p.bias = true;
+    } else if (name == "tiny_hd128") {
+        // head_dim 128 with 6 query heads per kv head and QKV bias, as the Qwen2.5-1.5B shape
+        p.arch = "qwen2";
+        p.n_vocab = 1024; p.n_embd = 768; p.n_ff = 1024; p.n_layer = 2; p.n_head = 6; p.n_kv_head = 1;
+        p.rope_theta = 1000000.0f;
+        p.rms_eps = 1e-6f;
+        p.bias = true;
     } else if (name == "small_q8") {
         // mid-size Llama-like model for parity at realistic row lengths (hd 64, GQA 4)
         p.n_vocab = 4096; p.n_embd = 512; p.n_ff = 1536; p.n_layer = 4; p.n_head = 8; p.n_kv_head = 2;
@@ -286,7 +293,7 @@ bool synth_preset(const std::string& name, SynthSpec* s) {
 
 std::vector<std::string> synth_preset_names() {
     return {"llama1b_q8", "qwen05b_q8", "llama1b_mixq4", "qwen15b_q8",
-            "tiny_f32",   "tiny_q8",    "tiny_mixq4",    "tiny_qwen", "small_q8"};
+            "tiny_f32",   "tiny_q8",    "tiny_mixq4",    "tiny_qwen", "tiny_hd128", "small_q8"};
 }
 
 // ---------------------------------------------------------------- writer

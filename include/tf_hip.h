@@ -112,10 +112,10 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
 /* Decode path of prefill / decode / generate. TF_HIP_PATH_STEP (the default): one
  * persistent cooperative kernel per call runs every token of the call, for models whose
  * layer matrices share one format the kernel is compiled for (Q8_0, F32, or Q4_0 with
- * Q4_1 wo / ffn_down allowed; others use the graph path; tokens attending more than 64
- * positions split each layer's attention over workgroups, shorter spans run it on one
- * workgroup per kv head; the environment variable TF_HIP_SPLIT_FROM moves that span, at
- * most 512). TF_HIP_PATH_GRAPH: one captured graph of
+ * Q4_1 wo / ffn_down allowed; others use the graph path; tokens attending more than
+ * split_from positions, 64 by default, split each layer's attention over workgroups,
+ * shorter spans run it on one workgroup per kv head; see tf_hip_set_split_from).
+ * TF_HIP_PATH_GRAPH: one captured graph of
  * per-layer kernels replayed per token. Both compute the same function; neither has a
  * counterpart in the reference (a backend choice below Model::decode, model.cpp:197-208).
  * tf_hip_get_decode_path returns the path the next call will take (needs every tensor
@@ -131,6 +131,28 @@ int tf_hip_get_decode_path(tf_hip_ctx* ctx);
  * model-derived default. Results are the same function either way; used by the tests to
  * place the switch inside a short decode. */
 int tf_hip_set_split_all_from(tf_hip_ctx* ctx, int32_t span);
+
+/* Tuning knob of the step kernel's attention (no counterpart in the reference): tokens
+ * attending at most `span` positions run attention on one workgroup per kv head, longer
+ * spans split it over workgroups. 0 <= span <= 512 (one workgroup per kv head attends at
+ * most 512 positions); span < 0 restores the default, 64. Out-of-range spans are rejected
+ * with TF_HIP_EINVAL. The environment variable TF_HIP_SPLIT_FROM, read once by
+ * tf_hip_create, sets the initial value when it is a whole number in that range. Results
+ * are the same function either way. */
+int tf_hip_set_split_from(tf_hip_ctx* ctx, int32_t span);
+
+/* The step kernel's attention configuration for this model (no counterpart in the
+ * reference): out[0] workgroups of a launch, out[1] splits per kv head of the trailing
+ * layout, out[2] splits per kv head when every workgroup splits (0: that layout is not
+ * available), out[3] split_from, out[4] the span past which every workgroup splits.
+ * n >= 5. Needs every tensor uploaded; TF_HIP_ESTATE when the step kernel does not run
+ * this model. */
+int tf_hip_get_step_config(tf_hip_ctx* ctx, int32_t* out, int32_t n);
+
+/* Test hook (no counterpart in the reference): sets the step kernel's exchange epoch
+ * counter, so that a test can run a launch across the counter's wrap at 2^32 (the kernel
+ * then clears its exchange words and starts the count again). */
+int tf_hip_set_exchange_epoch(tf_hip_ctx* ctx, uint32_t epoch);
 
 /* Prefill path (no counterpart in the reference, whose layer_prefill is the one
  * path, model.cpp:144-195): TF_HIP_PREFILL_MFMA runs a prompt of two or more tokens

@@ -27,7 +27,7 @@ import __graft_entry__  # noqa: E402
 from oracle.bind import RefModel, greedy_stream, ref_lib  # noqa: E402
 from rows import random_rows  # noqa: E402
 
-PRESETS = ["tiny_f32", "tiny_q8", "tiny_mixq4", "tiny_qwen", "small_q8"]
+PRESETS = ["tiny_f32", "tiny_q8", "tiny_mixq4", "tiny_qwen", "tiny_hd128", "small_q8"]
 N_GREEDY = 16
 
 

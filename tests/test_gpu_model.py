@@ -8,11 +8,11 @@ import numpy as np
 import pytest
 
 from conftest import rel_err
-from gpu_util import model_parity
+from gpu_util import REGRESS, model_parity
 
 pytestmark = pytest.mark.gpu
 
-SMALL = ["tiny_f32", "tiny_q8", "tiny_mixq4", "tiny_qwen", "small_q8"]
+SMALL = ["tiny_f32", "tiny_q8", "tiny_mixq4", "tiny_qwen", "tiny_hd128", "small_q8"]
 GRAPH, STEP = 0, 1  # HipModel.PATH_GRAPH, HipModel.PATH_STEP
 
 
@@ -28,7 +28,7 @@ def test_small_models(pkg, gguf, preset, layout, path):
 
 
 @pytest.mark.parametrize("preset,want", [("tiny_q8", STEP), ("tiny_f32", STEP), ("small_q8", STEP),
-                                         ("tiny_mixq4", STEP)])
+                                         ("tiny_mixq4", STEP), ("tiny_hd128", STEP)])
 def test_decode_path_selection(pkg, gguf, preset, want):
     """The persistent step kernel runs models whose layer matrices share a compiled format
     (Q4_0 layers may have Q4_1 wo / ffn_down, as tiny_mixq4's first and last layer do),
@@ -46,7 +46,7 @@ def test_decode_path_selection(pkg, gguf, preset, want):
 
 @pytest.mark.parametrize("path", [GRAPH, STEP], ids=["graph", "step"])
 @pytest.mark.parametrize("layout", [0, 1])
-@pytest.mark.parametrize("preset", ["tiny_q8", "tiny_f32", "tiny_qwen", "small_q8", "tiny_mixq4"])
+@pytest.mark.parametrize("preset", ["tiny_q8", "tiny_f32", "tiny_qwen", "small_q8", "tiny_mixq4", "tiny_hd128"])
 def test_long_cache_split_attention(pkg, gguf, preset, layout, path):
     """A 600-token prompt in a 1024-position cache: the step kernel's attention splits the
     positions over its trailing workgroups and merges the splits there, the graph path's
@@ -63,29 +63,87 @@ def test_long_cache_split_attention(pkg, gguf, preset, layout, path):
 # (tf_hip_set_split_all_from). The prompts end a few positions short of it, so the
 # per-token decodes and the one-launch greedy loop both cross it; with 1024 and 4096 the
 # trailing splits hold 64 positions each at the switch (16 and 64 splits per kv head).
+# tiny_hd128 runs the head_dim-128 build (6 query heads per kv head, as the Qwen2.5-1.5B
+# shape) through both layouts past 1,800 positions.
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("preset,n_prompt,max_seq,switch", [("tiny_f32", 1018, 2048, 1024),
                                                             ("tiny_q8", 4090, 4200, 4096),
-                                                            ("tiny_qwen", 700, 1024, 705)])
+                                                            ("tiny_qwen", 700, 1024, 705),
+                                                            ("tiny_hd128", 1800, 2048, 1805)])
 def test_long_cache_split_layout_switch(pkg, gguf, preset, n_prompt, max_seq, switch, layout):
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"] + 11, n_prompt, info["n_vocab"])
+
+    def setup(hip):
+        hip.set_split_all_from(switch)
+        cfg = hip.step_config()
+        assert cfg["split"] > 0 and cfg["split_all"] > 0 and cfg["split_all_from"] == switch, cfg
+
     ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, max_seq, layout, decode_path=STEP,
-                                                 setup=lambda hip: hip.set_split_all_from(switch))
+                                                 setup=setup)
     print(f"{preset} {n_prompt} layout {layout}: logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
 
 
 # Caches of at most 512 positions: tokens attending up to 64 positions run attention on one
 # workgroup per kv head, longer spans split it. Prompts of 60 tokens put the switch inside
 # the per-token decodes and inside the one-launch greedy loop, whose later, split tokens
-# read the rows the earlier ones stored from other workgroups.
+# read the rows the earlier ones stored from other workgroups. tiny_hd128 and the
+# full-size Qwen2.5-1.5B shape run the head_dim-128 build on both sides of the switch.
 @pytest.mark.parametrize("layout", [0, 1])
-@pytest.mark.parametrize("preset", ["tiny_f32", "tiny_q8", "tiny_qwen"])
+@pytest.mark.parametrize("preset", ["tiny_f32", "tiny_q8", "tiny_qwen", "tiny_hd128", "qwen15b_q8"])
 def test_short_cache_split_switch(pkg, gguf, preset, layout):
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"] + 5, 60, info["n_vocab"])
-    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, 512, layout, decode_path=STEP)
+
+    def setup(hip):
+        assert hip.decode_path() == STEP
+        cfg = hip.step_config()
+        # the switch really happens inside the decode: a split layout exists and spans
+        # 61..72 cross split_from
+        assert cfg["split"] > 0 and cfg["split_from"] == 64, cfg
+
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, 512, layout, decode_path=STEP,
+                                                 setup=setup)
     print(f"{preset} layout {layout}: logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
+
+
+@pytest.mark.parametrize("span", [0, 512])
+def test_split_from_knob(pkg, gguf, span):
+    """tf_hip_set_split_from: every token split (0) or none below 512 positions (512) gives
+    the same function; values above 512 are rejected."""
+    preset = "tiny_q8"
+    info = pkg.synth_preset_info(preset)
+    prompt = pkg.synth_prompt(info["seed"] + 3, 40, info["n_vocab"])
+
+    def setup(hip):
+        with pytest.raises(RuntimeError, match="above 512"):
+            hip.set_split_from(513)
+        hip.set_split_from(span)
+        assert hip.step_config()["split_from"] == span
+
+    ids, worst, _, _ = model_parity(pkg, gguf(preset), prompt, 12, 512, 0, decode_path=STEP, setup=setup)
+    print(f"split_from {span}: logits {worst:.2e}")
+
+
+def test_exchange_epoch_wrap(pkg, gguf):
+    """A greedy launch that runs the step kernel's 32-bit exchange epoch past 2^32: the
+    backend clears the exchange words and restarts the count, and the tokens and logits
+    are those of a run far from the wrap."""
+    path = gguf("small_q8")
+    prompt = np.array([3, 99, 7, 1200, 5, 42, 8], np.int32)
+    out = []
+    for start in (None, 2**32 - 300):
+        hip = pkg.HipModel(path, max_seq=64)
+        hip.set_decode_path(STEP)
+        hip.prefill(prompt)
+        if start is not None:
+            hip.set_exchange_epoch(start)  # a few tokens before the wrap (32 epochs per token)
+        ids = hip.generate(24)
+        ld, _ = hip.decode(int(ids[-1]))
+        out.append((ids, ld))
+        hip.close()
+    assert np.array_equal(out[0][0], out[1][0])
+    assert np.array_equal(out[0][1], out[1][1])
 
 
 TOKENS, MFMA = 0, 1  # HipModel.PREFILL_TOKENS, HipModel.PREFILL_MFMA
@@ -218,10 +276,66 @@ def test_errors_and_reset(pkg, gguf):
     ("qwen05b_q8", 16, 128, 512, 0),    # Qwen2.5-0.5B shape with QKV bias
     ("llama1b_mixq4", 6, 64, 512, 0),   # Q4_0 / Q4_1 / Q6_K mix
     ("qwen15b_q8", 64, 16, 8192, 1),    # Qwen2.5-1.5B shape, head-major cache (short prompt)
-    ("llama1b_q8", 512, 4, 1024, 0),    # 512-token prompt on the matrix cores
+    ("llama1b_q8", 512, 16, 1024, 0),   # 512-token prompt on the matrix cores, then 16 decode tokens
 ])
 def test_full_size(pkg, gguf, preset, n_prompt, n_gen, max_seq, layout):
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"], n_prompt, info["n_vocab"])
     ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, n_gen, max_seq, layout)
     print(f"{preset}: {len(ids)} tokens identical; logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
+
+
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+def test_long_context_workload_vs_reference_fixture(pkg, gguf):
+    """The Qwen2.5-1.5B-shape workload at full size: a 4096-token prompt (matrix-core
+    prefill in two chunks), head-major cache of 8192 positions, then 256 greedy tokens,
+    against the reference's own run (tests/golden/qwen15b_4096.npz, written by
+    make_golden_long.py from the compiled reference; the taps from the oracle run whose
+    logits equal the reference's bit for bit). Per step: the device argmax is the
+    reference's token, and the device logits at the reference's top-8 tokens are within
+    1e-3 of the largest of them; the last step's taps within 1e-3; the one-launch greedy
+    loop from a reset gives the same 256 tokens."""
+    fx = np.load(GOLDEN / "qwen15b_4096.npz")
+    path = gguf("qwen15b_q8")
+    import hashlib
+    h = hashlib.sha256()
+    with open(path, "rb") as f:
+        for chunk in iter(lambda: f.read(1 << 20), b""):
+            h.update(chunk)
+    assert h.digest() == fx["gguf_sha256"].tobytes(), "synthetic writer output changed"
+    info = pkg.synth_preset_info("qwen15b_q8")
+    prompt = pkg.synth_prompt(int(fx["prompt_seed"]), int(fx["n_prompt"]), info["n_vocab"])
+    ids, top_i, top_v = fx["ids"], fx["top_idx"], fx["top_val"]
+    hip = pkg.HipModel(path, max_seq=int(fx["max_seq"]), kv_layout=int(fx["layout"]))
+    try:
+        assert hip.decode_path() == STEP
+        worst = 0.0
+
+        def check(step, lg, am):
+            nonlocal worst
+            want = top_v[step].astype(np.float64)
+            e = float(np.max(np.abs(lg[top_i[step]] - want)) / np.max(np.abs(want)))
+            assert e <= 1e-3, f"step {step}: top-8 logits rel err {e:.3e}"
+            assert am == int(top_i[step][0]), f"step {step}: argmax {am} != reference {top_i[step][0]}"
+            worst = max(worst, e)
+
+        lg, am = hip.prefill(prompt)
+        check(0, lg, am)
+        for i in range(len(ids)):
+            lg, am = hip.decode(int(ids[i]))
+            check(i + 1, lg, am)
+        for layer, want in zip(fx["tap_layers"], fx["taps"]):
+            e = rel_err(hip.layer_act(int(layer)), want)
+            assert e <= 1e-3, f"tap {layer} rel err {e:.3e}"
+            assert e <= REGRESS, f"tap {layer}: numerics regression {e:.2e}"
+        hip.reset()
+        _, am0 = hip.prefill(prompt, want_logits=False)
+        assert am0 == ids[0]
+        gen = hip.generate(len(ids))  # its first token is the prefill's argmax
+        assert gen.tolist() == ids.tolist()
+        assert worst <= REGRESS, f"numerics regression: top-8 logits {worst:.2e}"
+        print(f"qwen15b 4096 + {len(ids)}: ids identical, top-8 logits rel err {worst:.2e}")
+    finally:
+        hip.close()
