@@ -76,6 +76,8 @@ def hip_lib() -> C.CDLL:
                                          C.c_int32, C.c_int32, _f32p]),
         "tf_hip_attn_prefill": (C.c_int, [C.c_int, _f32p, _f32p, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                           _f32p]),
+        "tf_hip_attn_decode_noalloc": (C.c_int, [C.c_int, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                                 C.c_int32, C.c_int32, vp, vp]),
         "tf_hip_argmax": (C.c_int, [C.c_int, _f32p, C.c_int32, _i32p]),
         "tf_hip_read_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p]),
         "tf_hip_copy_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p]),

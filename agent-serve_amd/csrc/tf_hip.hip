@@ -8,6 +8,7 @@
 // does) and the greedy loop (token = previous argmax, no host round trip).
 #include <algorithm>
 #include <cstdio>
+#include <mutex>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -1399,6 +1400,78 @@ int tf_hip_attn_decode(int device, const float* q, const float* k_rows, const fl
     OPCHK(hipMemcpyAsync(out, dout, (size_t)n_heads * hd * 4, hipMemcpyDeviceToHost, s.st));
     OPCHK(hipStreamSynchronize(s.st));
     return 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free attention
+
+namespace {
+
+// Device scratch of tf_hip_attn_decode_noalloc: the split partials (o, then m and l) of
+// one call. Each GPU the library runs on holds its own copy until the process ends.
+constexpr size_t kScratchFloats = TF_HIP_ATTN_SCRATCH_BYTES / sizeof(float);
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on `device` (the current device), looked up once per
+// device. In host code the array's name is only a stand-in; kernels get this address.
+int scratch_on(int device, float** out) {
+    if (device < 0 || device >= kMaxDevices) return TF_HIP_EINVAL;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return TF_HIP_EDEVICE;
+        g_scratch_ptr[device] = (float*)p;
+    }
+    *out = g_scratch_ptr[device];
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tf_hip_attn_decode_noalloc(int device, const float* q, const float* k_cache, const float* v_cache,
+                               int32_t n_heads, int32_t n_kv, int32_t hd, int32_t n_pos, int32_t max_seq,
+                               int32_t layout, float* out, void* stream) {
+    if (!q || !k_cache || !v_cache || !out || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > 8 ||
+        hd % 8 || hd > 256 || hd <= 0 || n_pos <= 0 || n_pos > max_seq || (layout != 0 && layout != 1))
+        return TF_HIP_EINVAL;
+    const int S = attn_splits(max_seq);
+    // o partials [n_heads][S][hd], then (m, l) pairs [n_heads][S][2]
+    const size_t need = (size_t)n_heads * S * hd + (size_t)n_heads * S * 2;
+    if (S > 1 && need > kScratchFloats) return TF_HIP_ESCRATCH;
+    if (hipSetDevice(device) != hipSuccess) return TF_HIP_EDEVICE;
+    float* ptr = nullptr;
+    int rc = scratch_on(device, &ptr);
+    if (rc) return rc;
+    AttnArgs a{};
+    a.q = q;
+    a.knew = nullptr;  // the row at n_pos - 1 is read from the cache
+    a.vnew = nullptr;
+    a.kc = const_cast<float*>(k_cache);  // read only: store_kv = 0
+    a.vc = const_cast<float*>(v_cache);
+    a.rope_cos = q;  // unused: rope = 0
+    a.rope_sin = q;
+    a.part_o = ptr;
+    a.part_ml = ptr + (size_t)n_heads * S * hd;
+    a.out = out;
+    a.ctl = nullptr;
+    a.H = n_heads;
+    a.G = n_kv;
+    a.hd = hd;
+    a.max_seq = max_seq;
+    a.layout = layout;
+    a.S = S;
+    a.rope = 0;
+    a.store_kv = 0;
+    a.fixed_pos = n_pos - 1;
+    a.fixed_start = 0;
+    return launch_attn_decode(a, (hipStream_t)stream) == hipSuccess ? 0 : TF_HIP_EDEVICE;
 }
 
 int tf_hip_argmax(int device, const float* x, int32_t n, int32_t* out) {

@@ -30,6 +30,7 @@ extern "C" {
 #define TF_HIP_ENOMEM -3   /* device allocation failed */
 #define TF_HIP_EDEVICE -4  /* HIP runtime error */
 #define TF_HIP_ESTATE -5   /* required tensors not uploaded */
+#define TF_HIP_ESCRATCH -6 /* request larger than a static scratch (tf_hip_attn_decode_noalloc) */
 
 /* ggml tensor types accepted by the token loop (tensor.cpp:18-28) */
 #define TF_HIP_TYPE_F32 0
@@ -219,6 +220,25 @@ int tf_hip_rmsnorm(int device, const float* x, const float* w, int32_t n, int32_
  * max_seq before the kernel runs; out [n_heads][hd]. */
 int tf_hip_attn_decode(int device, const float* q, const float* k_rows, const float* v_rows, int32_t n_heads,
                        int32_t n_kv, int32_t hd, int32_t n_pos, int32_t max_seq, int32_t layout, float* out);
+
+/* attn_decode over a device-resident cache with no allocation at all. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory -- code under HIP
+ * graph capture, serving loops that forbid hipMalloc. The same function and kernels as
+ * tf_hip_attn_decode on the same rows, but every pointer is device memory: q and out
+ * [n_heads][hd] (q already rotated), k_cache / v_cache a cache of the given layout and
+ * max_seq whose positions [0, n_pos) are filled. The work is enqueued on `stream` (a
+ * hipStream_t; NULL for the null stream) and not waited for; nothing is allocated,
+ * freed or synchronised. Caches longer than 512 positions split the positions over
+ * S = min(512, ceil(max_seq / 32)) workgroups per kv head, whose partials live in the
+ * library's static device scratch of TF_HIP_ATTN_SCRATCH_BYTES per GPU (held until the
+ * process ends): n_heads * S * (hd + 2) * 4 bytes must fit, else TF_HIP_ESCRATCH before
+ * any launch. Every call on a GPU shares that GPU's scratch, so calls that overlap on
+ * one GPU (other streams, other host threads) race; each call rewrites every partial it
+ * reads, so nothing needs clearing between calls. */
+#define TF_HIP_ATTN_SCRATCH_BYTES (4u << 20)
+int tf_hip_attn_decode_noalloc(int device, const float* q, const float* k_cache, const float* v_cache,
+                               int32_t n_heads, int32_t n_kv, int32_t hd, int32_t n_pos, int32_t max_seq,
+                               int32_t layout, float* out, void* stream);
 
 /* attn_prefill (attention.cpp:82-111, attention.hpp:29-30): causal GQA attention of seq
  * positions over their own rows. q [seq][n_heads][hd], k and v [seq][n_kv][hd] (already
