@@ -264,11 +264,13 @@ class HipModel:
     def reset(self):
         self._check(self._L.tfh_reset(self._h))
 
-    PATH_GRAPH, PATH_STEP = 0, 1
+    PATH_GRAPH, PATH_STEP, PATH_STREAM = 0, 1, 2
 
     def set_decode_path(self, path: int):
         """PATH_STEP: one persistent kernel per call where the model allows it (default);
-        PATH_GRAPH: the captured per-layer graph, replayed per token."""
+        PATH_GRAPH: the captured per-layer graph, replayed per token; PATH_STREAM: the
+        persistent kernel with loader waves streaming the weights through LDS (Q8_0 models,
+        head size <= 128; others take PATH_STEP's choice)."""
         H = hip_lib()
         rc = H.tf_hip_set_decode_path(self._L.tfh_ctx(self._h), int(path))
         if rc != 0:

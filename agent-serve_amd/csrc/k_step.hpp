@@ -354,9 +354,12 @@ __device__ __forceinline__ int64_t kv_at(int layout, int G, int max_seq, int hd,
 //     l = 0, o = 0 and does not wait for the head block.
 //   Both store the new row at agent scope (a later, split token of the launch reads it from
 //   other XCDs) and wait for the stores before returning, i.e. before their next puts.
-template <int HDM, bool kPart, int NB, class Fetch>
-__device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly, int g, int pos, int p0, int p1,
-                                          float* qkv, float* sm, float* out, Fetch&& fetch) {
+// bar() synchronises the kT threads that run the attention (a workgroup barrier, or the
+// compute waves' barrier of a kernel whose other waves do not take part). a supplies H, G,
+// hd, max_seq, layout and the RoPE tables, ly the layer's K and V cache (kc, vc).
+template <int HDM, bool kPart, int NB, class A, class Ly, class Fetch, class Bar>
+__device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int pos, int p0, int p1,
+                                          float* qkv, float* sm, float* out, Fetch&& fetch, Bar&& bar) {
     constexpr int kTV = (kTile * HDM / 4 + kT - 1) / kT;  // float4 of a K (or V) tile per thread
     constexpr int kPairs = (kMaxRep * HDM + kT - 1) / kT;  // (head, dim) pairs of P.V per thread
     const int hd = a.hd, d2 = hd / 2, hd4 = hd / 4;
@@ -376,7 +379,7 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
             const int d = i % ho;
             out[i] = d == hd ? -INFINITY : 0.0f;
         }
-        __syncthreads();
+        bar();
         return;
     }
     const TF_GLOBAL float* cs = gptr(a.rope_cos + (int64_t)pos * d2);
@@ -436,7 +439,7 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
         st[3 * tid] = -INFINITY;
         st[3 * tid + 1] = 0.0f;
     }
-    __syncthreads();
+    bar();
     const bool stores_row = pos >= p0 && pos < p1;
     if (stores_row) {
         const int64_t o = kv_at(a.layout, a.G, a.max_seq, hd, g, pos);
@@ -468,7 +471,7 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
             }
             if constexpr (NB == 4) load_tile(tile_at(ti + 4), kr, vr);
             if (tn > 0) {
-                __syncthreads();
+                bar();
                 // scores in dot_f32's order (8 lanes, then hsum8; quant.cpp:198-214)
                 for (int i = tid; i < n_rep * tn; i += kT) {
                     const int r = i / tn, j = i % tn;
@@ -489,7 +492,7 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
                     }
                     pr[r * kTile + j] = scale * (((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7])));
                 }
-                __syncthreads();
+                bar();
                 for (int r = wave; r < n_rep; r += kNW) {
                     const float v = lane < tn ? pr[r * kTile + lane] : -INFINITY;
                     const float m_old = st[3 * r];
@@ -504,7 +507,7 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
                         st[3 * r + 2] = alpha;
                     }
                 }
-                __syncthreads();
+                bar();
 #pragma unroll
                 for (int k = 0; k < kPairs; ++k) {
                     const int pi = tid + k * kT;
@@ -515,7 +518,7 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
                         o_acc[k] = o;
                     }
                 }
-                __syncthreads();
+                bar();
             }
     };
     if constexpr (NB == 4) {
@@ -549,30 +552,30 @@ __device__ __forceinline__ void attn_span(const StepArgs& a, const StepLayer& ly
     }
     // the row's stores are done before this workgroup's next puts
     if (stores_row) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    bar();
 }
 
-template <int HDM, class Fetch>
-__device__ __forceinline__ void attn_head(const StepArgs& a, const StepLayer& ly, int g, int pos, int start, float* qkv,
-                                          float* sm, float* out, Fetch&& fetch) {
+template <int HDM, class A, class Ly, class Fetch, class Bar>
+__device__ __forceinline__ void attn_head(const A& a, const Ly& ly, int g, int pos, int start, float* qkv,
+                                          float* sm, float* out, Fetch&& fetch, Bar&& bar) {
     const int n = pos + 1 - start;
     if (n > 2 * kTile)
-        attn_span<HDM, false, 4>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch);
+        attn_span<HDM, false, 4>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch, bar);
     else if (n > kTile)
-        attn_span<HDM, false, 2>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch);
+        attn_span<HDM, false, 2>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch, bar);
     else
-        attn_span<HDM, false, 1>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch);
+        attn_span<HDM, false, 1>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch, bar);
 }
 
-template <int HDM, class Fetch>
-__device__ __forceinline__ void attn_part(const StepArgs& a, const StepLayer& ly, int g, int pos, int p0, int p1,
-                                          float* qkv, float* sm, float* out, Fetch&& fetch) {
+template <int HDM, class A, class Ly, class Fetch, class Bar>
+__device__ __forceinline__ void attn_part(const A& a, const Ly& ly, int g, int pos, int p0, int p1,
+                                          float* qkv, float* sm, float* out, Fetch&& fetch, Bar&& bar) {
     if (p1 - p0 > 2 * kTile)
-        attn_span<HDM, true, 4>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch);
+        attn_span<HDM, true, 4>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch, bar);
     else if (p1 - p0 > kTile)
-        attn_span<HDM, true, 2>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch);
+        attn_span<HDM, true, 2>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch, bar);
     else
-        attn_span<HDM, true, 1>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch);
+        attn_span<HDM, true, 1>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch, bar);
 }
 
 // Floats of LDS the attention scratch needs.
@@ -894,7 +897,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                             gather<kGD, 1>(X(sc.QKV) + par * G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0,
                                            sc.a.ctl);
                             __syncthreads();
-                        });
+                        }, [] { __syncthreads(); });
                         u64* pw_base = pb + (size_t)(g * A + s) * n_rep * ho;
                         for (int i = tid; i < n_rep * ho; i += kT) put(pw_base + i, part[i], E(t, l, 6));
                     }
@@ -942,7 +945,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         gather<kGD, 1>(X(sc.QKV) + par * sc.G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0,
                                        sc.a.ctl);
                         __syncthreads();
-                    });
+                    }, [] { __syncthreads(); });
                     const int nh = sc.n_rep * sc.hd;
                     for (int i = tid; i < nh; i += kT) put(X(sc.ATT) + par * sc.Hd + g * nh + i, att_out[i], E(t, l, 2));
                     auto down_then_input = [&]() {

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "formats.hpp"
+#include "k_stream.hpp"
 #include "tf_internal.hpp"
 
 using namespace tfk;
@@ -78,6 +79,14 @@ struct tf_hip_ctx {
     int split_all_from = -1;                  // tf_hip_set_split_all_from (< 0: step_split_all_from)
     int split_from = kSplitFromDefault;       // tf_hip_set_split_from: spans up to this attend unsplit
     StepLayer* d_layers = nullptr;
+    // streaming step kernel (k_stream.hpp)
+    int stream_state = -1;            // -1 undecided, 0 not used, 1 ready
+    uint8_t* sbuf = nullptr;          // the weights as per-(workgroup, wave) streams
+    uint64_t* d_sbase = nullptr;
+    uint8_t* d_ssteps = nullptr;
+    uint32_t *d_sfirst = nullptr, *d_snl = nullptr, *d_snt = nullptr;
+    SLayer* d_slayers = nullptr;
+    int s_steps_max = 0, s_rs = 0;
     unsigned long long* ex = nullptr;
     size_t ex_words = 0;
     uint32_t epoch = 0;               // exchange epochs consumed (mirrors ctl->epoch)
@@ -440,7 +449,7 @@ int ensure_graph(tf_hip_ctx* c) {
 // attention over workgroups (step_split, step_split_all). Returns 1 (step kernel), 0
 // (graph) or < 0.
 int ensure_step(tf_hip_ctx* c) {
-    if (c->path_opt != TF_HIP_PATH_STEP) return 0;
+    if (c->path_opt == TF_HIP_PATH_GRAPH) return 0;
     if (c->step_state >= 0) return c->step_state;
     int rc = check_ready(c);
     if (rc) return rc;
@@ -509,6 +518,23 @@ int ensure_step(tf_hip_ctx* c) {
     return 1;
 }
 
+// Exchange words carry 32-bit epochs, P per token, and a launch of n tokens uses c->epoch +
+// 1 .. c->epoch + n P. Before that range would pass 2^32 (about 40 M tokens of the 1B shape)
+// the words are cleared and the count starts again at 0, so no word left from before can
+// carry an epoch a reader expects.
+int epoch_guard(tf_hip_ctx* c, int n) {
+    const uint64_t P = 6ull * (uint64_t)c->hp.n_layer + 8ull;
+    if ((uint64_t)c->epoch + (uint64_t)n * P >= 0xFFFFFFFFull) {
+        HIPCHK(c, hipStreamSynchronize(c->st));
+        HIPCHK(c, hipMemsetAsync(c->ex, 0, c->ex_words * 8, c->st));
+        c->epoch = 0;
+        c->ctl_host->epoch = 0;
+        HIPCHK(c, hipMemcpyAsync((char*)c->ctl + offsetof(Ctl, epoch), (char*)c->ctl_host + offsetof(Ctl, epoch),
+                                 sizeof(uint32_t), hipMemcpyHostToDevice, c->st));
+    }
+    return 0;
+}
+
 // n tokens through the persistent step kernel, from position c->pos.
 int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
     const tf_hip_hparams& p = c->hp;
@@ -543,23 +569,152 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
     a.split_from = c->split_from;
     a.split_all_from = c->split_all_from >= 0 ? c->split_all_from
                                               : step_split_all_from(p.n_head, p.n_kv_head, p.head_dim, c->step_split);
-    // Exchange words carry 32-bit epochs, P per token, and the launch uses c->epoch + 1 ..
-    // c->epoch + n P. Before that range would pass 2^32 (about 40 M tokens of the 1B shape)
-    // the words are cleared and the count starts again at 0, so no word left from before
-    // can carry an epoch a reader expects.
-    const uint64_t P = 6ull * (uint64_t)p.n_layer + 8ull;
-    if ((uint64_t)c->epoch + (uint64_t)n * P >= 0xFFFFFFFFull) {
-        HIPCHK(c, hipStreamSynchronize(c->st));
-        HIPCHK(c, hipMemsetAsync(c->ex, 0, c->ex_words * 8, c->st));
-        c->epoch = 0;
-        c->ctl_host->epoch = 0;
-        HIPCHK(c, hipMemcpyAsync((char*)c->ctl + offsetof(Ctl, epoch), (char*)c->ctl_host + offsetof(Ctl, epoch),
-                                 sizeof(uint32_t), hipMemcpyHostToDevice, c->st));
-    }
+    int rc = epoch_guard(c, n);
+    if (rc) return rc;
     const hipError_t e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);
     if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("step kernel launch: ") + hipGetErrorString(e));
-    c->epoch += (uint32_t)((uint64_t)n * P);
+    c->epoch += (uint32_t)((uint64_t)n * (6ull * (uint64_t)p.n_layer + 8ull));
     return 0;
+}
+
+// Decides once, after the step kernel's set-up, whether the streaming kernel runs this
+// model (TF_HIP_PATH_STREAM requested, Q8_0 layers and lm_head, its LDS holds a ring of at
+// least 4 slots per wave, and split attention available where the cache needs it), and
+// repacks the weights into its streams. Returns 1 (streaming kernel), 0 or < 0.
+int ensure_stream(tf_hip_ctx* c) {
+    if (c->path_opt != TF_HIP_PATH_STREAM) return 0;
+    if (c->stream_state >= 0) return c->stream_state;
+    const int s = ensure_step(c);
+    if (s <= 0) return s;
+    c->stream_state = 0;
+    const tf_hip_hparams& p = c->hp;
+    const int V = (int)output_mat(c).N;
+    if (!stream_supported(c->step_tl, c->step_to, p.head_dim, p.n_head / p.n_kv_head, p.n_embd, p.n_ff, c->H))
+        return 0;
+    if (p.max_seq > 512 && !c->step_split_all) return 0;
+    std::vector<uint64_t> sbase;
+    std::vector<uint32_t> sfirst, snl, snt;
+    uint64_t bytes = 0;
+    uint32_t steps_total = 0;
+    int steps_max = 0;
+    stream_plan(p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, V, c->n_wg, sbase, sfirst, snl, snt,
+                &bytes, &steps_total, &steps_max);
+    const int rs = stream_ring_slots(p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, V, c->n_wg,
+                                     steps_max);
+    if (rs < 4) return 0;
+    std::vector<SLayer> tab((size_t)p.n_layer);
+    for (int l = 0; l < p.n_layer; ++l) {
+        auto Vv = [&](int k) { return vec(c, TF_HIP_SLOT_LAYER(l, k)); };
+        SLayer& t = tab[(size_t)l];
+        t.attn_norm = Vv(TF_HIP_LAYER_ATTN_NORM);
+        t.ffn_norm = Vv(TF_HIP_LAYER_FFN_NORM);
+        t.bq = Vv(TF_HIP_LAYER_BQ);
+        t.bk = Vv(TF_HIP_LAYER_BK);
+        t.bv = Vv(TF_HIP_LAYER_BV);
+        t.kc = c->kc + (size_t)l * c->kv_layer;
+        t.vc = c->vc + (size_t)l * c->kv_layer;
+    }
+    const size_t n = sbase.size();
+    int rc = 0;
+    if ((rc = dalloc(c, &c->sbuf, bytes)) || (rc = dalloc(c, &c->d_sbase, n * 8)) ||
+        (rc = dalloc(c, &c->d_ssteps, steps_total)) || (rc = dalloc(c, &c->d_sfirst, n * 4)) ||
+        (rc = dalloc(c, &c->d_snl, n * 4)) || (rc = dalloc(c, &c->d_snt, n * 4)) ||
+        (rc = dalloc(c, &c->d_slayers, tab.size() * sizeof(SLayer))))
+        return rc;
+    HIPCHK(c, hipMemcpy(c->d_sbase, sbase.data(), n * 8, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(c->d_sfirst, sfirst.data(), n * 4, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(c->d_snl, snl.data(), n * 4, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(c->d_snt, snt.data(), n * 4, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(c->d_slayers, tab.data(), tab.size() * sizeof(SLayer), hipMemcpyHostToDevice));
+    HIPCHK(c, launch_stream_pack(c->d_layers, output_mat(c), p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head,
+                                 p.head_dim, V, c->n_wg, c->sbuf, c->d_sbase, c->d_ssteps, c->d_sfirst, c->st));
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    c->s_steps_max = steps_max;
+    c->s_rs = rs;
+    c->stream_state = 1;
+    return 1;
+}
+
+// n tokens through the streaming kernel, from position c->pos.
+int run_stream(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
+    const tf_hip_hparams& p = c->hp;
+    StreamArgs a{};
+    a.layers = c->d_slayers;
+    a.stream = c->sbuf;
+    a.sbase = c->d_sbase;
+    a.ssteps = c->d_ssteps;
+    a.sfirst = c->d_sfirst;
+    a.snl = c->d_snl;
+    a.snt = c->d_snt;
+    a.embd = mat(c, TF_HIP_SLOT_TOKEN_EMBD);
+    a.out_norm = vec(c, TF_HIP_SLOT_OUTPUT_NORM);
+    a.rope_cos = c->rope_cos;
+    a.rope_sin = c->rope_sin;
+    a.ex = c->ex;
+    a.ctl = c->ctl;
+    a.hist = c->hist;
+    a.logits = c->logits;
+    a.taps = c->taps;
+    a.n_layer = p.n_layer;
+    a.D = p.n_embd;
+    a.F = p.n_ff;
+    a.H = p.n_head;
+    a.G = p.n_kv_head;
+    a.hd = p.head_dim;
+    a.V = (int)output_mat(c).N;
+    a.max_seq = p.max_seq;
+    a.layout = p.kv_layout;
+    a.eps = p.rms_eps;
+    a.n_tokens = n;
+    a.greedy = greedy;
+    a.lm_every = lm_every;
+    a.att_start = att_start;
+    a.split_all = c->step_split_all;
+    a.split_from = c->split_from;
+    a.ring_slots = c->s_rs;
+    a.steps_max = c->s_steps_max;
+    int rc = epoch_guard(c, n);
+    if (rc) return rc;
+#ifdef TF_STREAM_PROBE
+    static unsigned long long* dbg = nullptr;
+    if (!dbg) (void)hipMalloc(&dbg, (size_t)c->n_wg * 64 * 8);
+    (void)hipMemsetAsync(dbg, 0, (size_t)c->n_wg * 64 * 8, c->st);
+    a.dbg = dbg;
+#endif
+    const hipError_t e = launch_stream(a, c->n_wg, c->st);
+    if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("stream kernel launch: ") + hipGetErrorString(e));
+#ifdef TF_STREAM_PROBE
+    {
+        std::vector<unsigned long long> h((size_t)c->n_wg * 64);
+        (void)hipMemcpyAsync(h.data(), dbg, h.size() * 8, hipMemcpyDeviceToHost, c->st);
+        (void)hipStreamSynchronize(c->st);
+        double sum[64] = {0};
+        for (int w = 0; w < c->n_wg; ++w)
+            for (int i = 0; i < 64; ++i) sum[i] += (double)h[(size_t)w * 64 + i] / c->n_wg;
+        for (int lw = 0; lw < 2; ++lw)
+            std::fprintf(stderr, "probe n=%d loader %d: rounds %.0f issue %.0f idle %.0f full %.0f cycles %.0f\n", n, lw,
+                         sum[lw * 5], sum[lw * 5 + 1], sum[lw * 5 + 2], sum[lw * 5 + 3], sum[lw * 5 + 4]);
+        for (int wv = 0; wv < 8; ++wv) {
+            const double* q = sum + 12 + wv * 6;
+            std::fprintf(stderr, "probe wave %d: total %.0f units %.0f (ready %.0f) bar %.0f gather %.0f n %.0f\n", wv, q[4],
+                         q[3], q[0], q[1], q[2], q[5]);
+        }
+    }
+#endif
+    c->epoch += (uint32_t)((uint64_t)n * (6ull * (uint64_t)p.n_layer + 8ull));
+    return 0;
+}
+
+// The persistent kernel of this context: 2 streaming, 1 step kernel, 0 none (graph path), < 0 error.
+int ensure_persistent(tf_hip_ctx* c) {
+    const int s = ensure_stream(c);
+    if (s < 0) return s;
+    if (s == 1) return 2;
+    return ensure_step(c);
+}
+
+int run_persistent(tf_hip_ctx* c, int kind, int n, int greedy, int lm_every, int att_start) {
+    return kind == 2 ? run_stream(c, n, greedy, lm_every, att_start) : run_step(c, n, greedy, lm_every, att_start);
 }
 
 // Writes att_start and mode of the device control block.
@@ -850,6 +1005,7 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
             if (rc) return rc;
             c->vecs[(size_t)slot] = d;
             c->step_state = -1;
+            c->stream_state = -1;
             c->pf_state = -1;
         }
         c->vec_len[(size_t)slot] = want;
@@ -898,6 +1054,7 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
     c->allocs.insert(c->allocs.end(), owned.begin(), owned.end());
     c->mats[(size_t)slot] = m;  // a re-upload leaves the old streams allocated until destroy
     c->step_state = -1;         // the step kernel's layer table is rebuilt
+    c->stream_state = -1;       // and the streams repacked
     c->pf_state = -1;
     return 0;
 }
@@ -937,7 +1094,7 @@ int tf_hip_decode(tf_hip_ctx* c, int32_t token, float* logits, int32_t* argmax) 
     if (c->pos >= c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
     if (token < 0 || token >= mat(c, TF_HIP_SLOT_TOKEN_EMBD).N)
         return fail(c, TF_HIP_ERANGE, "token " + std::to_string(token) + " out of range");
-    const int use_step = ensure_step(c);
+    const int use_step = ensure_persistent(c);
     if (use_step < 0) return use_step;
     int rc = use_step ? 0 : ensure_graph(c);
     if (rc) return rc;
@@ -945,7 +1102,7 @@ int tf_hip_decode(tf_hip_ctx* c, int32_t token, float* logits, int32_t* argmax) 
     HIPCHK(c, hipMemcpyAsync(c->hist + c->pos, c->tok_host, 4, hipMemcpyHostToDevice, c->st));
     if ((rc = set_ctl(c, 0, 0))) return rc;
     if (use_step) {
-        if ((rc = run_step(c, 1, 0, 1, 0))) return rc;
+        if ((rc = run_persistent(c, use_step, 1, 0, 1, 0))) return rc;
     } else {
         HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
     }
@@ -967,7 +1124,7 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
             return fail(c, TF_HIP_ERANGE, "token " + std::to_string(tokens[i]) + " out of range");
     const int use_pf = n >= 2 ? ensure_pf(c) : 0;
     if (use_pf < 0) return use_pf;
-    const int use_step = use_pf ? 0 : ensure_step(c);
+    const int use_step = use_pf ? 0 : ensure_persistent(c);
     if (use_step < 0) return use_step;
     int rc = (use_pf || use_step) ? 0 : ensure_graph(c);
     if (rc) return rc;
@@ -978,7 +1135,7 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
     if (use_pf) {
         if ((rc = prefill_mfma(c, n))) return rc;
     } else if (use_step) {
-        if ((rc = run_step(c, n, 0, 0, c->pos))) return rc;
+        if ((rc = run_persistent(c, use_step, n, 0, 0, c->pos))) return rc;
     } else {
         for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
     }
@@ -988,7 +1145,7 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
     if (rc) return rc;
     HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
     c->last_steps = use_pf ? 1 : (use_step ? 1 : n);
-    c->last_name = use_pf ? "prefill_mfma" : (use_step ? "k_step" : "decode_graph");
+    c->last_name = use_pf ? "prefill_mfma" : (use_step == 2 ? "k_stream" : (use_step ? "k_step" : "decode_graph"));
     c->have_logits = true;
     return 0;
 }
@@ -999,7 +1156,7 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     HIPCHK(c, hipSetDevice(c->device));
     if (!c->have_logits) return fail(c, TF_HIP_ESTATE, "generate needs a prior prefill or decode");
     if (n > c->hp.max_seq - c->pos) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
-    const int use_step = ensure_step(c);
+    const int use_step = ensure_persistent(c);
     if (use_step < 0) return use_step;
     int rc = use_step ? 0 : ensure_graph(c);
     if (rc) return rc;
@@ -1007,7 +1164,7 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     if ((rc = set_ctl(c, 0, 1))) return rc;
     HIPCHK(c, hipEventRecord(c->ev0, c->st));
     if (use_step) {
-        if ((rc = run_step(c, n, 1, 1, 0))) return rc;
+        if ((rc = run_persistent(c, use_step, n, 1, 1, 0))) return rc;
     } else {
         for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
     }
@@ -1019,14 +1176,16 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     std::memcpy(out, c->tok_host, (size_t)n * 4);
     HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
     c->last_steps = use_step ? 1 : n;
-    c->last_name = use_step == 1 ? "k_step" : "decode_graph";
+    c->last_name = use_step == 2 ? "k_stream" : (use_step == 1 ? "k_step" : "decode_graph");
     return 0;
 }
 
 int tf_hip_set_decode_path(tf_hip_ctx* c, int32_t path) {
-    if (!c || (path != TF_HIP_PATH_GRAPH && path != TF_HIP_PATH_STEP)) return TF_HIP_EINVAL;
+    if (!c || (path != TF_HIP_PATH_GRAPH && path != TF_HIP_PATH_STEP && path != TF_HIP_PATH_STREAM))
+        return TF_HIP_EINVAL;
     c->path_opt = path;
-    if (path == TF_HIP_PATH_STEP && c->step_state == 0) c->step_state = -1;  // decide again
+    if (path != TF_HIP_PATH_GRAPH && c->step_state == 0) c->step_state = -1;  // decide again
+    if (path == TF_HIP_PATH_STREAM && c->stream_state == 0) c->stream_state = -1;
     return 0;
 }
 
@@ -1092,8 +1251,8 @@ int tf_hip_get_prefill_path(tf_hip_ctx* c) {
 int tf_hip_get_decode_path(tf_hip_ctx* c) {
     if (!c) return TF_HIP_EINVAL;
     HIPCHK(c, hipSetDevice(c->device));
-    const int s = ensure_step(c);
-    return s < 0 ? s : (s ? TF_HIP_PATH_STEP : TF_HIP_PATH_GRAPH);
+    const int s = ensure_persistent(c);
+    return s < 0 ? s : (s == 2 ? TF_HIP_PATH_STREAM : (s ? TF_HIP_PATH_STEP : TF_HIP_PATH_GRAPH));
 }
 
 int tf_hip_get_layer_act(tf_hip_ctx* c, int32_t layer, float* out) {

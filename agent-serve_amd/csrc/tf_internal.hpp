@@ -232,6 +232,23 @@ bool step_supported(int type_layers, int type_out, int hd, int n_rep);
 int step_alt_type(int tl);
 hipError_t launch_step(const StepArgs& a, int type_layers, int type_out, int n_wg, hipStream_t st);
 
+// ---------------------------------------------------------------- streaming step kernel (k_stream.hpp)
+struct StepLayer;
+struct StreamArgs;
+// true when the streaming kernel runs this model: Q8_0 layer matrices and lm_head, head
+// size <= 128, row lengths divisible by 64.
+bool stream_supported(int type_layers, int type_out, int hd, int n_rep, int D, int F, int H);
+// Per-(workgroup, compute wave) streams of one token: byte offsets, first slot in the
+// steps table, slots of the layers and of the whole token; totals and the largest stream.
+int stream_plan(int n_layer, int D, int F, int H, int G, int hd, int V, int nwg, std::vector<uint64_t>& sbase,
+                std::vector<uint32_t>& sfirst, std::vector<uint32_t>& snl, std::vector<uint32_t>& snt,
+                uint64_t* stream_bytes, uint32_t* steps_total, int* steps_max);
+int stream_ring_slots(int n_layer, int D, int F, int H, int G, int hd, int V, int nwg, int steps_max);
+hipError_t launch_stream_pack(const StepLayer* d_layers, const DevMat& out, int n_layer, int D, int F, int H, int G,
+                              int hd, int V, int nwg, uint8_t* stream, const uint64_t* sbase, uint8_t* ssteps,
+                              const uint32_t* sfirst, hipStream_t st);
+hipError_t launch_stream(const StreamArgs& a, int nwg, hipStream_t st);
+
 // Launchers (k_*.hip).
 hipError_t launch_gemv(const GemvArgs& a, int rows_per_wave, hipStream_t st);
 int64_t gemv_groups(int64_t n_rows, int rows_per_wave);

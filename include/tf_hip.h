@@ -123,6 +123,10 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
  * uploaded). */
 #define TF_HIP_PATH_GRAPH 0
 #define TF_HIP_PATH_STEP 1
+/* TF_HIP_PATH_STREAM: the persistent kernel with a loader wave per CU streaming every
+ * weight tile into LDS (Q8_0 models with head size <= 128); models it does not cover take
+ * TF_HIP_PATH_STEP's choice. */
+#define TF_HIP_PATH_STREAM 2
 int tf_hip_set_decode_path(tf_hip_ctx* ctx, int32_t path);
 int tf_hip_get_decode_path(tf_hip_ctx* ctx);
 
