@@ -4,9 +4,6 @@
 
 #include "k_stream.hpp"
 
-#ifndef TF_STREAM_DEPTH
-#define TF_STREAM_DEPTH 3
-#endif
 
 namespace tfk {
 
@@ -16,7 +13,7 @@ namespace {
 
 // LDS layout of the stream kernel (byte offsets), the same on host and device.
 struct SLds {
-    int layers, steps, ctr, xr, xs, qkv, att, part0, part1, ring, total;
+    int layers, steps, xr, xs, qkv, att, part0, part1, ring, total;
 };
 __host__ __device__ inline int al16(int x) { return (x + 15) / 16 * 16; }
 __host__ __device__ inline SLds s_lds(int L, int D, int F, int H, int G, int hd, int nwg, int steps_max, int part_max,
@@ -25,8 +22,7 @@ __host__ __device__ inline SLds s_lds(int L, int D, int F, int H, int G, int hd,
     const int n_rep = H / G;
     o.layers = 0;
     o.steps = al16(L * (int)sizeof(SLayer));
-    o.ctr = al16(o.steps + kSCW * steps_max);
-    o.xr = o.ctr + 256;  // ready[8], released[8], barrier, loader fifo
+    o.xr = al16(o.steps + kSCW * steps_max);
     o.xs = al16(o.xr + 4 * D);
     o.qkv = al16(o.xs + 4 * region_floats(D, F, n_rep, hd, nwg));
     o.att = al16(o.qkv + 4 * (n_rep + 2) * hd);
@@ -36,15 +32,11 @@ __host__ __device__ inline SLds s_lds(int L, int D, int F, int H, int G, int hd,
     o.total = o.ring + kSCW * rs * kSlotBytes;
     return o;
 }
-// counter words at SLds::ctr
-constexpr int kCtrReady = 0, kCtrReleased = 8, kCtrBar = 16;  // u32 index
 
-constexpr int kBarSpin = 1 << 22;
-
-// Optional per-workgroup cycle counts (built with -DTF_STREAM_PROBE only): where the loader
-// and each compute wave spend their time, written to StreamArgs::dbg at the end.
+// Optional time stamps (built with -DTF_STREAM_PROBE only): where each wave spends its
+// time, in 10 ns ticks of s_memrealtime, written to StreamArgs::dbg at the end.
 #ifdef TF_STREAM_PROBE
-#define SP_NOW() __builtin_amdgcn_s_memtime()
+#define SP_NOW() __builtin_amdgcn_s_memrealtime()
 #define SP_ACC(var, t0) (var) += SP_NOW() - (t0)
 #else
 #define SP_NOW() 0ull
@@ -170,6 +162,119 @@ struct SConst {
     int XA, XB, QKV, ATT, HH, DONE, BEST, PART;
 };
 
+// One wave's feed of its ring (wave-uniform state). iss: slots issued over the launch, clr:
+// slots known to be in LDS, cons: slots consumed. The next slot to issue is slot fk of token
+// ftok's stream, fg bytes into it, ring position fw.
+struct Feed {
+    const uint8_t* base;   // the wave's stream
+    const uint8_t* steps;  // lane steps of each slot of a token's stream (LDS)
+    uint32_t ring_o;       // LDS byte offset of the wave's ring
+    int RS, n_tok, nl, nt, depth, lane;
+    bool lm_all;
+    uint32_t iss, clr, cons, fg;
+    int fk, ftok, fw;
+
+    __device__ __forceinline__ int n_cur(int t) const { return (lm_all || t == n_tok - 1) ? nt : nl; }
+    __device__ __forceinline__ void skip_empty() {
+        while (ftok < n_tok && n_cur(ftok) == 0) ++ftok;
+    }
+    __device__ __forceinline__ void issue_one() {
+        const int st = __builtin_amdgcn_readfirstlane((int)steps[fk]);
+        const uint8_t* src = base + fg;
+        const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane((int)(ring_o + (uint32_t)(fw * kSlotBytes)));
+        if (lane < st) dma16(src + 16 * lane, dst);
+        if (4 * lane < st) dma4(src + 16 * st + 4 * lane, dst + kSlotQ);
+        ++iss;
+        fw = fw + 1 == RS ? 0 : fw + 1;
+        fg += (uint32_t)s_gbytes(st);
+        if (++fk >= n_cur(ftok)) {
+            fk = 0;
+            fg = 0;
+            ++ftok;
+            skip_empty();
+        }
+    }
+    // issue while the ring has room and fewer than p slots are in flight
+    __device__ __forceinline__ void topup(int p) {
+        while (ftok < n_tok && (int)(iss - cons) < RS && (int)(iss - clr) < p) issue_one();
+    }
+    // slots cons .. n - 1 in LDS
+    __device__ __forceinline__ void need(uint32_t n) {
+        while (iss < n) issue_one();
+        if (n > clr) {
+            wait_vm_even(2 * (int)(iss - n));
+            clr = n;
+        }
+    }
+    __device__ __forceinline__ void top() { topup(depth); }
+    // every load issued so far is complete
+    __device__ __forceinline__ void pass() {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        clr = iss;
+    }
+};
+
+// gather() of k_step.hpp with the feed kept going: top() runs before the first round of
+// loads and before every re-poll (it issues the wave's next slots, ring and depth
+// permitting), pass() after each round (every load the wave issued before the round is
+// then complete). The re-poll loop runs while any lane of the wave has a word pending, so
+// top() always runs with the whole wave.
+template <int NA, int NB>
+__device__ __forceinline__ void fgather(u64* pa, int na, uint32_t ea, float* da, u64* pb, int nb, uint32_t eb,
+                                        Ctl* ctl, Feed& f) {
+    const int tid = threadIdx.x;
+    f.top();
+    u64 wa[NA], wb[NB];
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+        if (tid + i * kT < na) wa[i] = get(pa + tid + i * kT);
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+        if (tid + i * kT < nb) wb[i] = get(pb + tid + i * kT);
+    uint32_t pend = 0;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int j = tid + i * kT;
+        if (j < na) {
+            if ((uint32_t)(wa[i] >> 32) == ea)
+                da[j] = __uint_as_float((uint32_t)wa[i]);
+            else
+                pend |= 1u << i;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+        if (tid + i * kT < nb && (uint32_t)(wb[i] >> 32) != eb) pend |= 1u << (NA + i);
+    f.pass();
+    for (int spin = 0; __builtin_amdgcn_ballot_w64(pend != 0) != 0; ++spin) {
+        if (spin >= kSpinLimit || ((spin & 1023) == 1023 && get_err(ctl))) {
+            set_err(ctl, kErrTimeout);
+            break;
+        }
+        f.top();
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            if (pend & (1u << i)) {
+                const int j = tid + i * kT;
+                const u64 w = get(pa + j);
+                if ((uint32_t)(w >> 32) == ea) {
+                    da[j] = __uint_as_float((uint32_t)w);
+                    pend &= ~(1u << i);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (pend & (1u << (NA + i))) {
+                const u64 w = get(pb + tid + i * kT);
+                if ((uint32_t)(w >> 32) == eb) pend &= ~(1u << (NA + i));
+            }
+        }
+        f.pass();
+    }
+}
+
 template <int HDM>
 __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) {
     using F8 = Fmt<TF_HIP_TYPE_Q8_0>;
@@ -215,7 +320,6 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
     const SLds& LO = sc.lds;
     SLayer* lay = (SLayer*)(smem + LO.layers);
     uint8_t* steps_tab = smem + LO.steps;
-    uint32_t* ctr = (uint32_t*)(smem + LO.ctr);
     {
         const uint64_t* src = (const uint64_t*)args.layers;
         uint64_t* dst = (uint64_t*)lay;
@@ -227,200 +331,54 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
             const int n = (int)args.snt[cw];
             for (int i = tid; i < n; i += kSThreads) steps_tab[w * args.steps_max + i] = s[i];
         }
-        if (tid < 64) ctr[tid] = 0;
     }
     __syncthreads();
 
-    // ============================================================ loader waves
-    if (wave >= kSCW) {
-        // Loader wave lw feeds the rings of compute waves 4 lw .. 4 lw + 3 (its streams j =
-        // 0..3, per-stream state in scalar registers). Each round issues up to two slots per
-        // stream (ring space permitting, from the released counts read at the round's start)
-        // as direct global->LDS loads, then waits until only this round's loads are in flight
-        // -- the previous round's slots are in LDS -- and publishes those. The loads are inline
-        // asm, so the compiler adds no waits of its own for them.
-        constexpr int NS = kSCW / kSLW;
-        constexpr int NPR = 3;  // slots per stream per round
-        constexpr int DEPTH = TF_STREAM_DEPTH;  // rounds in flight
-        static_assert(2 * NPR * NS * (DEPTH - 1) <= 62, "vmcnt counts at most 63 loads");
-        const int lw = wave - kSCW;
-        // the loaders' few instructions go first when they share a SIMD with compute waves
-        __builtin_amdgcn_s_setprio(3);
-        const StreamArgs& a = sc.a;
-        const int RS = __builtin_amdgcn_readfirstlane(sc.RS);
-        const int n_tok = __builtin_amdgcn_readfirstlane(a.n_tokens);
-        const int smax = __builtin_amdgcn_readfirstlane(a.steps_max);
-        const bool lm_all = __builtin_amdgcn_readfirstlane(a.lm_every) != 0;
-        const uint32_t ring_o = __builtin_amdgcn_readfirstlane(lds_off(smem + LO.ring));
-        uint32_t* const ready = ctr + kCtrReady;
-        const uint32_t* const released = ctr + kCtrReleased;
-        Ctl* const ctl = a.ctl;
-        uint32_t iss[NS], pub[NS], prev[NS], k[NS], g[NS], nl[NS], nt[NS];
-        int ridx[NS], tok[NS];
-        const uint8_t* base[NS];
-#pragma unroll
-        for (int j = 0; j < NS; ++j) {
-            const int cw = wg * kSCW + lw * NS + j;
-            base[j] = (const uint8_t*)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(
-                                            (int)(((uint64_t)(a.stream + a.sbase[cw])) >> 32))
-                                        << 32) |
-                                       (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint64_t)(a.stream + a.sbase[cw])));
-            nl[j] = __builtin_amdgcn_readfirstlane(a.snl[cw]);
-            nt[j] = __builtin_amdgcn_readfirstlane(a.snt[cw]);
-            iss[j] = pub[j] = prev[j] = k[j] = g[j] = 0;
-            ridx[j] = 0;
-            tok[j] = 0;
-            while (tok[j] < n_tok && ((lm_all || tok[j] == n_tok - 1) ? nt[j] : nl[j]) == 0) ++tok[j];
-        }
-        int idle = 0;
-        uint32_t prev_loads = 0, prev_loads2 = 0;
-#ifdef TF_STREAM_PROBE
-        uint64_t pl_rounds = 0, pl_issue = 0, pl_idle = 0, pl_full = 0;
-        const uint64_t pl_t0 = SP_NOW();
-#endif
-        while (true) {
-            // released counts of the wave's streams: lane j reads stream j's (one LDS access)
-            const uint32_t rel_v = __hip_atomic_load(released + lw * NS + (lane & (NS - 1)), __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_WORKGROUP);
-            // lane steps of each stream's next NPR slots: lane NPR j + r reads stream j's slot
-            // k + r (or, past the token's end, the next token's from slot 0)
-            int idx_v = 0;
-#pragma unroll
-            for (int j = 0; j < NS; ++j) {
-                const int w = lw * NS + j;
-                const int n_cur = (int)((lm_all || tok[j] == n_tok - 1) ? nt[j] : nl[j]);
-                const int n_next = (int)((lm_all || tok[j] + 1 == n_tok - 1) ? nt[j] : nl[j]);
-#pragma unroll
-                for (int r = 0; r < NPR; ++r) {
-                    int kr = (int)k[j] + r;
-                    if (kr >= n_cur) kr -= n_cur;
-                    if (n_next > 0 && kr >= n_next) kr = n_next - 1;  // past the next token too: not issued
-                    idx_v = lane == NPR * j + r ? w * smax + kr : idx_v;
-                }
-            }
-            const int steps_v = steps_tab[idx_v];
-            uint32_t n_loads = 0;
-            bool pending = false;
-#pragma unroll
-            for (int j = 0; j < NS; ++j) {
-                const uint32_t rel = (uint32_t)__builtin_amdgcn_readlane((int)rel_v, j);
-                const int w = lw * NS + j;
-                uint32_t issued_now = 0;
-#pragma unroll
-                for (int rep = 0; rep < NPR; ++rep) {
-                    if (tok[j] < n_tok) {
-                        pending = true;
-                        if (iss[j] - rel < (uint32_t)RS) {
-                            const int steps = __builtin_amdgcn_readlane(steps_v, NPR * j + rep);
-                            const uint8_t* src = base[j] + g[j];
-                            const uint32_t dst = ring_o + (uint32_t)((w * RS + ridx[j]) * kSlotBytes);
-                            if (lane < steps) dma16(src + 16 * lane, dst);
-                            if (4 * lane < steps) dma4(src + 16 * steps + 4 * lane, dst + kSlotQ);
-                            n_loads += 2;
-                            ++issued_now;
-                            ++iss[j];
-                            ridx[j] = ridx[j] + 1 == RS ? 0 : ridx[j] + 1;
-                            g[j] += (uint32_t)s_gbytes(steps);
-                            ++k[j];
-                            while (tok[j] < n_tok && k[j] >= ((lm_all || tok[j] == n_tok - 1) ? nt[j] : nl[j])) {
-                                ++tok[j];
-                                k[j] = 0;
-                                g[j] = 0;
-                            }
-                        }
-                    }
-                }
-                prev[j] = (prev[j] << 8) | issued_now;  // byte i: the slots issued i rounds ago
-            }
-            // the slots issued DEPTH - 1 rounds ago are in LDS once only the later rounds'
-            // loads remain
-            wait_vm_even((int)(n_loads + (DEPTH > 2 ? prev_loads : 0)));
-            bool published = false;
-#pragma unroll
-            for (int j = 0; j < NS; ++j) {
-                const uint32_t done_prev = (prev[j] >> (8 * (DEPTH - 1))) & 0xFFu;
-                if (done_prev) {
-                    pub[j] += done_prev;
-                    if (lane == 0)
-                        __hip_atomic_store(ready + lw * NS + j, pub[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    published = true;
-                }
-                prev[j] &= (1u << (8 * (DEPTH - 1))) - 1u;
-            }
-#ifdef TF_STREAM_PROBE
-            ++pl_rounds;
-            pl_issue += n_loads ? 1 : 0;
-            pl_idle += (!n_loads && !published) ? 1 : 0;
-            pl_full += n_loads == 2 * NPR * NS ? 1 : 0;
-#endif
-            if (!pending && n_loads == 0 && prev_loads == 0 && prev_loads2 == 0) break;
-            if (n_loads == 0 && !published) {
-                // every ring full: wait for the compute waves
-                if (++idle > kBarSpin || ((idle & 1023) == 1023 && get_err(ctl))) {
-                    set_err(ctl, kErrTimeout);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            } else {
-                idle = 0;
-            }
-            prev_loads2 = DEPTH > 2 ? prev_loads : 0;
-            prev_loads = n_loads;
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#ifdef TF_STREAM_PROBE
-        if (lane == 0 && a.dbg) {
-            unsigned long long* o = a.dbg + (size_t)wg * 64 + lw * 5;
-            o[0] = pl_rounds;
-            o[1] = pl_issue;
-            o[2] = pl_idle;
-            o[3] = pl_full;
-            o[4] = SP_NOW() - pl_t0;
-        }
-#endif
-        return;
-    }
+    // Barrier over the workgroup's LDS accesses only: the feed's loads stay in flight.
+    auto bar = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
-    // ============================================================ compute waves
+    // ------------------------------------------------------------ the feed
+    const StreamArgs& A0 = sc.a;
+    const int RS = __builtin_amdgcn_readfirstlane(sc.RS);
+    const int depth = __builtin_amdgcn_readfirstlane(A0.depth);
+    const int depth_lm = __builtin_amdgcn_readfirstlane(A0.depth_lm);
+    Feed fd;
+    {
+        const int cwi = wg * kSCW + wave;
+        const uint64_t fb_u = (uint64_t)(args.stream + args.sbase[cwi]);
+        fd.base = (const uint8_t*)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(fb_u >> 32)) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)fb_u));
+        fd.steps = steps_tab + wave * args.steps_max;
+        fd.ring_o = __builtin_amdgcn_readfirstlane((int)lds_off(smem + LO.ring + (size_t)wave * RS * kSlotBytes));
+        fd.RS = RS;
+        fd.n_tok = __builtin_amdgcn_readfirstlane(args.n_tokens);
+        fd.nl = __builtin_amdgcn_readfirstlane((int)args.snl[cwi]);
+        fd.nt = __builtin_amdgcn_readfirstlane((int)args.snt[cwi]);
+        fd.depth = depth;
+        fd.lane = lane;
+        fd.lm_all = __builtin_amdgcn_readfirstlane(args.lm_every) != 0;
+        fd.iss = fd.clr = fd.cons = fd.fg = 0;
+        fd.fk = fd.ftok = fd.fw = 0;
+        fd.skip_empty();
+    }
+    const unsigned char* const ring_w = smem + LO.ring + (size_t)wave * RS * kSlotBytes;
+    int cw_r = 0;  // ring position of the next slot to consume
+
     float* xr = (float*)(smem + LO.xr);
     float* xs = (float*)(smem + LO.xs);
     float* part0 = (float*)(smem + LO.part0);
     float* part1 = (float*)(smem + LO.part1);
-    const unsigned char* ring_w = smem + LO.ring + (size_t)wave * sc.RS * kSlotBytes;
-    uint32_t* ready_w = ctr + kCtrReady + wave;
-    uint32_t* released_w = ctr + kCtrReleased + wave;
-    uint32_t* bar_ctr = ctr + kCtrBar;
-    uint32_t bar_gen = 0;
-    uint32_t cons = 0;  // slots this wave has consumed over the launch
-    int ridx = 0;       // their ring position: cons mod RS
-    const int ct = tid;  // compute thread index, < 512
+    const int ct = tid;
 
-    uint64_t pc_ready = 0, pc_bar = 0, pc_gather = 0, pc_units = 0, pc_attn = 0, pc_n = 0;
+    uint64_t pc_feed = 0, pc_gather = 0, pc_units = 0, pc_attn = 0, pc_lm = 0;
     const uint64_t pc_t0 = SP_NOW();
     (void)pc_t0;
-    (void)pc_n;
-    auto cbar = [&]() {
-        const uint64_t tb = SP_NOW();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        bar_gen += kSCW;
-        if (lane == 0) __hip_atomic_fetch_add(bar_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        for (int spin = 0; __hip_atomic_load(bar_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < bar_gen;
-             ++spin) {
-            if (spin > kBarSpin || ((spin & 1023) == 1023 && get_err(sc.a.ctl))) {
-                set_err(sc.a.ctl, kErrTimeout);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        asm volatile("" ::: "memory");
-        SP_ACC(pc_bar, tb);
-    };
     auto E = [&](int t, int l, int p) -> uint32_t { return sc.e0 + (uint32_t)(t * sc.P + 6 * l + p); };
     auto X = [&](int off) -> u64* { return sc.a.ex + off; };
 
-    // xs = rmsnorm(xr) (layers.cpp:7-12) or a copy, as stage() of k_step.hpp
+    // xs = rmsnorm(src) (layers.cpp:7-12) or a copy, as stage() of k_step.hpp
     auto sstage = [&](const float* src, int K, bool norm, const float (&wr)[NWR], float eps) {
-        cbar();
+        bar();
         if (norm) {
             double ss = 0;
             for (int j = ct; j < K; j += kT) {
@@ -429,7 +387,7 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
             }
             ss = wave_sum_d(ss);
             if (lane == 0) red[wave] = ss;
-            cbar();
+            bar();
             ss = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
             const float inv = 1.0f / sqrtf((float)(ss / K) + eps);
 #pragma unroll
@@ -438,20 +396,15 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                 if (j < K) xs[j] = (src[j] * inv) * wr[i];
             }
         }
-        cbar();
+        bar();
     };
 
     // The units of phase p this wave owns, read from its ring: partial dot products of
     // each unit's row tile with xs, summed over the wave's consecutive tiles of a row and
     // written at the run's last unit (0 at the others), so a row's value is the fixed-order
-    // sum of its T entries. Releases each slot as soon as it is read. The phase's shape is
-    // copied into scalar registers first (read through the LDS constants it would be
-    // reloaded after every ordering fence), and the last ready count seen is kept, so a
-    // unit whose slots are known to be in LDS reads no counter.
-    const int RSr = __builtin_amdgcn_readfirstlane(sc.RS);
+    // sum of its T entries. The slot's ring position is refilled once its bytes are read.
     const int nwg_r = __builtin_amdgcn_readfirstlane(sc.nwg);
-    uint32_t rdy = 0;
-    auto run_units_t = [&](auto spu_c, const SPhase& pp) __attribute__((always_inline)) {
+    auto run_units_t = [&](auto spu_c, const SPhase& pp, int p_depth) __attribute__((always_inline)) {
         constexpr int SPU = decltype(spu_c)::value;
         const int T = __builtin_amdgcn_readfirstlane(pp.T);
         const int tail = __builtin_amdgcn_readfirstlane(pp.tail);
@@ -464,28 +417,15 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
         int j = u0 % T;  // tile of unit u, advanced below
         for (int u = u0; u < u1; ++u) {
             const int steps = j == T - 1 ? tail : 64;
-            const uint32_t need = cons + (uint32_t)SPU;
-            if (need > rdy) {
-                const uint64_t tr = SP_NOW();
-                rdy = __hip_atomic_load(ready_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                for (int spin = 0; rdy < need; ++spin) {
-                    if (spin > kBarSpin || ((spin & 1023) == 1023 && get_err(sc.a.ctl))) {
-                        set_err(sc.a.ctl, kErrTimeout);
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                    rdy = __hip_atomic_load(ready_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
-                SP_ACC(pc_ready, tr);
+            {
+                const uint64_t tf = SP_NOW();
+                fd.need(fd.cons + (uint32_t)SPU);
+                SP_ACC(pc_feed, tf);
             }
-            asm volatile("" ::: "memory");
-#ifdef TF_STREAM_PROBE
-            ++pc_n;
-#endif
             const bool act = lane < steps;
             const int ls = act ? lane : 0;
-            const int ridx1 = ridx + 1 == RSr ? 0 : ridx + 1;
-            const unsigned char* s0 = ring_w + ridx * kSlotBytes;
+            const int ridx1 = cw_r + 1 == RS ? 0 : cw_r + 1;
+            const unsigned char* s0 = ring_w + cw_r * kSlotBytes;
             typename F8::Raw w0;
             w0.q = *(const uint4*)(s0 + 16 * ls);
             w0.d = *(const uint16_t*)(s0 + kSlotQ + 2 * (ls >> 1));
@@ -499,11 +439,11 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
             const float d0 = F8::dot(w0, xj, nullptr, ls);
             float d1 = 0.0f;
             if constexpr (SPU == 2) d1 = F8::dot(w1, xj, nullptr, ls);
-            // the slot's bytes are in registers: release it
+            // the slots' bytes are in registers before their ring positions are refilled
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            cons = need;
-            ridx = SPU == 2 ? (ridx1 + 1 == RSr ? 0 : ridx1 + 1) : ridx1;
-            if (lane == 0) __hip_atomic_store(released_w, cons, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            fd.cons += (uint32_t)SPU;
+            cw_r = SPU == 2 ? (ridx1 + 1 == RS ? 0 : ridx1 + 1) : ridx1;
+            fd.topup(p_depth);
             a0 += act ? d0 : 0.0f;
             if constexpr (SPU == 2) a1 += act ? d1 : 0.0f;
             const bool end = j == T - 1 || u == u1 - 1;
@@ -521,11 +461,11 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
         }
         SP_ACC(pc_units, tu);
     };
-    auto run_units = [&](const SPhase& p) {
+    auto run_units = [&](const SPhase& p, int p_depth) {
         if (p.spu == 2)
-            run_units_t(std::integral_constant<int, 2>{}, p);
+            run_units_t(std::integral_constant<int, 2>{}, p, p_depth);
         else
-            run_units_t(std::integral_constant<int, 1>{}, p);
+            run_units_t(std::integral_constant<int, 1>{}, p, p_depth);
     };
     // value of row rl (workgroup-local) of phase p after run_units and a barrier
     auto row_sum = [&](const SPhase& p, const float* part, int rl) -> float {
@@ -564,10 +504,10 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                     if (t > 0) {
                         if (a.greedy) {
                             float* kb = xs;
-                            cbar();
-                            gather<kGW, 1>(X(sc.BEST) + ((t - 1) & 1) * 2 * sc.nwg, 2 * sc.nwg,
-                                           E(t - 1, a.n_layer, 6), kb, nullptr, 0, 0, a.ctl);
-                            cbar();
+                            bar();
+                            fgather<kGW, 1>(X(sc.BEST) + ((t - 1) & 1) * 2 * sc.nwg, 2 * sc.nwg,
+                                            E(t - 1, a.n_layer, 6), kb, nullptr, 0, 0, a.ctl, fd);
+                            bar();
                             if (ct == 0) {
                                 u64 b = 0;
                                 for (int i = 0; i < sc.nwg; ++i) {
@@ -577,11 +517,11 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                                 }
                                 wbest[0] = b;
                             }
-                            cbar();
+                            bar();
                             tok = key_to_index(wbest[0]);
                         } else {
-                            gather<1, kGW>(nullptr, 0, 0, nullptr, X(sc.DONE) + ((a.n_layer - 1) & 1) * sc.nwg, sc.nwg,
-                                           E(t - 1, a.n_layer - 1, 5), a.ctl);
+                            fgather<1, kGW>(nullptr, 0, 0, nullptr, X(sc.DONE) + ((a.n_layer - 1) & 1) * sc.nwg, sc.nwg,
+                                            E(t - 1, a.n_layer - 1, 5), a.ctl, fd);
                             tok = *gptr(a.hist + pos);
                         }
                     } else {
@@ -595,7 +535,7 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                         *gptr(a.hist + pos) = tok;
                         *gptr(&a.ctl->last_token) = tok;
                     }
-                    cbar();  // xs (the key scratch) is read before the embedding row lands in xr
+                    bar();  // xs (the key scratch) is read before the embedding row lands in xr
                     const RowPtr rp = F8::row(a.embd, tok);
                     for (int s = ct; s < D / F8::E; s += kT) {
                         float v[F8::E];
@@ -604,16 +544,14 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                         for (int i = 0; i < F8::E; ++i) xr[s * F8::E + i] = v[i];
                     }
                 } else {
-                    {
-                        const uint64_t tg = SP_NOW();
-                        gather<kGD, kGW>(X(sc.XA) + ((l - 1) & 1) * D, D, E(t, l - 1, 5), xr,
-                                         X(sc.DONE) + ((l - 1) & 1) * sc.nwg, sc.nwg, E(t, l - 1, 5), a.ctl);
-                        SP_ACC(pc_gather, tg);
-                    }
+                    const uint64_t tg = SP_NOW();
+                    fgather<kGD, kGW>(X(sc.XA) + ((l - 1) & 1) * D, D, E(t, l - 1, 5), xr,
+                                      X(sc.DONE) + ((l - 1) & 1) * sc.nwg, sc.nwg, E(t, l - 1, 5), a.ctl, fd);
+                    SP_ACC(pc_gather, tg);
                 }
                 sstage(xr, D, true, wr, a.eps);
-                run_units(p);
-                cbar();
+                run_units(p, depth);
+                bar();
                 if (ct < rows) {
                     const int row = r0 + ct;
                     const float v = row_sum(p, part0, ct) + bias;
@@ -641,11 +579,11 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                     // kv head g on workgroup nwg - G + g
                     if (wg >= sc.nwg - G) {
                         const int g = wg - (sc.nwg - G);
-                        cbar();  // xs is free: every wave is past its QKV units
+                        bar();  // xs is free: every wave is past its QKV units
                         attn_head<HDM>(a, ly, g, pos, a.att_start, qkv, xs, aout, [&]() {
                             gather<kGD, 1>(X(sc.QKV) + par * G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0, a.ctl);
-                            cbar();
-                        }, cbar);
+                            bar();
+                        }, bar);
                         const int nh = n_rep * hd;
                         for (int i = ct; i < nh; i += kT) put(X(sc.ATT) + par * sc.Hd + g * nh + i, aout[i], E(t, l, 2));
                     }
@@ -654,7 +592,7 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                     // slice of hd / parts) merge of the splits' partials (flash-decoding)
                     const int A = sc.A_all, parts = sc.parts_all, ho = hd + 2;
                     u64* pb = X(sc.PART) + par * sc.PW;
-                    cbar();
+                    bar();
                     if (wg < G * A) {
                         const int g = wg % G, s = wg / G;
                         const int start = a.att_start;
@@ -662,8 +600,8 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                         const int p0 = start + s * chunk, p1 = min(pos + 1, p0 + chunk);
                         attn_part<HDM>(a, ly, g, pos, p0, p1, qkv, xs, aout, [&]() {
                             gather<kGD, 1>(X(sc.QKV) + par * G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0, a.ctl);
-                            cbar();
-                        }, cbar);
+                            bar();
+                        }, bar);
                         u64* pw_base = pb + (size_t)(g * A + s) * n_rep * ho;
                         for (int i = ct; i < n_rep * ho; i += kT) put(pw_base + i, aout[i], E(t, l, 6));
                     }
@@ -672,12 +610,12 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                         const int h = wg / parts, d0 = (wg % parts) * sz;
                         const int g = h / n_rep, r = h % n_rep, w = sz + 2;
                         float* buf = xs;
-                        cbar();
+                        bar();
                         gather_idx<3>(pb, [&](int j) {
                             const int s = j / w, k = j % w;
                             return (size_t)((g * A + s) * n_rep + r) * ho + (k < sz ? d0 + k : hd + k - sz);
                         }, A * w, E(t, l, 6), buf, a.ctl);
-                        cbar();
+                        bar();
                         for (int k = wave; k < sz; k += kSCW) {
                             float m = -INFINITY;
                             for (int s = lane; s < A; s += kWave) m = fmaxf(m, buf[s * w + sz]);
@@ -700,15 +638,15 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
             {
                 const SPhase& p = sc.plan.ph[SP_WO];
                 float no_w[NWR];
-                cbar();  // the attention's LDS use (xs) is over
+                bar();  // the attention's LDS use (xs) is over
                 {
                     const uint64_t tg = SP_NOW();
-                    gather<kGD, 1>(X(sc.ATT) + par * sc.Hd, sc.Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl);
+                    fgather<kGD, 1>(X(sc.ATT) + par * sc.Hd, sc.Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl, fd);
                     SP_ACC(pc_gather, tg);
                 }
                 sstage(xs, sc.Hd, false, no_w, 0.0f);
-                run_units(p);
-                cbar();
+                run_units(p, depth);
+                bar();
                 const int r0 = split_lo(p.n_rows, wg, sc.nwg), rows = split_lo(p.n_rows, wg + 1, sc.nwg) - r0;
                 if (ct < rows) {
                     const int row = r0 + ct;
@@ -720,15 +658,15 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                 const SPhase& p = sc.plan.ph[SP_GU];
                 float wr[NWR];
                 load_norm(ly.ffn_norm, D, wr);
-                cbar();  // every wave has read xr's residual for its wo rows
+                bar();  // every wave has read xr's residual for its wo rows
                 {
                     const uint64_t tg = SP_NOW();
-                    gather<kGD, 1>(X(sc.XB) + par * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl);
+                    fgather<kGD, 1>(X(sc.XB) + par * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl, fd);
                     SP_ACC(pc_gather, tg);
                 }
                 sstage(xr, D, true, wr, sc.a.eps);
-                run_units(p);
-                cbar();
+                run_units(p, depth);
+                bar();
                 const int r0 = split_lo(p.n_rows, wg, sc.nwg), rows = split_lo(p.n_rows, wg + 1, sc.nwg) - r0;
                 for (int i = ct; i < rows; i += kT) {
                     const float g = row_sum(p, part0, i), u = row_sum(p, part1, i);
@@ -739,15 +677,15 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
             {
                 const SPhase& p = sc.plan.ph[SP_DOWN];
                 float no_w[NWR];
-                cbar();
+                bar();
                 {
                     const uint64_t tg = SP_NOW();
-                    gather<kGF, 1>(X(sc.HH) + par * sc.a.F, sc.a.F, E(t, l, 4), xs, nullptr, 0, 0, sc.a.ctl);
+                    fgather<kGF, 1>(X(sc.HH) + par * sc.a.F, sc.a.F, E(t, l, 4), xs, nullptr, 0, 0, sc.a.ctl, fd);
                     SP_ACC(pc_gather, tg);
                 }
                 sstage(xs, sc.a.F, false, no_w, 0.0f);
-                run_units(p);
-                cbar();
+                run_units(p, depth);
+                bar();
                 const int r0 = split_lo(p.n_rows, wg, sc.nwg), rows = split_lo(p.n_rows, wg + 1, sc.nwg) - r0;
                 if (ct < rows) {
                     const int row = r0 + ct;
@@ -755,24 +693,25 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                     put(X(sc.XA) + par * D + row, nv, E(t, l, 5));
                     if (last && sc.a.taps) *gptr(sc.a.taps + (size_t)l * D + row) = nv;
                 }
-                cbar();
+                bar();
                 if (ct == 0) put(X(sc.DONE) + par * sc.nwg + wg, 0.0f, E(t, l, 5));
             }
         }
         // ---- output_norm + lm_head + greedy argmax
         if (sc.a.lm_every || last) {
+            const uint64_t tl = SP_NOW();
             const SPhase& p = sc.plan.ph[SP_LM];
             const int D = sc.a.D, Lm = sc.a.n_layer - 1;
             float wr[NWR];
             load_norm(sc.a.out_norm, D, wr);
-            cbar();
-            gather<kGD, kGW>(X(sc.XA) + (Lm & 1) * D, D, E(t, Lm, 5), xr, X(sc.DONE) + (Lm & 1) * sc.nwg, sc.nwg,
-                             E(t, Lm, 5), sc.a.ctl);
+            bar();
+            fgather<kGD, kGW>(X(sc.XA) + (Lm & 1) * D, D, E(t, Lm, 5), xr, X(sc.DONE) + (Lm & 1) * sc.nwg, sc.nwg,
+                              E(t, Lm, 5), sc.a.ctl, fd);
             sstage(xr, D, true, wr, sc.a.eps);
             if (last && sc.a.taps && wg == 0)
                 for (int j = ct; j < D; j += kT) *gptr(sc.a.taps + (size_t)sc.a.n_layer * D + j) = xs[j];
-            run_units(p);
-            cbar();
+            run_units(p, depth_lm);
+            bar();
             const int r0 = split_lo(p.n_rows, wg, sc.nwg), rows = split_lo(p.n_rows, wg + 1, sc.nwg) - r0;
             u64 best = 0;
             for (int i = ct; i < rows; i += kT) {
@@ -783,7 +722,7 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
             }
             best = wave_max_u64(best);
             if (lane == 0) wbest[wave] = best;
-            cbar();
+            bar();
             if (ct == 0) {
                 u64 b = wbest[0];
                 for (int i = 1; i < kSCW; ++i) b = wbest[i] > b ? wbest[i] : b;
@@ -791,27 +730,31 @@ __global__ __launch_bounds__(kSThreads, 1) void k_stream(const StreamArgs args) 
                 put(bw, __uint_as_float((uint32_t)(b >> 32)), E(t, sc.a.n_layer, 6));
                 put(bw + 1, __uint_as_float((uint32_t)b), E(t, sc.a.n_layer, 6));
             }
+            SP_ACC(pc_lm, tl);
         }
     }
+    // no load of the feed outlives the workgroup
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #ifdef TF_STREAM_PROBE
     if (lane == 0 && sc.a.dbg) {
-        unsigned long long* o = sc.a.dbg + (size_t)wg * 64 + 12 + wave * 6;
-        o[0] = pc_ready;
-        o[1] = pc_bar;
-        o[2] = pc_gather;
-        o[3] = pc_units;
-        o[4] = SP_NOW() - pc_t0;
-        o[5] = pc_n;
+        unsigned long long* o = sc.a.dbg + (size_t)wg * 64 + wave * 8;
+        o[0] = pc_feed;
+        o[1] = pc_gather;
+        o[2] = pc_units;
+        o[3] = pc_attn;
+        o[4] = pc_lm;
+        o[5] = SP_NOW() - pc_t0;
+        o[6] = fd.iss;
     }
 #endif
     // workgroup 0 folds the last token's keys and advances the control block
     if (wg == 0) {
         const int t = n_tokens - 1;
         float* kb = xs;
-        cbar();
+        bar();
         gather<kGW, 1>(X(sc.BEST) + (t & 1) * 2 * sc.nwg, 2 * sc.nwg, E(t, sc.a.n_layer, 6), kb, nullptr, 0, 0,
                        sc.a.ctl);
-        cbar();
+        bar();
         if (ct == 0) {
             u64 b = 0;
             for (int i = 0; i < sc.nwg; ++i) {

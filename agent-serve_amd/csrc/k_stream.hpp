@@ -1,36 +1,31 @@
 // Streaming persistent decode step for Q8_0 models: the token loop of k_step.hpp
 // (Model::decode, model.cpp:197-208, and the per-token layers of Model::prefill,
 // model.cpp:144-195) with the same phases, exchange protocol and per-element arithmetic,
-// and the weights delivered by a wave of their own.
+// and the weights fed through LDS at a bounded depth.
 //
-// A workgroup is 10 waves on one CU: 8 compute waves and 2 loader waves. The weights are
-// repacked once (k_stream_pack) into one contiguous byte stream per (workgroup, compute
-// wave): the slots that wave will consume in one token, in order -- its share of every
-// layer's QKV, wo, gate/up and down rows, then of the lm_head. The loader waves copy the 8
-// streams of their workgroup (4 each) into 8 LDS rings with direct global->LDS loads, two
-// rounds of at most two slots per stream in flight, and keep doing so whatever the compute
-// waves are waiting for: the
-// compute waves never issue a weight load, so their exchange polls never queue behind
-// one (a wave's loads complete in issue order), while HBM keeps streaming through the
-// hand-offs. The compute waves synchronise among themselves with an LDS counter (the
-// loaders take part in no barrier).
+// The weights are repacked once (k_stream_pack) into one contiguous byte stream per
+// (workgroup, wave): the slots that wave will consume in one token, in order -- its share
+// of every layer's QKV, wo, gate/up and down rows, then of the lm_head. Each wave copies its
+// own stream into an LDS ring of its own with direct global->LDS loads and keeps at most a
+// few slots in flight: the CU's vector memory path is one queue, and an exchange poll
+// waits behind every load the CU has in flight (one-way hand-offs measured on MI355X: 0.57
+// us idle, 1.3 us at 16 KiB in flight per CU, 2.4 us at 32 KiB and more), while 16 KiB per
+// CU already streams 5.9 of the 6.3 TB/s the chip reads. The ring is topped up after every
+// slot a wave consumes and on every round of an exchange poll, so HBM keeps streaming
+// through the hand-offs at that depth.
 //
 // A slot is one tile of a row: up to 64 lane steps of 16 weights. In the stream: q bytes
 // (16 per step) then the fp16 block scales (1 byte per step), padded to 16 bytes. In LDS:
-// 1024 q bytes then 64 scale bytes.
-//
-// Ring protocol, per compute wave w: ready[w] counts the slots whose loads have completed
-// (a loader writes it after s_waitcnt vmcnt), released[w] the slots wave w has read
-// (written after its reads complete). The loader fills a slot only while fewer than RS are
-// unreleased; wave w reads slot k once ready[w] > k.
+// 1024 q bytes then 64 scale bytes. Every slot is two load instructions (q, scales), so a
+// wave knows slot k is in LDS once at most 2 j of its loads are outstanding, j being the
+// slots it issued after k (its loads complete in order).
 #pragma once
 #include "k_step.hpp"
 
 namespace tfk {
 
-constexpr int kSCW = 8;                        // compute waves per workgroup
-constexpr int kSLW = 2;                        // loader waves per workgroup
-constexpr int kSThreads = (kSCW + kSLW) * kWave;
+constexpr int kSCW = 8;                        // waves per workgroup
+constexpr int kSThreads = kSCW * kWave;
 constexpr int kSlotBytes = 1088;               // LDS bytes per ring slot
 constexpr int kSlotQ = 1024;                   // q bytes of a full slot (64 steps x 16)
 
@@ -117,9 +112,11 @@ struct StreamArgs {
     int n_tokens, greedy, lm_every, att_start;
     int split_all;              // splits per kv head of long spans (every workgroup splits), 0: none
     int split_from;             // spans up to this attend on one workgroup per kv head
-    int ring_slots;             // RS: slots per compute wave's ring
+    int ring_slots;             // RS: slots per wave's ring
     int steps_max;              // slots of the largest per-wave token stream (LDS steps table)
-    unsigned long long* dbg;    // builds with TF_STREAM_PROBE: [nwg][64] cycle counts, or nullptr
+    int depth;                  // slots a wave keeps in flight in the layer phases
+    int depth_lm;               // and in the lm_head phase (no hand-off waits behind its loads)
+    unsigned long long* dbg;    // builds with TF_STREAM_PROBE: [nwg][64] time stamps, or nullptr
 };
 
 }  // namespace tfk

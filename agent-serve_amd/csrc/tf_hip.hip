@@ -87,6 +87,7 @@ struct tf_hip_ctx {
     uint32_t *d_sfirst = nullptr, *d_snl = nullptr, *d_snt = nullptr;
     SLayer* d_slayers = nullptr;
     int s_steps_max = 0, s_rs = 0;
+    int s_depth = 2, s_depth_lm = 6;  // slots in flight per wave of the streaming kernel
     unsigned long long* ex = nullptr;
     size_t ex_words = 0;
     uint32_t epoch = 0;               // exchange epochs consumed (mirrors ctl->epoch)
@@ -631,6 +632,8 @@ int ensure_stream(tf_hip_ctx* c) {
     HIPCHK(c, hipStreamSynchronize(c->st));
     c->s_steps_max = steps_max;
     c->s_rs = rs;
+    if (const char* e = std::getenv("TF_HIP_STREAM_DEPTH")) c->s_depth = std::max(1, std::min(8, std::atoi(e)));
+    if (const char* e = std::getenv("TF_HIP_STREAM_DEPTH_LM")) c->s_depth_lm = std::max(1, std::min(8, std::atoi(e)));
     c->stream_state = 1;
     return 1;
 }
@@ -673,6 +676,8 @@ int run_stream(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
     a.split_from = c->split_from;
     a.ring_slots = c->s_rs;
     a.steps_max = c->s_steps_max;
+    a.depth = c->s_depth;
+    a.depth_lm = c->s_depth_lm;
     int rc = epoch_guard(c, n);
     if (rc) return rc;
 #ifdef TF_STREAM_PROBE
@@ -688,16 +693,12 @@ int run_stream(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
         std::vector<unsigned long long> h((size_t)c->n_wg * 64);
         (void)hipMemcpyAsync(h.data(), dbg, h.size() * 8, hipMemcpyDeviceToHost, c->st);
         (void)hipStreamSynchronize(c->st);
-        double sum[64] = {0};
-        for (int w = 0; w < c->n_wg; ++w)
-            for (int i = 0; i < 64; ++i) sum[i] += (double)h[(size_t)w * 64 + i] / c->n_wg;
-        for (int lw = 0; lw < 2; ++lw)
-            std::fprintf(stderr, "probe n=%d loader %d: rounds %.0f issue %.0f idle %.0f full %.0f cycles %.0f\n", n, lw,
-                         sum[lw * 5], sum[lw * 5 + 1], sum[lw * 5 + 2], sum[lw * 5 + 3], sum[lw * 5 + 4]);
         for (int wv = 0; wv < 8; ++wv) {
-            const double* q = sum + 12 + wv * 6;
-            std::fprintf(stderr, "probe wave %d: total %.0f units %.0f (ready %.0f) bar %.0f gather %.0f n %.0f\n", wv, q[4],
-                         q[3], q[0], q[1], q[2], q[5]);
+            double q[8] = {0};
+            for (int w = 0; w < c->n_wg; ++w)
+                for (int i = 0; i < 8; ++i) q[i] += (double)h[(size_t)w * 64 + wv * 8 + i] / c->n_wg / 100.0 / n;
+            std::fprintf(stderr, "probe n=%d wave %d us/token: total %.1f feed-wait %.1f gather %.1f units %.1f attn %.1f lm %.1f slots %.0f\n",
+                         n, wv, q[5], q[0], q[1], q[2], q[3], q[4], q[6] * 100.0);
         }
     }
 #endif
