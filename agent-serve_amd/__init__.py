@@ -72,6 +72,7 @@ def hip_lib() -> C.CDLL:
         "tf_hip_dequant_rows": (C.c_int, [C.c_int, C.c_int, vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _f32p]),
         "tf_hip_matmul": (C.c_int, [C.c_int, C.c_int, vp, C.c_int64, C.c_int64, _f32p, C.c_int32, _f32p]),
         "tf_hip_rmsnorm": (C.c_int, [C.c_int, _f32p, _f32p, C.c_int32, C.c_int32, C.c_float, _f32p]),
+        "tf_hip_rope": (C.c_int, [C.c_int, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _f32p, _f32p, C.c_int32]),
         "tf_hip_attn_decode": (C.c_int, [C.c_int, _f32p, _f32p, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                          C.c_int32, C.c_int32, _f32p]),
         "tf_hip_attn_prefill": (C.c_int, [C.c_int, _f32p, _f32p, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
@@ -402,6 +403,17 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, device: int = 0) -> np.nda
     w = np.ascontiguousarray(w, dtype=np.float32)
     out = np.zeros_like(x)
     _op(hip_lib().tf_hip_rmsnorm(device, _f(x), _f(w), x.shape[1], x.shape[0], eps, _f(out)), "tf_hip_rmsnorm")
+    return out
+
+
+def rope(x: np.ndarray, pos0: int, cos_tab: np.ndarray, sin_tab: np.ndarray, device: int = 0) -> np.ndarray:
+    """apply_rope_many (attention.cpp:48-53) of x [seq][n_heads][head_dim] on the GPU, angles from
+    the host tables [n_pos][head_dim/2] (rope_tables); returns the rotated copy."""
+    out = np.ascontiguousarray(x, dtype=np.float32).copy()
+    seq, n_heads, hd = out.shape
+    c = np.ascontiguousarray(cos_tab, dtype=np.float32)
+    s = np.ascontiguousarray(sin_tab, dtype=np.float32)
+    _op(hip_lib().tf_hip_rope(device, _f(out), seq, n_heads, hd, pos0, _f(c), _f(s), c.shape[0]), "tf_hip_rope")
     return out
 
 

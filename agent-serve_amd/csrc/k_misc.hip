@@ -134,6 +134,24 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float* x, const f
     for (int k = threadIdx.x; k < n; k += kBlock) o[k] = xr[k] * inv * w[k];
 }
 
+// apply_rope_many (attention.cpp:48-53): thread i rotates pair j of (row, head) i / d2 with
+// the angles of position pos0 + row from the host tables, as rope_one (attention.cpp:31-41)
+// in the reference's build, which contracts each output's first product into an fma.
+__global__ __launch_bounds__(kBlock) void k_rope_rows(float* x, int64_t n_pairs, int n_heads, int hd, int pos0,
+                                                      const float* cos_tab, const float* sin_tab) {
+    const int d2 = hd / 2;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n_pairs; i += (int64_t)gridDim.x * kBlock) {
+        const int64_t rh = i / d2;  // row * n_heads + head
+        const int j = (int)(i - rh * d2);
+        const int64_t pos = pos0 + rh / n_heads;
+        float* v = x + rh * hd;
+        const float c = cos_tab[pos * d2 + j], s = sin_tab[pos * d2 + j];
+        const float x0 = v[j], x1 = v[j + d2];
+        v[j] = fmaf(x0, c, -(x1 * s));
+        v[j + d2] = fmaf(x0, s, x1 * c);
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void k_argmax(const float* x, int n, Ctl* ctl) {
     __shared__ unsigned long long wb[kWavesPerBlock];
     unsigned long long best = 0;
@@ -226,6 +244,14 @@ hipError_t launch_repack(int type, const uint8_t* raw, int64_t K, int64_t N, Dev
 
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, int n, int rows, float eps, float* out, hipStream_t st) {
     hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(kBlock), 0, st, x, w, n, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_rows(float* x, int seq, int n_heads, int hd, int pos0, const float* cos_tab,
+                            const float* sin_tab, hipStream_t st) {
+    const int64_t n_pairs = (int64_t)seq * n_heads * (hd / 2);
+    hipLaunchKernelGGL(k_rope_rows, dim3(grid_for(n_pairs)), dim3(kBlock), 0, st, x, n_pairs, n_heads, hd, pos0, cos_tab,
+                       sin_tab);
     return hipGetLastError();
 }
 

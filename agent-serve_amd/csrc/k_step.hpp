@@ -39,6 +39,20 @@ constexpr int kSpinLimit = 1 << 20;  // about a second of polling
 constexpr int kErrToken = 1;
 constexpr int kErrTimeout = 2;
 
+// Builds with -DTF_STEP_PROBE record wall-clock stamps (10 ns ticks) of one token's phases
+// per layer and workgroup into StepArgs::dbg: [layer][workgroup][16], layer n_layer = lm_head.
+#ifdef TF_STEP_PROBE
+#define STEP_STAMP(layer, i)                                                                              \
+    do {                                                                                                  \
+        if (threadIdx.x == 0 && sc.a.dbg && t == sc.a.n_tokens / 2)                                       \
+            sc.a.dbg[((size_t)(layer) * sc.nwg + blockIdx.x) * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define STEP_STAMP(layer, i) \
+    do {                     \
+    } while (0)
+#endif
+
 __device__ __forceinline__ void put(u64* p, float v, uint32_t e) {
     __hip_atomic_store(gptr(p), ((u64)e << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -353,15 +367,18 @@ __device__ __forceinline__ int64_t kv_at(int layout, int G, int max_seq, int hd,
 //     merges the splits. The cache is read at agent scope. An empty split leaves m = -inf,
 //     l = 0, o = 0 and does not wait for the head block.
 //   Both store the new row at agent scope (a later, split token of the launch reads it from
-//   other XCDs) and wait for the stores before returning, i.e. before their next puts.
+//   other XCDs). With wait_row they wait for the stores before returning, i.e. before their
+//   next puts; without it the caller waits for them (s_waitcnt vmcnt(0) in the waves with
+//   tid < hd) before the workgroup's end-of-layer word, which every later reader of the row
+//   waits for.
 // bar() synchronises the kT threads that run the attention (a workgroup barrier, or the
 // compute waves' barrier of a kernel whose other waves do not take part). a supplies H, G,
 // hd, max_seq, layout and the RoPE tables, ly the layer's K and V cache (kc, vc).
 template <int HDM, bool kPart, int NB, class A, class Ly, class Fetch, class Bar>
 __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int pos, int p0, int p1,
-                                          float* qkv, float* sm, float* out, Fetch&& fetch, Bar&& bar) {
+                                          float* qkv, float* sm, float* out, Fetch&& fetch, Bar&& bar,
+                                          bool wait_row = true) {
     constexpr int kTV = (kTile * HDM / 4 + kT - 1) / kT;  // float4 of a K (or V) tile per thread
-    constexpr int kPairs = (kMaxRep * HDM + kT - 1) / kT;  // (head, dim) pairs of P.V per thread
     const int hd = a.hd, d2 = hd / 2, hd4 = hd / 4;
     const int n_rep = a.H / a.G;
     const int tid = threadIdx.x;
@@ -372,8 +389,6 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
     float* vn = kn + hd;              // [hd]
     float* kt = sm;                   // [kTile][hd + 4]
     float* vt = kt + kTile * ks;      // [kTile][hd]
-    float* pr = vt + kTile * hd;      // [n_rep][kTile]
-    float* st = pr + n_rep * kTile;   // [n_rep][3]
     if (kPart && p0 >= p1) {
         for (int i = tid; i < n_rep * ho; i += kT) {
             const int d = i % ho;
@@ -435,10 +450,6 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
             v[j + d2] = fmaf(x0, s, x1 * c);
         }
     }
-    if (tid < n_rep) {
-        st[3 * tid] = -INFINITY;
-        st[3 * tid + 1] = 0.0f;
-    }
     bar();
     const bool stores_row = pos >= p0 && pos < p1;
     if (stores_row) {
@@ -451,10 +462,16 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
         }
     }
     const float scale = 1.0f / sqrtf((float)hd);
-    float o_acc[kPairs];
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // Query head r = wave (n_rep <= kNW): its online-softmax state and its outputs (dims
+    // lane + 64 c) stay in the wave's registers; lane j scores position j of a tile.
+    constexpr int kOD = (HDM + kWave - 1) / kWave;
+    const bool head_wave = wave < n_rep;
+    const float* qr = qs + (head_wave ? wave : 0) * hd;
+    float m_run = -INFINITY, l_run = 0.0f;
+    float o_acc[kOD];
 #pragma unroll
-    for (int k = 0; k < kPairs; ++k) o_acc[k] = 0.0f;
-    const int lane = tid & 63, wave = tid >> 6;
+    for (int c = 0; c < kOD; ++c) o_acc[c] = 0.0f;
 
     auto step = [&](int ti, float4 (&kr)[kTV], float4 (&vr)[kTV]) __attribute__((always_inline)) {
             const int t0 = p0 + ti * kTile;
@@ -472,50 +489,49 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
             if constexpr (NB == 4) load_tile(tile_at(ti + 4), kr, vr);
             if (tn > 0) {
                 bar();
-                // scores in dot_f32's order (8 lanes, then hsum8; quant.cpp:198-214)
-                for (int i = tid; i < n_rep * tn; i += kT) {
-                    const int r = i / tn, j = i % tn;
-                    const float* qr = qs + r * hd;
-                    const float* krow = kt + j * ks;
-                    float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-                    for (int e = 0; e < hd; e += 8) {
-                        const float4 q0 = *(const float4*)(qr + e), q1 = *(const float4*)(qr + e + 4);
-                        const float4 x0 = *(const float4*)(krow + e), x1 = *(const float4*)(krow + e + 4);
-                        c[0] = fmaf(q0.x, x0.x, c[0]);
-                        c[1] = fmaf(q0.y, x0.y, c[1]);
-                        c[2] = fmaf(q0.z, x0.z, c[2]);
-                        c[3] = fmaf(q0.w, x0.w, c[3]);
-                        c[4] = fmaf(q1.x, x1.x, c[4]);
-                        c[5] = fmaf(q1.y, x1.y, c[5]);
-                        c[6] = fmaf(q1.z, x1.z, c[6]);
-                        c[7] = fmaf(q1.w, x1.w, c[7]);
+                if (head_wave) {
+                    // score of position lane in dot_f32's order (8 lanes, then hsum8;
+                    // quant.cpp:198-214)
+                    float v = -INFINITY;
+                    if (lane < tn) {
+                        const float* krow = kt + lane * ks;
+                        float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll 8
+                        for (int e = 0; e < HDM; e += 8) {
+                            if (e < hd) {
+                                const float4 q0 = *(const float4*)(qr + e), q1 = *(const float4*)(qr + e + 4);
+                                const float4 x0 = *(const float4*)(krow + e), x1 = *(const float4*)(krow + e + 4);
+                                c[0] = fmaf(q0.x, x0.x, c[0]);
+                                c[1] = fmaf(q0.y, x0.y, c[1]);
+                                c[2] = fmaf(q0.z, x0.z, c[2]);
+                                c[3] = fmaf(q0.w, x0.w, c[3]);
+                                c[4] = fmaf(q1.x, x1.x, c[4]);
+                                c[5] = fmaf(q1.y, x1.y, c[5]);
+                                c[6] = fmaf(q1.z, x1.z, c[6]);
+                                c[7] = fmaf(q1.w, x1.w, c[7]);
+                            }
+                        }
+                        v = scale * (((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7])));
                     }
-                    pr[r * kTile + j] = scale * (((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7])));
-                }
-                bar();
-                for (int r = wave; r < n_rep; r += kNW) {
-                    const float v = lane < tn ? pr[r * kTile + lane] : -INFINITY;
-                    const float m_old = st[3 * r];
-                    const float m_new = fmaxf(m_old, wave_max(v));
+                    // online softmax over the tile (softmax, layers.cpp:25-35, one tile at a time)
+                    const float m_new = fmaxf(m_run, wave_max(v));
                     const float e = lane < tn ? expf(v - m_new) : 0.0f;
-                    if (lane < tn) pr[r * kTile + lane] = e;
                     const float l_tile = wave_sum(e);
-                    if (lane == 0) {
-                        const float alpha = expf(m_old - m_new);
-                        st[3 * r] = m_new;
-                        st[3 * r + 1] = fmaf(st[3 * r + 1], alpha, l_tile);
-                        st[3 * r + 2] = alpha;
-                    }
-                }
-                bar();
+                    const float alpha = expf(m_run - m_new);
+                    m_run = m_new;
+                    l_run = fmaf(l_run, alpha, l_tile);
+                    // P.V: dim lane + 64 c, positions in order; p_j read from lane j
 #pragma unroll
-                for (int k = 0; k < kPairs; ++k) {
-                    const int pi = tid + k * kT;
-                    if (pi < n_rep * hd) {
-                        const int r = pi / hd, d = pi % hd;
-                        float o = o_acc[k] * st[3 * r + 2];
-                        for (int j = 0; j < tn; ++j) o = fmaf(pr[r * kTile + j], vt[j * hd + d], o);
-                        o_acc[k] = o;
+                    for (int c = 0; c < kOD; ++c) {
+                        const int d = lane + c * kWave;
+                        if (c * kWave < hd) {
+                            const int dd = d < hd ? d : hd - 1;
+                            float o = o_acc[c] * alpha;
+#pragma unroll 8
+                            for (int j = 0; j < tn; ++j)
+                                o = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j)), vt[j * hd + dd], o);
+                            o_acc[c] = o;
+                        }
                     }
                 }
                 bar();
@@ -533,49 +549,52 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
         step(0, kr0, vr0);
         if constexpr (NB == 2) step(1, kr1, vr1);
     }
-    if constexpr (kPart) {
+    if (head_wave) {
+        const int r = wave;
 #pragma unroll
-        for (int k = 0; k < kPairs; ++k) {
-            const int pi = tid + k * kT;
-            if (pi < n_rep * hd) out[(pi / hd) * ho + pi % hd] = o_acc[k];
+        for (int c = 0; c < kOD; ++c) {
+            const int d = lane + c * kWave;
+            if (d < hd) {
+                if constexpr (kPart)
+                    out[r * ho + d] = o_acc[c];
+                else
+                    out[r * hd + d] = o_acc[c] / l_run;
+            }
         }
-        if (tid < n_rep) {
-            out[tid * ho + hd] = st[3 * tid];
-            out[tid * ho + hd + 1] = st[3 * tid + 1];
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < kPairs; ++k) {
-            const int pi = tid + k * kT;
-            if (pi < n_rep * hd) out[pi] = o_acc[k] / st[3 * (pi / hd) + 1];
+        if constexpr (kPart) {
+            if (lane == 0) {
+                out[r * ho + hd] = m_run;
+                out[r * ho + hd + 1] = l_run;
+            }
         }
     }
     // the row's stores are done before this workgroup's next puts
-    if (stores_row) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (stores_row && wait_row) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     bar();
 }
 
 template <int HDM, class A, class Ly, class Fetch, class Bar>
 __device__ __forceinline__ void attn_head(const A& a, const Ly& ly, int g, int pos, int start, float* qkv,
-                                          float* sm, float* out, Fetch&& fetch, Bar&& bar) {
+                                          float* sm, float* out, Fetch&& fetch, Bar&& bar, bool wait_row = true) {
     const int n = pos + 1 - start;
     if (n > 2 * kTile)
-        attn_span<HDM, false, 4>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch, bar);
+        attn_span<HDM, false, 4>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch, bar, wait_row);
     else if (n > kTile)
-        attn_span<HDM, false, 2>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch, bar);
+        attn_span<HDM, false, 2>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch, bar, wait_row);
     else
-        attn_span<HDM, false, 1>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch, bar);
+        attn_span<HDM, false, 1>(a, ly, g, pos, start, pos + 1, qkv, sm, out, fetch, bar, wait_row);
 }
 
 template <int HDM, class A, class Ly, class Fetch, class Bar>
 __device__ __forceinline__ void attn_part(const A& a, const Ly& ly, int g, int pos, int p0, int p1,
-                                          float* qkv, float* sm, float* out, Fetch&& fetch, Bar&& bar) {
+                                          float* qkv, float* sm, float* out, Fetch&& fetch, Bar&& bar,
+                                          bool wait_row = true) {
     if (p1 - p0 > 2 * kTile)
-        attn_span<HDM, true, 4>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch, bar);
+        attn_span<HDM, true, 4>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch, bar, wait_row);
     else if (p1 - p0 > kTile)
-        attn_span<HDM, true, 2>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch, bar);
+        attn_span<HDM, true, 2>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch, bar, wait_row);
     else
-        attn_span<HDM, true, 1>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch, bar);
+        attn_span<HDM, true, 1>(a, ly, g, pos, p0, p1, qkv, sm, out, fetch, bar, wait_row);
 }
 
 // Floats of LDS the attention scratch needs.
@@ -753,6 +772,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             // short spans attend on one workgroup per kv head (attn_head), longer ones split
             const bool split = sc.A && (all || span > sc.a.split_from);
             const int attn_wg0 = split ? sc.attn_wg0 : sc.nwg - sc.G;
+            STEP_STAMP(l, 0);
             // ---- 1: QKV (attn_norm fused)
             {
                 const int D = sc.D;
@@ -812,6 +832,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                                          X(sc.DONE) + ((l - 1) & 1) * sc.nwg, sc.nwg, E(t, l - 1, 5), a.ctl);
                     }
                     stage(xr, D, true, wr, a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
+                    STEP_STAMP(l, 1);
                 };
                 auto epi = [&](int si, int row, float v, float, float extra) {
                     const int hd = sc.hd, n_rep = sc.n_rep, HB = sc.HB;
@@ -826,6 +847,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 };
                 gemv_phase<TL, 1, GEMV_STORE, UL>(3, groups, seg, bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
                                                  prep, epi);
+                STEP_STAMP(l, 2);
             }
             // ---- 2: attention (kv head g on workgroup attn_wg0 + g), then 4: gate/up
             // ---- 3: wo + residual (workgroups without an attention head), then 4: gate/up
@@ -846,6 +868,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 auto gu_input = [&]() {
                     gather<kGD, 1>(X(sc.XB) + par * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl);
                     stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
+                    STEP_STAMP(l, 6);
                 };
                 // ---- 3: wo + residual, rows dealt over nw waves from wave 0
                 auto wo_phase = [&](int nw) {
@@ -860,6 +883,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     auto prep = [&]() {
                         gather<kGD, 1>(X(sc.ATT) + par * Hd, Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl);
                         stage(xs, Hd, false, wo_wr, 0.0f, xs, x16, kSums, red);
+                        STEP_STAMP(l, 4);
                     };
                     auto epi = [&](int, int row, float v, float, float) {
                         put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
@@ -893,11 +917,13 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         const int pos = sc.pos0 + t, start = sc.a.att_start;
                         const int chunk = (pos + 1 - start + A - 1) / A;
                         const int p0 = start + s * chunk, p1 = min(pos + 1, p0 + chunk);
+                        // trailing layout: the stored row is waited for after attention, off the
+                        // chain (the workgroup then waits for wo's output anyway)
                         attn_part<HDM>(sc.a, ly, g, pos, p0, p1, qkv, xs, part, [&]() {
                             gather<kGD, 1>(X(sc.QKV) + par * G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0,
                                            sc.a.ctl);
                             __syncthreads();
-                        }, [] { __syncthreads(); });
+                        }, [] { __syncthreads(); }, all);
                         u64* pw_base = pb + (size_t)(g * A + s) * n_rep * ho;
                         for (int i = tid; i < n_rep * ho; i += kT) put(pw_base + i, part[i], E(t, l, 6));
                     }
@@ -928,8 +954,15 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         }
                     }
                 }
+                // an attention workgroup that left its K/V row stores in flight waits for them
+                // (the waves that stored) before it issues the FFN's loads: wo's output is
+                // still a hand-off away, and the end-of-layer word comes after this
+                auto row_stores_done = [&]() {
+                    if (wave * kWave < sc.hd) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                };
                 if (split && !all && wg >= attn_wg0) {
                     auto down_then_input = [&]() {
+                        row_stores_done();
                         issue_down(ly);
                         gu_input();
                     };
@@ -945,10 +978,13 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         gather<kGD, 1>(X(sc.QKV) + par * sc.G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0,
                                        sc.a.ctl);
                         __syncthreads();
-                    }, [] { __syncthreads(); });
+                        STEP_STAMP(l, 3);
+                    }, [] { __syncthreads(); }, false);
                     const int nh = sc.n_rep * sc.hd;
                     for (int i = tid; i < nh; i += kT) put(X(sc.ATT) + par * sc.Hd + g * nh + i, att_out[i], E(t, l, 2));
+                    STEP_STAMP(l, 10);
                     auto down_then_input = [&]() {
+                        row_stores_done();
                         issue_down(ly);
                         gu_input();
                     };
@@ -958,6 +994,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     auto wo_then_input = [&]() {
                         issue_down(ly);
                         wo_phase((all ? sc.nwg : attn_wg0) * kNW);
+                        STEP_STAMP(l, 5);
                         __syncthreads();  // every wave's wo rows are read out of xs before the input is staged
                         gu_input();
                     };
@@ -965,6 +1002,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                                                     x16, wo_then_input, gu_epi);
                 }
             }
+            STEP_STAMP(l, 7);
             // ---- 5: down + residual
             {
                 const int F = sc.F;
@@ -974,6 +1012,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 auto prep = [&]() {
                     gather<kGF, 1>(X(sc.HH) + par * F, F, E(t, l, 4), xs, nullptr, 0, 0, sc.a.ctl);
                     stage(xs, F, false, wr, 0.0f, xs, x16, kSums, red);
+                    STEP_STAMP(l, 8);
                 };
                 auto epi = [&](int, int row, float v, float, float) {
                     const float nv = xr[row] + v;
@@ -1007,11 +1046,13 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                                                          xs, x16, prep, epi);
                 }
                 __syncthreads();
+                STEP_STAMP(l, 9);
                 if (tid == 0) put(X(sc.DONE) + par * sc.nwg + wg, 0.0f, E(t, l, 5));
             }
         }
         // ---- output_norm + lm_head + greedy argmax
         if (sc.a.lm_every || last) {
+            STEP_STAMP(sc.L, 0);
             const int D = sc.D;
             float wr[NWR];
             load_norm(sc.a.out_norm, D, wr);
@@ -1022,6 +1063,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 gather<kGD, kGW>(X(sc.XA) + (Lm & 1) * D, D, E(t, Lm, 5), xr, X(sc.DONE) + (Lm & 1) * sc.nwg, sc.nwg,
                                  E(t, Lm, 5), sc.a.ctl);
                 stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TO>::kNeedSums, red);
+                STEP_STAMP(sc.L, 1);
                 if (last && sc.a.taps && wg == 0)
                     for (int j = tid; j < D; j += kT) *gptr(sc.a.taps + (size_t)sc.L * D + j) = xs[j];
             };
@@ -1036,6 +1078,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             best = wave_max_u64(best);
             if (lane == 0) wbest[wave] = best;
             __syncthreads();
+            STEP_STAMP(sc.L, 2);
             if (tid == 0) {
                 u64 b = wbest[0];
                 for (int i = 1; i < kNW; ++i) b = wbest[i] > b ? wbest[i] : b;

@@ -572,8 +572,67 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
                                               : step_split_all_from(p.n_head, p.n_kv_head, p.head_dim, c->step_split);
     int rc = epoch_guard(c, n);
     if (rc) return rc;
+#ifdef TF_STEP_PROBE
+    const size_t n_dbg = (size_t)(p.n_layer + 1) * c->n_wg * 16;
+    if (n >= 8) {
+        (void)hipMalloc((void**)&a.dbg, n_dbg * 8);
+        (void)hipMemsetAsync(a.dbg, 0, n_dbg * 8, c->st);
+    }
+#endif
     const hipError_t e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);
     if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("step kernel launch: ") + hipGetErrorString(e));
+#ifdef TF_STEP_PROBE
+    if (a.dbg) {
+        // per stamp: median and max over workgroups of (stamp - the layer's earliest start),
+        // means over layers 1 .. L-2, in microseconds
+        std::vector<unsigned long long> h(n_dbg);
+        (void)hipMemcpyAsync(h.data(), a.dbg, n_dbg * 8, hipMemcpyDeviceToHost, c->st);
+        (void)hipStreamSynchronize(c->st);
+        (void)hipFree(a.dbg);
+        const int L = p.n_layer, W = c->n_wg;
+        double med[16] = {0}, mx[16] = {0}, cnt[16] = {0}, layer_us = 0;
+        for (int l = 1; l + 1 < L; ++l) {
+            unsigned long long t0 = ~0ull, t1 = ~0ull;
+            for (int w = 0; w < W; ++w) {
+                const unsigned long long s = h[((size_t)l * W + w) * 16];
+                const unsigned long long s1 = h[((size_t)(l + 1) * W + w) * 16];
+                if (s) t0 = std::min(t0, s);
+                if (s1) t1 = std::min(t1, s1);
+            }
+            if (t0 == ~0ull || t1 == ~0ull) continue;
+            layer_us += (double)(t1 - t0) / 100.0;
+            for (int i = 0; i < 16; ++i) {
+                std::vector<double> v;
+                for (int w = 0; w < W; ++w) {
+                    const unsigned long long s = h[((size_t)l * W + w) * 16 + i];
+                    if (s) v.push_back((double)(s - t0) / 100.0);
+                }
+                if (v.empty()) continue;
+                std::sort(v.begin(), v.end());
+                med[i] += v[v.size() / 2];
+                mx[i] += v.back();
+                cnt[i] += 1;
+            }
+        }
+        std::fprintf(stderr, "step probe n=%d pos=%d: layer %.2f us (start to next start, mean of layers 1..%d)\n", n,
+                     a.att_start, layer_us / std::max(1, L - 2), L - 2);
+        const char* nm[11] = {"start", "qkv in", "qkv done", "attn qkv in", "wo in", "wo done",
+                              "gu in", "gu done", "down in", "down done", "attn out put"};
+        for (int i = 0; i < 11; ++i)
+            if (cnt[i] > 0)
+                std::fprintf(stderr, "  %-16s med %6.2f max %6.2f\n", nm[i], med[i] / cnt[i], mx[i] / cnt[i]);
+        unsigned long long l0 = ~0ull, l1 = 0, l2 = 0;
+        for (int w = 0; w < W; ++w) {
+            const unsigned long long* q = &h[((size_t)L * W + w) * 16];
+            if (q[0]) l0 = std::min(l0, q[0]);
+            l1 = std::max(l1, q[1]);
+            l2 = std::max(l2, q[2]);
+        }
+        if (l0 != ~0ull)
+            std::fprintf(stderr, "  lm_head: in by %.2f, done by %.2f us\n", (double)(l1 - l0) / 100.0,
+                         (double)(l2 - l0) / 100.0);
+    }
+#endif
     c->epoch += (uint32_t)((uint64_t)n * (6ull * (uint64_t)p.n_layer + 8ull));
     return 0;
 }
@@ -1474,6 +1533,28 @@ int tf_hip_rmsnorm(int device, const float* x, const float* w, int32_t n, int32_
     OPCHK(hipMemcpy(dw, w, (size_t)n * 4, hipMemcpyHostToDevice));
     OPCHK(launch_rmsnorm_rows(dx, dw, n, rows, eps, dout, s.st));
     OPCHK(hipMemcpyAsync(out, dout, (size_t)n * rows * 4, hipMemcpyDeviceToHost, s.st));
+    OPCHK(hipStreamSynchronize(s.st));
+    return 0;
+}
+
+int tf_hip_rope(int device, float* x, int32_t seq, int32_t n_heads, int32_t hd, int32_t pos0, const float* cos_tab,
+                const float* sin_tab, int32_t n_pos_tab) {
+    if (!x || !cos_tab || !sin_tab || seq <= 0 || n_heads <= 0 || hd <= 0 || hd % 2 || pos0 < 0 || n_pos_tab <= 0 ||
+        seq > n_pos_tab - pos0)
+        return TF_HIP_EINVAL;
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    const size_t nx = (size_t)seq * n_heads * hd, nt = (size_t)(pos0 + seq) * (hd / 2);
+    float *dx, *dc, *ds;
+    OPCHK(s.alloc(&dx, nx * 4));
+    OPCHK(s.alloc(&dc, nt * 4));
+    OPCHK(s.alloc(&ds, nt * 4));
+    OPCHK(hipMemcpy(dx, x, nx * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemcpy(dc, cos_tab, nt * 4, hipMemcpyHostToDevice));
+    OPCHK(hipMemcpy(ds, sin_tab, nt * 4, hipMemcpyHostToDevice));
+    OPCHK(launch_rope_rows(dx, seq, n_heads, hd, pos0, dc, ds, s.st));
+    OPCHK(hipMemcpyAsync(x, dx, nx * 4, hipMemcpyDeviceToHost, s.st));
     OPCHK(hipStreamSynchronize(s.st));
     return 0;
 }

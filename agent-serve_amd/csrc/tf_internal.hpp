@@ -148,6 +148,7 @@ struct StepArgs {
     int split_all;             // > 0: splits per kv head when every workgroup splits (step_split_all)
     int split_all_from;        // spans longer than this use split_all (step_split_all_from)
     int split_from;            // spans (positions attended) up to this attend on one workgroup per kv head
+    unsigned long long* dbg;   // builds with TF_STEP_PROBE: [n_layer + 1][n_wg][16] time stamps, or nullptr
 };
 
 // ---------------------------------------------------------------- prefill on the matrix cores
@@ -259,6 +260,8 @@ hipError_t launch_dequant_rows(const DevMat& m, int64_t row0, int64_t nrows, flo
 hipError_t launch_repack(int type, const uint8_t* raw, int64_t K, int64_t N, DevMat& m, hipStream_t st);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, int n, int rows, float eps, float* out,
                                hipStream_t st);
+hipError_t launch_rope_rows(float* x, int seq, int n_heads, int hd, int pos0, const float* cos_tab,
+                            const float* sin_tab, hipStream_t st);
 hipError_t launch_argmax(const float* x, int n, Ctl* ctl, hipStream_t st);
 hipError_t launch_copy_stream(float4* dst, const float4* src, size_t n4, int blocks, hipStream_t st);
 hipError_t launch_read_stream(const float4* p, size_t n4, double* out, int blocks, hipStream_t st);

@@ -219,6 +219,16 @@ int tf_hip_matmul(int device, int ggml_type, const void* w, int64_t ne0, int64_t
 /* rmsnorm (layers.cpp:7-12) of n_rows rows of length n. */
 int tf_hip_rmsnorm(int device, const float* x, const float* w, int32_t n, int32_t n_rows, float eps, float* out);
 
+/* apply_rope_many (attention.cpp:48-53; apply_rope, attention.cpp:43-46, is seq = 1):
+ * rotates x [seq][n_heads][head_dim] in place, row i at position pos0 + i, pairs
+ * (x[j], x[j + head_dim/2]) as rope_one (attention.cpp:31-41) with its two contracted
+ * products. The angles come from cos_tab / sin_tab [n_pos_tab][head_dim/2], the tables
+ * tf_hip_set_rope_table takes (cos/sin((float)pos * freq) on the host), so the result is
+ * bit-identical to the reference's. TF_HIP_EINVAL for an odd head_dim or rows past the
+ * tables. */
+int tf_hip_rope(int device, float* x, int32_t seq, int32_t n_heads, int32_t head_dim, int32_t pos0,
+                const float* cos_tab, const float* sin_tab, int32_t n_pos_tab);
+
 /* attn_decode (attention.cpp:55-80) for one layer: q [n_heads][hd] (already rotated),
  * k_rows/v_rows [n_pos][n_kv][hd] logical rows stored into a cache of the given layout and
  * max_seq before the kernel runs; out [n_heads][hd]. */

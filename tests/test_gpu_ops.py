@@ -222,6 +222,39 @@ def test_rmsnorm(pkg, n):
         assert rel_err(got[i], want) <= 2.5e-7
 
 
+ROPE_CASES = [  # theta, head_dim, heads, rows, first position
+    (500000.0, 64, 32, 6, 0), (1e6, 64, 14, 37, 100), (1e6, 128, 12, 5, 4091), (10000.0, 8, 4, 9, 0),
+]
+
+
+@pytest.mark.parametrize("theta,hd,heads,seq,pos0", ROPE_CASES)
+def test_rope_bit_exact(pkg, theta, hd, heads, seq, pos0):
+    """tf_hip_rope against the oracle's rope_one, position by position, bit for bit (the host
+    tables hold the reference's own cos/sin values)."""
+    rng = np.random.default_rng(hd * 7 + seq)
+    x = (rng.standard_normal((seq, heads, hd)) * 2).astype(np.float32)
+    cos_t, sin_t = pkg.rope_tables(theta, hd, pos0 + seq)
+    got = pkg.rope(x, pos0, cos_t, sin_t)
+    L = oracle_lib()
+    fp = C.POINTER(C.c_float)
+    freq = np.zeros(hd // 2, np.float32)
+    L.orc_rope_freqs(freq.ctypes.data_as(fp), hd, theta, 0, 1.0, 1.0, 4.0, 8192.0)
+    want = x.copy()
+    for i in range(seq):
+        row = np.ascontiguousarray(want[i])
+        L.orc_rope(row.ctypes.data_as(fp), heads, hd, pos0 + i, freq.ctypes.data_as(fp))
+        want[i] = row
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if pos0 == 0:
+        assert np.array_equal(got[0], x[0])  # position 0 is the identity
+
+
+def test_rope_rejects_rows_past_the_tables(pkg):
+    cos_t, sin_t = pkg.rope_tables(10000.0, 8, 4)
+    with pytest.raises(RuntimeError):
+        pkg.rope(np.zeros((3, 2, 8), np.float32), 2, cos_t, sin_t)
+
+
 ATTN_CASES = [  # heads, kv heads, head_dim, n_pos, max_seq
     (32, 8, 64, 1, 64), (32, 8, 64, 7, 64), (32, 8, 64, 38, 512), (32, 8, 64, 300, 512),
     (14, 2, 64, 144, 256), (12, 2, 128, 1000, 2048), (12, 2, 128, 4352, 8192), (4, 2, 8, 9, 16),
