@@ -21,6 +21,8 @@
 // hand-off completes. Every wait is bounded: past the limit, or once another workgroup
 // has flagged a failure, it flags ctl->err and goes on, and the host reports the error.
 #pragma once
+#include <type_traits>
+
 #include "formats.hpp"
 
 namespace tfk {
@@ -47,7 +49,24 @@ constexpr int kErrTimeout = 2;
         if (threadIdx.x == 0 && sc.a.dbg && t == sc.a.n_tokens / 2)                                       \
             sc.a.dbg[((size_t)(layer) * sc.nwg + blockIdx.x) * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
+// attention sub-phases: ticks since the previous mark summed per workgroup into the
+// lm_head row's slots 13..15 (slot 12 counts the calls), every token and layer
+#define ATTN_MARK(i)                                                                                  \
+    do {                                                                                              \
+        if constexpr (std::is_same<A, StepArgs>::value) {                                             \
+            if (threadIdx.x == 0 && a.dbg) {                                                          \
+                const unsigned long long now_ = __builtin_amdgcn_s_memrealtime();                      \
+                unsigned long long* row_ = a.dbg + ((size_t)a.n_layer * gridDim.x + blockIdx.x) * 16; \
+                if ((i) > 0) row_[12 + (i)] += now_ - probe_t_;                                       \
+                if ((i) == 3) row_[12] += 1;                                                          \
+                probe_t_ = now_;                                                                      \
+            }                                                                                         \
+        }                                                                                             \
+    } while (0)
 #else
+#define ATTN_MARK(i) \
+    do {             \
+    } while (0)
 #define STEP_STAMP(layer, i) \
     do {                     \
     } while (0)
@@ -437,7 +456,11 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
         rc[k] = cs[j];
         rs[k] = sn[j];
     }
+#ifdef TF_STEP_PROBE
+    unsigned long long probe_t_ = 0;
+#endif
     fetch();
+    ATTN_MARK(0);
     // RoPE (rope_one, with the reference build's contractions)
 #pragma unroll
     for (int k = 0; k < kRope; ++k) {
@@ -461,6 +484,7 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
             __hip_atomic_store(gptr(ly.vc + o + j), vn[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    ATTN_MARK(1);
     const float scale = 1.0f / sqrtf((float)hd);
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // Query head r = wave (n_rep <= kNW): its online-softmax state and its outputs (dims
@@ -549,6 +573,7 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
         step(0, kr0, vr0);
         if constexpr (NB == 2) step(1, kr1, vr1);
     }
+    ATTN_MARK(2);
     if (head_wave) {
         const int r = wave;
 #pragma unroll
@@ -571,6 +596,7 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
     // the row's stores are done before this workgroup's next puts
     if (stores_row && wait_row) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     bar();
+    ATTN_MARK(3);
 }
 
 template <int HDM, class A, class Ly, class Fetch, class Bar>
@@ -923,9 +949,11 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                             gather<kGD, 1>(X(sc.QKV) + par * G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0,
                                            sc.a.ctl);
                             __syncthreads();
+                            STEP_STAMP(l, 3);
                         }, [] { __syncthreads(); }, all);
                         u64* pw_base = pb + (size_t)(g * A + s) * n_rep * ho;
                         for (int i = tid; i < n_rep * ho; i += kT) put(pw_base + i, part[i], E(t, l, 6));
+                        STEP_STAMP(l, 10);
                     }
                     if (aw < sc.a.H * parts) {
                         const int sz = hd / parts;
@@ -938,6 +966,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                             return (size_t)((g * A + s) * n_rep + r) * ho + (k < sz ? d0 + k : hd + k - sz);
                         }, A * w, E(t, l, 6), buf, sc.a.ctl);
                         __syncthreads();
+                        STEP_STAMP(l, 11);
                         for (int k = wave; k < sz; k += kNW) {
                             float m = -INFINITY;
                             for (int s = lane; s < A; s += kWave) m = fmaxf(m, buf[s * w + sz]);
@@ -952,6 +981,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                             osum = wave_sum(osum);
                             if (lane == 0) put(X(sc.ATT) + par * sc.Hd + h * hd + d0 + k, osum / lsum, E(t, l, 2));
                         }
+                        STEP_STAMP(l, 12);
                     }
                 }
                 // an attention workgroup that left its K/V row stores in flight waits for them
@@ -990,10 +1020,22 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     };
                     gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, down_then_input, gu_epi);
+                } else if (all) {
+                    // Every workgroup split the attention: the merged output comes right after
+                    // the merge, so gate/up's tiles wait until wo is done. (A wave's loads
+                    // complete in issue order and the CU's vector memory path is one queue:
+                    // every load issued before the attention-output polls delays them.)
+                    issue_down(ly);
+                    wo_phase(sc.nwg * kNW);
+                    STEP_STAMP(l, 5);
+                    gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                                                    x16, gu_input, gu_epi);
                 } else {
+                    // The attention runs on other workgroups for several microseconds: gate/up's
+                    // first tiles and the ffn_down rows stream in meanwhile.
                     auto wo_then_input = [&]() {
                         issue_down(ly);
-                        wo_phase((all ? sc.nwg : attn_wg0) * kNW);
+                        wo_phase(attn_wg0 * kNW);
                         STEP_STAMP(l, 5);
                         __syncthreads();  // every wave's wo rows are read out of xs before the input is staged
                         gu_input();

@@ -616,9 +616,9 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
         }
         std::fprintf(stderr, "step probe n=%d pos=%d: layer %.2f us (start to next start, mean of layers 1..%d)\n", n,
                      a.att_start, layer_us / std::max(1, L - 2), L - 2);
-        const char* nm[11] = {"start", "qkv in", "qkv done", "attn qkv in", "wo in", "wo done",
-                              "gu in", "gu done", "down in", "down done", "attn out put"};
-        for (int i = 0; i < 11; ++i)
+        const char* nm[13] = {"start", "qkv in", "qkv done", "attn qkv in", "wo in", "wo done",
+                              "gu in", "gu done", "down in", "down done", "attn out put", "merge in", "merge put"};
+        for (int i = 0; i < 13; ++i)
             if (cnt[i] > 0)
                 std::fprintf(stderr, "  %-16s med %6.2f max %6.2f\n", nm[i], med[i] / cnt[i], mx[i] / cnt[i]);
         unsigned long long l0 = ~0ull, l1 = 0, l2 = 0;
@@ -631,6 +631,15 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
         if (l0 != ~0ull)
             std::fprintf(stderr, "  lm_head: in by %.2f, done by %.2f us\n", (double)(l1 - l0) / 100.0,
                          (double)(l2 - l0) / 100.0);
+        double acc[3] = {0, 0, 0}, calls = 0;
+        for (int w = 0; w < W; ++w) {
+            const unsigned long long* q = &h[((size_t)L * W + w) * 16];
+            calls += (double)q[12];
+            for (int i = 0; i < 3; ++i) acc[i] += (double)q[13 + i];
+        }
+        if (calls > 0)
+            std::fprintf(stderr, "  attention per call (%.0f calls): rope+row %.2f, tiles %.2f, output %.2f us\n", calls,
+                         acc[0] / calls / 100.0, acc[1] / calls / 100.0, acc[2] / calls / 100.0);
     }
 #endif
     c->epoch += (uint32_t)((uint64_t)n * (6ull * (uint64_t)p.n_layer + 8ull));
