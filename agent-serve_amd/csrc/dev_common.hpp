@@ -86,10 +86,18 @@ __device__ __forceinline__ double wave_sum_d(double v) {
     return v;
 }
 
+// Wavefront max (exact in any order): DPP within rows of 16, then row_bcast:15 (row r's
+// lane 15 into row r + 1, rows 1 and 3) and row_bcast:31 (lane 31 into rows 2 and 3), so
+// lane 63 holds the maximum; it is read back as a uniform value. No LDS round trip.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppMirror>(v));
+    const int ninf = __float_as_int(-INFINITY);
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x142, 0xA, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x143, 0xC, 0xF, false)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {

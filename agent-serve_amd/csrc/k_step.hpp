@@ -49,16 +49,17 @@ constexpr int kErrTimeout = 2;
         if (threadIdx.x == 0 && sc.a.dbg && t == sc.a.n_tokens / 2)                                       \
             sc.a.dbg[((size_t)(layer) * sc.nwg + blockIdx.x) * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
-// attention sub-phases: ticks since the previous mark summed per workgroup into the
-// lm_head row's slots 13..15 (slot 12 counts the calls), every token and layer
+// attention sub-phases: ticks since the previous mark, stored (no read: a load would wait
+// for the wave's loads in flight) per workgroup into the lm_head row's slots 12..15 (slot
+// 11 set to 1); the launch's last call of each workgroup remains
 #define ATTN_MARK(i)                                                                                  \
     do {                                                                                              \
         if constexpr (std::is_same<A, StepArgs>::value) {                                             \
             if (threadIdx.x == 0 && a.dbg) {                                                          \
                 const unsigned long long now_ = __builtin_amdgcn_s_memrealtime();                      \
                 unsigned long long* row_ = a.dbg + ((size_t)a.n_layer * gridDim.x + blockIdx.x) * 16; \
-                if ((i) > 0) row_[12 + (i)] += now_ - probe_t_;                                       \
-                if ((i) == 3) row_[12] += 1;                                                          \
+                if ((i) > 0) row_[11 + (i)] = now_ - probe_t_;                                        \
+                if ((i) == 4) row_[11] = 1;                                                           \
                 probe_t_ = now_;                                                                      \
             }                                                                                         \
         }                                                                                             \
@@ -513,27 +514,32 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
             if constexpr (NB == 4) load_tile(tile_at(ti + 4), kr, vr);
             if (tn > 0) {
                 bar();
+                if (ti == 0) ATTN_MARK(2);
                 if (head_wave) {
                     // score of position lane in dot_f32's order (8 lanes, then hsum8;
-                    // quant.cpp:198-214)
+                    // quant.cpp:198-214). Unguarded and fully unrolled when hd is the
+                    // instantiation's head size, so the LDS reads pipeline.
                     float v = -INFINITY;
                     if (lane < tn) {
                         const float* krow = kt + lane * ks;
                         float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll 8
-                        for (int e = 0; e < HDM; e += 8) {
-                            if (e < hd) {
-                                const float4 q0 = *(const float4*)(qr + e), q1 = *(const float4*)(qr + e + 4);
-                                const float4 x0 = *(const float4*)(krow + e), x1 = *(const float4*)(krow + e + 4);
-                                c[0] = fmaf(q0.x, x0.x, c[0]);
-                                c[1] = fmaf(q0.y, x0.y, c[1]);
-                                c[2] = fmaf(q0.z, x0.z, c[2]);
-                                c[3] = fmaf(q0.w, x0.w, c[3]);
-                                c[4] = fmaf(q1.x, x1.x, c[4]);
-                                c[5] = fmaf(q1.y, x1.y, c[5]);
-                                c[6] = fmaf(q1.z, x1.z, c[6]);
-                                c[7] = fmaf(q1.w, x1.w, c[7]);
-                            }
+                        auto dot8 = [&](int e) __attribute__((always_inline)) {
+                            const float4 q0 = *(const float4*)(qr + e), q1 = *(const float4*)(qr + e + 4);
+                            const float4 x0 = *(const float4*)(krow + e), x1 = *(const float4*)(krow + e + 4);
+                            c[0] = fmaf(q0.x, x0.x, c[0]);
+                            c[1] = fmaf(q0.y, x0.y, c[1]);
+                            c[2] = fmaf(q0.z, x0.z, c[2]);
+                            c[3] = fmaf(q0.w, x0.w, c[3]);
+                            c[4] = fmaf(q1.x, x1.x, c[4]);
+                            c[5] = fmaf(q1.y, x1.y, c[5]);
+                            c[6] = fmaf(q1.z, x1.z, c[6]);
+                            c[7] = fmaf(q1.w, x1.w, c[7]);
+                        };
+                        if (hd == HDM) {
+#pragma unroll
+                            for (int e = 0; e < HDM; e += 8) dot8(e);
+                        } else {
+                            for (int e = 0; e < hd; e += 8) dot8(e);
                         }
                         v = scale * (((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7])));
                     }
@@ -551,8 +557,19 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
                         if (c * kWave < hd) {
                             const int dd = d < hd ? d : hd - 1;
                             float o = o_acc[c] * alpha;
-#pragma unroll 8
-                            for (int j = 0; j < tn; ++j)
+                            // eight positions at a time with their V reads issued together
+                            // (readlane is convergent: the compiler does not unroll a loop
+                            // with a run-time trip count around it)
+                            int j = 0;
+                            for (; j + 8 <= tn; j += 8) {
+                                float vv[8];
+#pragma unroll
+                                for (int u = 0; u < 8; ++u) vv[u] = vt[(j + u) * hd + dd];
+#pragma unroll
+                                for (int u = 0; u < 8; ++u)
+                                    o = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j + u)), vv[u], o);
+                            }
+                            for (; j < tn; ++j)
                                 o = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j)), vt[j * hd + dd], o);
                             o_acc[c] = o;
                         }
@@ -573,7 +590,7 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
         step(0, kr0, vr0);
         if constexpr (NB == 2) step(1, kr1, vr1);
     }
-    ATTN_MARK(2);
+    ATTN_MARK(3);
     if (head_wave) {
         const int r = wave;
 #pragma unroll
@@ -596,7 +613,7 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
     // the row's stores are done before this workgroup's next puts
     if (stores_row && wait_row) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     bar();
-    ATTN_MARK(3);
+    ATTN_MARK(4);
 }
 
 template <int HDM, class A, class Ly, class Fetch, class Bar>

@@ -631,15 +631,17 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
         if (l0 != ~0ull)
             std::fprintf(stderr, "  lm_head: in by %.2f, done by %.2f us\n", (double)(l1 - l0) / 100.0,
                          (double)(l2 - l0) / 100.0);
-        double acc[3] = {0, 0, 0}, calls = 0;
+        double acc[4] = {0, 0, 0, 0}, calls = 0;
         for (int w = 0; w < W; ++w) {
             const unsigned long long* q = &h[((size_t)L * W + w) * 16];
-            calls += (double)q[12];
-            for (int i = 0; i < 3; ++i) acc[i] += (double)q[13 + i];
+            calls += (double)q[11];
+            for (int i = 0; i < 4; ++i) acc[i] += (double)q[12 + i];
         }
         if (calls > 0)
-            std::fprintf(stderr, "  attention per call (%.0f calls): rope+row %.2f, tiles %.2f, output %.2f us\n", calls,
-                         acc[0] / calls / 100.0, acc[1] / calls / 100.0, acc[2] / calls / 100.0);
+            std::fprintf(stderr,
+                         "  attention per call (%.0f calls): rope+row %.2f, first tile staged %.2f, tiles %.2f, output %.2f us\n",
+                         calls, acc[0] / calls / 100.0, acc[1] / calls / 100.0, acc[2] / calls / 100.0,
+                         acc[3] / calls / 100.0);
     }
 #endif
     c->epoch += (uint32_t)((uint64_t)n * (6ull * (uint64_t)p.n_layer + 8ull));
