@@ -73,6 +73,9 @@ def hip_lib() -> C.CDLL:
         "tf_hip_matmul": (C.c_int, [C.c_int, C.c_int, vp, C.c_int64, C.c_int64, _f32p, C.c_int32, _f32p]),
         "tf_hip_rmsnorm": (C.c_int, [C.c_int, _f32p, _f32p, C.c_int32, C.c_int32, C.c_float, _f32p]),
         "tf_hip_rope": (C.c_int, [C.c_int, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _f32p, _f32p, C.c_int32]),
+        "tf_hip_sample": (C.c_int, [vp, C.c_float, C.c_float, C.c_float, _i32p]),
+        "tf_hip_sample_logits": (C.c_int, [C.c_int, _f32p, C.c_int32, C.c_float, C.c_float, C.c_float, _i32p, _i32p,
+                                           _f32p]),
         "tf_hip_attn_decode": (C.c_int, [C.c_int, _f32p, _f32p, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                          C.c_int32, C.c_int32, _f32p]),
         "tf_hip_attn_prefill": (C.c_int, [C.c_int, _f32p, _f32p, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
@@ -121,6 +124,8 @@ def host_lib() -> C.CDLL:
         "tfh_file_rope_tables": (C.c_int, [C.c_char_p, C.c_int32, _f32p, _f32p]),
         "tfh_quantize_row": (C.c_int, [C.c_int32, _f32p, C.c_int64, vp]),
         "tfh_gguf_summary": (C.c_int, [C.c_char_p, _u64p, C.c_char_p, C.c_int32]),
+        "tfh_tokenize_file": (C.c_int32, [C.c_char_p, C.c_char_p, C.c_int32, _i32p, C.c_int32]),
+        "tfh_detokenize_file": (C.c_int32, [C.c_char_p, _i32p, C.c_int32, C.c_char_p, C.c_int32]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -187,6 +192,29 @@ def rope_tables(theta: float, n_rot: int, n_pos: int):
     if host_lib().tfh_rope_tables(theta, n_rot, n_pos, _f(c), _f(s)) != 0:
         raise RuntimeError(host_lib().tfh_global_error().decode())
     return c, s
+
+
+def tokenize(path: str, text: bytes, add_bos: bool = True) -> np.ndarray:
+    """Tokenizer::encode (tokenizer.cpp:183-201) of text with the GGUF's vocabulary (host side)."""
+    L = host_lib()
+    cap = 4 * len(text) + 8
+    out = np.zeros(cap, np.int32)
+    n = L.tfh_tokenize_file(str(path).encode(), text, int(add_bos), _i(out), cap)
+    if n < 0:
+        raise RuntimeError(L.tfh_global_error().decode())
+    return out[:n].copy()
+
+
+def detokenize(path: str, ids) -> bytes:
+    """Tokenizer::decode (tokenizer.cpp:233-237) with the GGUF's vocabulary (host side)."""
+    L = host_lib()
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    cap = 64 * len(ids) + 16
+    buf = C.create_string_buffer(cap)
+    n = L.tfh_detokenize_file(str(path).encode(), _i(ids), len(ids), buf, cap)
+    if n < 0:
+        raise RuntimeError(L.tfh_global_error().decode())
+    return buf.raw[:n]
 
 
 def file_decode_bytes(path: str, pos: int) -> float:
@@ -262,6 +290,14 @@ class HipModel:
         self._check(self._L.tfh_generate(self._h, n, _i(out)))
         return out
 
+    def sample(self, temperature: float, top_p: float, r: float) -> int:
+        """sample_logits (sampler.cpp:15-52) of the last step's logits on the GPU for the draw r."""
+        tok = np.zeros(1, np.int32)
+        rc = hip_lib().tf_hip_sample(self._L.tfh_ctx(self._h), temperature, top_p, r, _i(tok))
+        if rc != 0:
+            raise RuntimeError(f"tf_hip_sample failed: {rc}")
+        return int(tok[0])
+
     def reset(self):
         self._check(self._L.tfh_reset(self._h))
 
@@ -270,8 +306,8 @@ class HipModel:
     def set_decode_path(self, path: int):
         """PATH_STEP: one persistent kernel per call where the model allows it (default);
         PATH_GRAPH: the captured per-layer graph, replayed per token; PATH_STREAM: the
-        persistent kernel with loader waves streaming the weights through LDS (Q8_0 models,
-        head size <= 128; others take PATH_STEP's choice)."""
+        persistent kernel with each wave streaming its weights through an LDS ring (Q8_0
+        models, head size <= 128; others take PATH_STEP's choice)."""
         H = hip_lib()
         rc = H.tf_hip_set_decode_path(self._L.tfh_ctx(self._h), int(path))
         if rc != 0:
@@ -404,6 +440,21 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, device: int = 0) -> np.nda
     out = np.zeros_like(x)
     _op(hip_lib().tf_hip_rmsnorm(device, _f(x), _f(w), x.shape[1], x.shape[0], eps, _f(out)), "tf_hip_rmsnorm")
     return out
+
+
+def sample_logits(logits: np.ndarray, temperature: float, top_p: float, r: float, device: int = 0,
+                  details: bool = False):
+    """sample_logits (sampler.cpp:15-52) of host logits on the GPU for the uniform draw r; with
+    details, also the sorted order and the final probabilities."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    n = x.shape[0]
+    tok = np.zeros(1, np.int32)
+    idx = np.zeros(n, np.int32) if details else None
+    p = np.zeros(n, np.float32) if details else None
+    _op(hip_lib().tf_hip_sample_logits(device, _f(x), n, temperature, top_p, r, _i(tok),
+                                       _i(idx) if details else None, _f(p) if details else None),
+        "tf_hip_sample_logits")
+    return (int(tok[0]), idx, p) if details else int(tok[0])
 
 
 def rope(x: np.ndarray, pos0: int, cos_tab: np.ndarray, sin_tab: np.ndarray, device: int = 0) -> np.ndarray:

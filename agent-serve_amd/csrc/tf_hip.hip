@@ -65,6 +65,10 @@ struct tf_hip_ctx {
     int S = 1;                    // attention splits per kv head
     int pos = 0;
     bool have_logits = false;
+    void* sample_work = nullptr;      // tf_hip_sample: sort buffers, probabilities, radix-sort scratch
+    size_t sample_bytes = 0;
+    int32_t* d_sampled = nullptr;     // the sampled token
+    Ctl* sample_ctl = nullptr;        // argmax of a greedy tf_hip_sample
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -1724,6 +1728,66 @@ int tf_hip_attn_decode_noalloc(int device, const float* q, const float* k_cache,
     a.fixed_pos = n_pos - 1;
     a.fixed_start = 0;
     return launch_attn_decode(a, (hipStream_t)stream) == hipSuccess ? 0 : TF_HIP_EDEVICE;
+}
+
+int tf_hip_sample(tf_hip_ctx* c, float temperature, float top_p, float r, int32_t* token) {
+    if (!c || !token || !(r >= 0.0f && r < 1.0f) || top_p != top_p || temperature != temperature)
+        return TF_HIP_EINVAL;
+    if (!c->have_logits) return fail(c, TF_HIP_ESTATE, "sample needs a prior prefill, decode or generate");
+    HIPCHK(c, hipSetDevice(c->device));
+    const int V = c->hp.n_vocab;
+    int rc;
+    if (!c->d_sampled) {
+        const size_t bytes = sample_work_bytes(V);
+        if ((rc = dalloc(c, (uint8_t**)&c->sample_work, bytes)) || (rc = dalloc(c, &c->d_sampled, 64)) ||
+            (rc = dalloc(c, &c->sample_ctl, sizeof(Ctl))))
+            return rc;
+        c->sample_bytes = bytes;
+    }
+    int32_t tok = 0;
+    if (temperature <= 0.0f) {
+        // sample_greedy (sampler.cpp:8-13), as sample_logits does for temperature <= 0
+        HIPCHK(c, hipMemsetAsync(c->sample_ctl, 0, sizeof(Ctl), c->st));
+        HIPCHK(c, launch_argmax(c->logits, V, c->sample_ctl, c->st));
+        Ctl h;
+        HIPCHK(c, hipMemcpyAsync(&h, c->sample_ctl, sizeof(Ctl), hipMemcpyDeviceToHost, c->st));
+        HIPCHK(c, hipStreamSynchronize(c->st));
+        tok = key_to_index(h.key);
+    } else {
+        HIPCHK(c, launch_sample(c->logits, V, temperature, top_p, r, c->sample_work, c->sample_bytes, c->d_sampled,
+                                nullptr, nullptr, c->st));
+        HIPCHK(c, hipMemcpyAsync(c->tok_host, c->d_sampled, 4, hipMemcpyDeviceToHost, c->st));
+        HIPCHK(c, hipStreamSynchronize(c->st));
+        tok = c->tok_host[0];
+    }
+    *token = tok;
+    return 0;
+}
+
+int tf_hip_sample_logits(int device, const float* logits, int32_t n, float temperature, float top_p, float r,
+                         int32_t* token, int32_t* sorted_idx, float* probs) {
+    if (!logits || !token || n <= 0 || !(r >= 0.0f && r < 1.0f) || top_p != top_p || temperature != temperature)
+        return TF_HIP_EINVAL;
+    if (temperature <= 0.0f) return tf_hip_argmax(device, logits, n, token);
+    OpScope s;
+    int rc = op_begin(device, s);
+    if (rc) return rc;
+    float *dl, *dp = nullptr;
+    int32_t *dt, *di = nullptr;
+    void* work;
+    const size_t bytes = sample_work_bytes(n);
+    OPCHK(s.alloc(&dl, (size_t)n * 4));
+    OPCHK(s.alloc(&dt, 64));
+    OPCHK(s.alloc((uint8_t**)&work, bytes));
+    if (sorted_idx) OPCHK(s.alloc(&di, (size_t)n * 4));
+    if (probs) OPCHK(s.alloc(&dp, (size_t)n * 4));
+    OPCHK(hipMemcpy(dl, logits, (size_t)n * 4, hipMemcpyHostToDevice));
+    OPCHK(launch_sample(dl, n, temperature, top_p, r, work, bytes, dt, di, dp, s.st));
+    OPCHK(hipMemcpyAsync(token, dt, 4, hipMemcpyDeviceToHost, s.st));
+    if (sorted_idx) OPCHK(hipMemcpyAsync(sorted_idx, di, (size_t)n * 4, hipMemcpyDeviceToHost, s.st));
+    if (probs) OPCHK(hipMemcpyAsync(probs, dp, (size_t)n * 4, hipMemcpyDeviceToHost, s.st));
+    OPCHK(hipStreamSynchronize(s.st));
+    return 0;
 }
 
 int tf_hip_argmax(int device, const float* x, int32_t n, int32_t* out) {

@@ -260,6 +260,12 @@ hipError_t launch_dequant_rows(const DevMat& m, int64_t row0, int64_t nrows, flo
 hipError_t launch_repack(int type, const uint8_t* raw, int64_t K, int64_t N, DevMat& m, hipStream_t st);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, int n, int rows, float eps, float* out,
                                hipStream_t st);
+// Temperature / nucleus sampling (k_sample.hip): device workspace bytes for n logits, and
+// the launches that sample one token into d_token (optional sorted order and final
+// probabilities into d_sorted_idx / d_probs, n each).
+size_t sample_work_bytes(int n);
+hipError_t launch_sample(const float* logits, int n, float temperature, float top_p, float r, void* work,
+                         size_t work_bytes, int32_t* d_token, int32_t* d_sorted_idx, float* d_probs, hipStream_t st);
 hipError_t launch_rope_rows(float* x, int seq, int n_heads, int hd, int pos0, const float* cos_tab,
                             const float* sin_tab, hipStream_t st);
 hipError_t launch_argmax(const float* x, int n, Ctl* ctl, hipStream_t st);

@@ -2,6 +2,7 @@
 // open a GGUF as a Model over the HIP backend, run it, and write synthetic GGUFs.
 // Every function returns 0 on success and a negative status on failure; the message
 // is tfh_last_error(handle) (or tfh_global_error() for calls without a model).
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <exception>
@@ -11,6 +12,7 @@
 
 #include "model.hpp"
 #include "synth.hpp"
+#include "tokenizer.hpp"
 
 namespace {
 
@@ -201,6 +203,34 @@ int tfh_rope_tables(float theta, int32_t n_rot, int32_t n_pos, float* cos_out, f
         std::memcpy(cos_out, c.data(), c.size() * 4);
         std::memcpy(sin_out, s.data(), s.size() * 4);
     });
+}
+
+// Tokenizer::encode (tokenizer.cpp:183-201) of text with the vocabulary of the GGUF at
+// path: writes up to cap ids to out and returns how many the text has (or < 0).
+int32_t tfh_tokenize_file(const char* path, const char* text, int32_t add_bos, int32_t* out, int32_t cap) {
+    int32_t n = -1;
+    guard(nullptr, [&] {
+        tfh::GgufFile g(path);
+        const tfh::Tokenizer tok(g);
+        const std::vector<int> ids = tok.encode(text, add_bos != 0);
+        for (size_t i = 0; i < ids.size() && (int32_t)i < cap; ++i) out[i] = ids[i];
+        n = (int32_t)ids.size();
+    });
+    return n;
+}
+
+// Tokenizer::decode (tokenizer.cpp:233-237) of ids with the vocabulary of the GGUF at path:
+// writes the bytes (up to cap) to out and returns their count (or < 0).
+int32_t tfh_detokenize_file(const char* path, const int32_t* ids, int32_t n, char* out, int32_t cap) {
+    int32_t len = -1;
+    guard(nullptr, [&] {
+        tfh::GgufFile g(path);
+        const tfh::Tokenizer tok(g);
+        const std::string s = tok.decode(std::vector<int>(ids, ids + n));
+        std::memcpy(out, s.data(), std::min(s.size(), (size_t)std::max(cap, 0)));
+        len = (int32_t)s.size();
+    });
+    return len;
 }
 
 }  // extern "C"

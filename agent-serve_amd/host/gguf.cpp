@@ -171,6 +171,7 @@ GgufFile::GgufFile(const std::string& path) {
                     break;
                 case 6: f32_[key] = r.get<float>(); break;
                 case 12: f32_[key] = (float)r.get<double>(); break;
+                case 7: bool_[key] = r.get<uint8_t>() != 0; break;
                 case 8: str_[key] = r.str(); break;
                 case 9: {
                     const uint8_t* save = r.p;
@@ -255,6 +256,11 @@ float GgufFile::f32(const std::string& key, float def) const {
 std::string GgufFile::str(const std::string& key, const std::string& def) const {
     auto it = str_.find(key);
     return it == str_.end() ? def : it->second;
+}
+
+bool GgufFile::boolean(const std::string& key, bool def) const {
+    auto it = bool_.find(key);
+    return it == bool_.end() ? def : it->second;
 }
 
 size_t GgufFile::arr_len(const std::string& key) const {

@@ -52,6 +52,7 @@ public:
     uint64_t u64(const std::string& key, uint64_t def = 0) const;
     float f32(const std::string& key, float def = 0) const;
     std::string str(const std::string& key, const std::string& def = "") const;
+    bool boolean(const std::string& key, bool def = false) const;
     size_t arr_len(const std::string& key) const;  // length of an array value, 0 if absent
     const std::vector<std::string>& arr_str(const std::string& key) const;
 
@@ -70,6 +71,7 @@ private:
     std::unordered_map<std::string, uint64_t> u64_;
     std::unordered_map<std::string, float> f32_;
     std::unordered_map<std::string, std::string> str_;
+    std::unordered_map<std::string, bool> bool_;
     std::unordered_map<std::string, size_t> arr_len_;
     std::unordered_map<std::string, std::vector<std::string>> arr_str_;
 };

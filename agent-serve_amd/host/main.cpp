@@ -1,9 +1,10 @@
 // tinferno_hip: the reference CLI (main.cpp:40-146) with the token loop on the MI355X.
 //
-// Same flags and output: prompt ids from --tokens (no BOS added, main.cpp:99), prefill,
-// then up to --n-predict tokens, stopping when the sampled id is eos after the first
-// (main.cpp:112-122); prefill/decode rates on stderr. Adds --device. --prompt needs
-// the reference's BPE tokenizer, which stays on the reference's side of the boundary.
+// Same flags and output: prompt ids from --tokens (no BOS added, main.cpp:99) or from
+// --prompt through the byte-level BPE tokenizer (BOS unless --no-bos), prefill, then up to
+// --n-predict tokens sampled on the GPU (greedy at --temp 0, else temperature / top-p with
+// the reference's std::mt19937 draws), stopping when the sampled id is eos after the first
+// (main.cpp:112-122); prefill/decode rates on stderr. Adds --device and --decode-path.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -17,6 +18,7 @@
 #include <vector>
 
 #include "model.hpp"
+#include "tokenizer.hpp"
 
 using namespace tfh;
 
@@ -38,7 +40,8 @@ void usage() {
                  "\n"
                  "usage: tinferno_hip --model PATH [options]\n"
                  "  --model PATH         GGUF file (F32 / F16 / Q8_0 / Q4_0 / Q4_1 / Q6_K)\n"
-                 "  --tokens 1,2,3       comma-separated prompt ids\n"
+                 "  --prompt TEXT        prompt string\n"
+                 "  --tokens 1,2,3       skip tokenizer; comma-separated ids\n"
                  "  --n-predict N        tokens to generate (default 64)\n"
                  "  --stage v0..v5       stage preset (default v2; selects the KV layout)\n"
                  "  --threads N          accepted for compatibility (the GPU does not use it)\n"
@@ -47,6 +50,7 @@ void usage() {
                  "  --seed N             rng seed (default 42)\n"
                  "  --max-seq N          KV cache length (default 4096)\n"
                  "  --kv-layout seq|head override KV layout\n"
+                 "  --no-bos             do not prepend BOS\n"
                  "  --device N           HIP device (default 0)\n"
                  "  --decode-path P      step (persistent kernel, the default) | graph\n"
                  "  --profile            print the per-kernel-class breakdown of one greedy pass\n");
@@ -61,55 +65,13 @@ std::vector<int> parse_tokens(const std::string& s) {
     return v;
 }
 
-// sample_logits of sampler.cpp:15-52 (temperature, top-p, std::mt19937).
-int sample_logits(const float* logits, int n, float temperature, float top_p, std::mt19937& rng) {
-    if (temperature <= 0.0f) {
-        int b = 0;
-        for (int i = 1; i < n; ++i)
-            if (logits[i] > logits[b]) b = i;
-        return b;
-    }
-    std::vector<int> idx((size_t)n);
-    std::iota(idx.begin(), idx.end(), 0);
-    std::sort(idx.begin(), idx.end(), [&](int a, int b) { return logits[a] > logits[b]; });
-    std::vector<float> p((size_t)n);
-    const float m = logits[idx[0]];
-    float s = 0;
-    for (int i = 0; i < n; ++i) {
-        p[(size_t)i] = std::exp((logits[idx[(size_t)i]] - m) / temperature);
-        s += p[(size_t)i];
-    }
-    for (int i = 0; i < n; ++i) p[(size_t)i] /= s;
-    int last = n;
-    if (top_p < 1.0f) {
-        float acc = 0;
-        last = 0;
-        for (int i = 0; i < n; ++i) {
-            acc += p[(size_t)i];
-            last = i + 1;
-            if (acc >= top_p) break;
-        }
-        float z = 0;
-        for (int i = 0; i < last; ++i) z += p[(size_t)i];
-        for (int i = 0; i < last; ++i) p[(size_t)i] /= z;
-    }
-    std::uniform_real_distribution<float> dist(0.0f, 1.0f);
-    const float r = dist(rng);
-    float acc = 0;
-    for (int i = 0; i < last; ++i) {
-        acc += p[(size_t)i];
-        if (r <= acc) return idx[(size_t)i];
-    }
-    return idx[(size_t)last - 1];
-}
-
 }  // namespace
 
 int main(int argc, char** argv) {
     std::string model_path, prompt, token_str, stage = "v2", kv_layout, decode_path = "step";
     int n_predict = 64, seed = 42, max_seq = 4096, device = 0;
     float temp = 0, topp = 0.9f;
-    bool profile = false;
+    bool profile = false, add_bos = true;
     for (int i = 1; i < argc; ++i) {
         std::string a = argv[i];
         auto next = [&]() -> std::string {
@@ -129,7 +91,8 @@ int main(int argc, char** argv) {
         else if (a == "--kv-layout") kv_layout = next();
         else if (a == "--device") device = std::stoi(next());
         else if (a == "--decode-path") decode_path = next();
-        else if (a == "--pin" || a == "--no-bos") {
+        else if (a == "--no-bos") add_bos = false;
+        else if (a == "--pin") {
         } else if (a == "--profile") profile = true;
         else if (a == "-h" || a == "--help") {
             usage();
@@ -154,9 +117,8 @@ int main(int argc, char** argv) {
         cfg.profile = profile;
         if (kv_layout == "head") cfg.kv_layout = KVLayout::HeadMajor;
         if (kv_layout == "seq") cfg.kv_layout = KVLayout::SeqMajor;
-        if (token_str.empty())
-            die(prompt.empty() ? "empty prompt" : "--prompt needs the reference tokenizer; pass --tokens");
         Model model(model_path, cfg);
+        const Tokenizer tok(model.gguf());
         if (decode_path == "graph" || decode_path == "step") {
             if (tf_hip_set_decode_path(model.ctx(), decode_path == "graph" ? TF_HIP_PATH_GRAPH : TF_HIP_PATH_STEP))
                 die("tf_hip_set_decode_path failed");
@@ -164,13 +126,9 @@ int main(int argc, char** argv) {
             die("--decode-path takes step or graph");
         }
         std::fprintf(stderr, "%s\n", model.describe().c_str());
-        std::vector<int> ids = parse_tokens(token_str);
+        const std::vector<int> ids = !token_str.empty() ? parse_tokens(token_str) : tok.encode(prompt, add_bos);
         if (ids.empty()) die("empty prompt");
 
-        const auto& vocab = model.gguf().arr_str("tokenizer.ggml.tokens");
-        auto piece = [&](int id) -> std::string {
-            return (id >= 0 && id < (int)vocab.size()) ? vocab[(size_t)id] : std::string();
-        };
         std::vector<float> logits((size_t)model.n_vocab());
         double t0 = now_s();
         model.prefill(ids.data(), (int)ids.size(), logits.data());
@@ -180,14 +138,12 @@ int main(int argc, char** argv) {
         std::vector<int> gen;
         t0 = now_s();
         for (int i = 0; i < n_predict; ++i) {
-            const int id = temp > 0 ? sample_logits(logits.data(), model.n_vocab(), temp, topp, rng)
-                                    : model.last_argmax();
+            const int id = model.sample(temp, topp, rng);
             if (id == model.eos() && i > 0) break;
             gen.push_back(id);
-            std::fputs(piece(id).c_str(), stdout);
-            std::fputc(' ', stdout);
+            std::fputs(tok.decode_one(id).c_str(), stdout);
             std::fflush(stdout);
-            model.decode(id, temp > 0 ? logits.data() : nullptr);
+            model.decode(id, nullptr);
         }
         const double t_decode = now_s() - t0;
         std::fputc('\n', stdout);

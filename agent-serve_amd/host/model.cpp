@@ -204,6 +204,15 @@ void Model::decode(int token, float* logits) {
     n_pos_ += 1;
 }
 
+int Model::sample(float temperature, float top_p, std::mt19937& rng) {
+    if (temperature <= 0.0f) return last_argmax_;
+    std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+    const float r = dist(rng);
+    int32_t tok = -1;
+    check(tf_hip_sample(ctx_, temperature, top_p, r, &tok), "sample");
+    return tok;
+}
+
 void Model::generate(int n, int32_t* out_tokens) {
     if (n <= 0) return;
     if (n > cfg_.max_seq - n_pos_) throw std::runtime_error("decode exceeds max_seq");

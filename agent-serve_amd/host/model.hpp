@@ -6,6 +6,7 @@
 
 #include <cstdint>
 #include <memory>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -86,6 +87,10 @@ public:
     int last_argmax() const { return last_argmax_; }
     // The greedy loop on the device: n tokens, as n x (sample_greedy + decode).
     void generate(int n, int32_t* out_tokens);
+    // sample_logits (sampler.cpp:15-52) of the last step's logits on the GPU: temperature
+    // <= 0 is the greedy argmax and draws nothing from rng; otherwise one
+    // uniform_real_distribution<float>(0, 1) draw, as the reference makes.
+    int sample(float temperature, float top_p, std::mt19937& rng);
 
     int n_vocab() const { return n_vocab_; }
     int n_embd() const { return n_embd_; }

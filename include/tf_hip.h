@@ -123,9 +123,9 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
  * uploaded). */
 #define TF_HIP_PATH_GRAPH 0
 #define TF_HIP_PATH_STEP 1
-/* TF_HIP_PATH_STREAM: the persistent kernel with a loader wave per CU streaming every
- * weight tile into LDS (Q8_0 models with head size <= 128); models it does not cover take
- * TF_HIP_PATH_STEP's choice. */
+/* TF_HIP_PATH_STREAM: the persistent kernel with every wave streaming its weight tiles
+ * through an LDS ring of its own at a bounded depth (Q8_0 models with head size <= 128);
+ * models it does not cover take TF_HIP_PATH_STEP's choice. */
 #define TF_HIP_PATH_STREAM 2
 int tf_hip_set_decode_path(tf_hip_ctx* ctx, int32_t path);
 int tf_hip_get_decode_path(tf_hip_ctx* ctx);
@@ -259,6 +259,23 @@ int tf_hip_attn_decode_noalloc(int device, const float* q, const float* k_cache,
  * rotated), out [seq][n_heads][hd]; hd 32, 64 or 128, n_heads / n_kv at most 8. */
 int tf_hip_attn_prefill(int device, const float* q, const float* k, const float* v, int32_t seq, int32_t n_heads,
                         int32_t n_kv, int32_t hd, float* out);
+
+/* sample_logits (sampler.cpp:15-52) over the logits of the context's last step (its last
+ * tf_hip_prefill, tf_hip_decode or tf_hip_generate), for the uniform draw r in [0, 1) that the
+ * reference takes from its std::mt19937 (uniform_real_distribution<float>(0, 1),
+ * sampler.cpp:44-45; the caller keeps the generator, main.cpp:109). temperature <= 0 is
+ * sample_greedy and leaves r unused, as the reference draws nothing then. The logits never
+ * leave the GPU; the reference's arithmetic (its libm's expf, the sums in sorted order) picks
+ * the reference's token for the same draw. Logits that compare equal are taken in ascending
+ * index order (std::sort leaves their order unspecified). TF_HIP_ESTATE before any step. */
+int tf_hip_sample(tf_hip_ctx* ctx, float temperature, float top_p, float r, int32_t* token);
+
+/* sample_logits (sampler.cpp:15-52) of n host logits for the draw r, as tf_hip_sample.
+ * sorted_idx / probs (n each, may be NULL) receive the descending order and the final
+ * probabilities in that order (after the nucleus renormalisation; entries past the nucleus
+ * hold p_i / sum). */
+int tf_hip_sample_logits(int device, const float* logits, int32_t n, float temperature, float top_p, float r,
+                         int32_t* token, int32_t* sorted_idx, float* probs);
 
 /* sample_greedy (sampler.cpp:8-13): index of the first maximum. */
 int tf_hip_argmax(int device, const float* x, int32_t n, int32_t* out);

@@ -54,6 +54,8 @@ def oracle_lib() -> C.CDLL:
                                    _f32p]),
         "orc_attn_prefill": (None, [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, _f32p]),
         "orc_argmax": (C.c_int, [_f32p, C.c_int]),
+        "orc_uniform_draws": (None, [C.c_uint32, C.c_int, _f32p]),
+        "orc_sample_logits": (C.c_int, [_f32p, C.c_int, C.c_float, C.c_float, C.c_float, _i32p, _f32p, _i32p]),
         "orc_open": (vp, [C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_char_p, C.c_int]),
         "orc_close": (None, [vp]),
         "orc_prefill": (C.c_int, [vp, _i32p, C.c_int, _f32p]),
@@ -91,6 +93,10 @@ def ref_lib() -> C.CDLL:
         "ref_dequant_row": (C.c_int, [C.c_int, vp, C.c_int64, _f32p]),
         "ref_matmul": (C.c_int, [_f32p, _f32p, C.c_int, C.c_int, vp, C.c_int64, C.c_int64, C.c_int]),
         "ref_dot_f32": (C.c_float, [_f32p, _f32p, C.c_int]),
+        "ref_sample_logits_seq": (None, [_f32p, C.c_int, C.c_float, C.c_float, C.c_uint32, C.c_int, _i32p]),
+        "ref_uniform_draws": (None, [C.c_uint32, C.c_int, _f32p]),
+        "ref_tokenize": (C.c_int32, [C.c_char_p, C.c_char_p, C.c_int32, _i32p, C.c_int32]),
+        "ref_detokenize": (C.c_int32, [C.c_char_p, _i32p, C.c_int32, C.c_char_p, C.c_int32]),
         "ref_rmsnorm": (None, [_f32p, _f32p, _f32p, C.c_int, C.c_float]),
         "ref_silu_mul": (None, [_f32p, _f32p, C.c_int]),
         "ref_softmax": (None, [_f32p, C.c_int]),

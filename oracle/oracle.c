@@ -381,6 +381,106 @@ int orc_argmax(const float* x, int n) {
     return b;
 }
 
+/* ------------------------------------------------------------------ sampler.cpp:15-52 */
+
+typedef struct {
+    uint32_t mt[624];
+    int i;
+} orc_mt19937;
+
+static void mt_seed(orc_mt19937* m, uint32_t seed) {
+    m->mt[0] = seed;
+    for (int i = 1; i < 624; ++i) m->mt[i] = 1812433253u * (m->mt[i - 1] ^ (m->mt[i - 1] >> 30)) + (uint32_t)i;
+    m->i = 624;
+}
+
+static uint32_t mt_next(orc_mt19937* m) {
+    if (m->i >= 624) {
+        for (int k = 0; k < 624; ++k) {
+            const uint32_t y = (m->mt[k] & 0x80000000u) | (m->mt[(k + 1) % 624] & 0x7fffffffu);
+            m->mt[k] = m->mt[(k + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+        }
+        m->i = 0;
+    }
+    uint32_t y = m->mt[m->i++];
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    y ^= y >> 18;
+    return y;
+}
+
+void orc_uniform_draws(uint32_t seed, int n, float* out) {
+    orc_mt19937 m;
+    mt_seed(&m, seed);
+    for (int i = 0; i < n; ++i) {
+        float r = (float)mt_next(&m) / 4294967296.0f;
+        if (r >= 1.0f) r = nextafterf(1.0f, 0.0f);
+        out[i] = r;
+    }
+}
+
+typedef struct {
+    float v;
+    int32_t i;
+} orc_vi;
+
+static int cmp_desc(const void* a, const void* b) {
+    const orc_vi* x = (const orc_vi*)a;
+    const orc_vi* y = (const orc_vi*)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return (x->i > y->i) - (x->i < y->i);
+}
+
+int orc_sample_logits(const float* logits, int n, float temperature, float top_p, float r, int32_t* sorted_idx,
+                      float* probs, int* n_last) {
+    if (temperature <= 0.0f) return orc_argmax(logits, n);
+    orc_vi* o = (orc_vi*)malloc((size_t)n * sizeof(orc_vi));
+    float* p = (float*)malloc((size_t)n * sizeof(float));
+    for (int i = 0; i < n; ++i) {
+        o[i].v = logits[i];
+        o[i].i = i;
+    }
+    qsort(o, (size_t)n, sizeof(orc_vi), cmp_desc);
+    const float m = o[0].v;
+    float s = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        p[i] = expf((o[i].v - m) / temperature);
+        s += p[i];
+    }
+    for (int i = 0; i < n; ++i) p[i] /= s;
+    int last = n;
+    if (top_p < 1.0f) {
+        float acc = 0.0f;
+        last = 0;
+        for (int i = 0; i < n; ++i) {
+            acc += p[i];
+            last = i + 1;
+            if (acc >= top_p) break;
+        }
+        float z = 0.0f;
+        for (int i = 0; i < last; ++i) z += p[i];
+        for (int i = 0; i < last; ++i) p[i] /= z;
+    }
+    int tok = o[last - 1].i;
+    float acc = 0.0f;
+    for (int i = 0; i < last; ++i) {
+        acc += p[i];
+        if (r <= acc) {
+            tok = o[i].i;
+            break;
+        }
+    }
+    if (sorted_idx)
+        for (int i = 0; i < n; ++i) sorted_idx[i] = o[i].i;
+    if (probs) memcpy(probs, p, (size_t)n * sizeof(float));
+    if (n_last) *n_last = last;
+    free(o);
+    free(p);
+    return tok;
+}
+
 /* ------------------------------------------------------------------ GGUF (gguf.cpp:88-168) */
 
 typedef struct {

@@ -52,6 +52,17 @@ void orc_attn_prefill(float* out, const float* q, const float* k, const float* v
 
 /* sampler.cpp:8-13: first maximum wins */
 int orc_argmax(const float* x, int n);
+/* The draws of sample_logits (sampler.cpp:44-45) from std::mt19937(seed): the 32-bit
+ * Mersenne Twister (Matsumoto & Nishimura 1998), and libstdc++'s
+ * uniform_real_distribution<float>(0, 1) over it (generate_canonical<float, 24>: one
+ * draw u, (float)u / 2^32, 1 - 2^-24 when that rounds to 1). n draws in order. */
+void orc_uniform_draws(uint32_t seed, int n, float* out);
+/* sample_logits (sampler.cpp:15-52) for the uniform draw r: temperature <= 0 is greedy.
+ * Optional outputs (may be NULL): the order (descending logits, ties: lower index first;
+ * std::sort leaves the order of ties unspecified), the final probabilities in that order
+ * (after the nucleus renormalisation) and the nucleus size. */
+int orc_sample_logits(const float* logits, int n, float temperature, float top_p, float r, int32_t* sorted_idx,
+                      float* probs, int* n_last);
 
 /* model.cpp: Model(path, cfg), prefill, decode, reset */
 typedef struct orc_model orc_model;

@@ -5,11 +5,13 @@
 // tests can pin the oracle (oracle.c) against the real reference bit for bit, and so
 // that bench.py can time the reference --stage v2 path as the CPU baseline. Nothing
 // in the product loads it.
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <exception>
 #include <string>
 #include <thread>
+#include <random>
 #include <vector>
 
 #include "attention.hpp"
@@ -18,6 +20,7 @@
 #include "model.hpp"
 #include "quant.hpp"
 #include "sampler.hpp"
+#include "tokenizer.hpp"
 
 using namespace tinf;
 
@@ -76,6 +79,49 @@ void ref_rmsnorm(float* out, const float* x, const float* w, int n, float eps) {
 void ref_silu_mul(float* g, const float* u, int n) { silu_mul(g, u, n); }
 void ref_softmax(float* x, int n) { softmax(x, n); }
 int ref_argmax(const float* x, int n) { return sample_greedy(x, n); }
+
+// The reference's sampling loop (main.cpp:109-116): one std::mt19937(seed), then n_draws
+// calls of sample_logits on the same logits.
+void ref_sample_logits_seq(const float* logits, int n, float temperature, float top_p, uint32_t seed, int n_draws,
+                           int32_t* out) {
+    std::mt19937 rng(seed);
+    for (int i = 0; i < n_draws; ++i) out[i] = sample_logits(logits, n, temperature, top_p, rng);
+}
+
+// Tokenizer::encode / decode of the reference over the GGUF at path (ids up to cap; returns
+// the full count, or -1 with ref_last_error()).
+int32_t ref_tokenize(const char* path, const char* text, int32_t add_bos, int32_t* out, int32_t cap) {
+    try {
+        GGUF g(path);
+        Tokenizer tok(g);
+        const std::vector<int> ids = tok.encode(text, add_bos != 0);
+        for (size_t i = 0; i < ids.size() && (int32_t)i < cap; ++i) out[i] = ids[i];
+        return (int32_t)ids.size();
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+int32_t ref_detokenize(const char* path, const int32_t* ids, int32_t n, char* out, int32_t cap) {
+    try {
+        GGUF g(path);
+        Tokenizer tok(g);
+        const std::string s = tok.decode(std::vector<int>(ids, ids + n));
+        std::memcpy(out, s.data(), std::min(s.size(), (size_t)(cap > 0 ? cap : 0)));
+        return (int32_t)s.size();
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// The uniform draws sample_logits makes (sampler.cpp:44-45) from std::mt19937(seed).
+void ref_uniform_draws(uint32_t seed, int n, float* out) {
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+    for (int i = 0; i < n; ++i) out[i] = dist(rng);
+}
 
 void ref_rope_freqs(float* freq, int n_rot, float theta, int llama3, float scale, float lo, float hi, float orig) {
     RopeParams rp;

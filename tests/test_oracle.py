@@ -342,3 +342,78 @@ def test_model_errors(gguf, tmp_path):
     bad.write_bytes(raw[: len(raw) // 2])
     with pytest.raises(RuntimeError, match="out of range"):
         OracleModel(str(bad))
+
+
+# ---------------------------------------------------------------- sampler.cpp:15-52
+
+
+def draws(L, seed, n):
+    out = np.zeros(n, np.float32)
+    L.orc_uniform_draws(seed, n, F(out))
+    return out
+
+
+def test_mt19937_known_answer():
+    """The C++ standard fixes mt19937's 10000th output of the default seed (5489) at
+    4123659995 ([rand.predef]); the draw is that word as a float over 2^32."""
+    L = oracle_lib()
+    r = draws(L, 5489, 10000)
+    assert r[-1] == np.float32(np.float32(4123659995) / np.float32(4294967296.0))
+    assert np.all((r >= 0) & (r < 1))
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [0, 1, 42, 2**31 + 5, 2**32 - 1])
+def test_uniform_draws_match_reference(seed):
+    L, R = oracle_lib(), ref_lib()
+    want = np.zeros(3000, np.float32)
+    R.ref_uniform_draws(seed, 3000, F(want))
+    assert np.array_equal(draws(L, seed, 3000).view(np.uint32), want.view(np.uint32))
+
+
+def sample(L, logits, temp, top_p, r, with_probs=False):
+    n = len(logits)
+    idx = np.zeros(n, np.int32)
+    p = np.zeros(n, np.float32)
+    last = np.zeros(1, np.int32)
+    tok = L.orc_sample_logits(F(logits), n, temp, top_p, r, idx.ctypes.data_as(C.POINTER(C.c_int32)), F(p),
+                              last.ctypes.data_as(C.POINTER(C.c_int32)))
+    return (tok, idx, p, int(last[0])) if with_probs else tok
+
+
+def test_sample_logits_closed_forms():
+    """Two tokens with logits 0 and ln 3 at temperature 1: probabilities 3/4 and 1/4 in the
+    order (1, 0); the draw picks token 1 up to 3/4. Nucleus 0.5 keeps token 1 alone.
+    Temperature 0 is the first maximum."""
+    L = oracle_lib()
+    x = np.array([0.0, np.log(3.0)], np.float32)
+    tok, idx, p, last = sample(L, x, 1.0, 1.0, 0.5, True)
+    assert tok == 1 and list(idx) == [1, 0] and last == 2
+    assert abs(p[0] - 0.75) < 1e-7 and abs(p[1] - 0.25) < 1e-7
+    assert sample(L, x, 1.0, 1.0, 0.9) == 0
+    assert sample(L, x, 1.0, 0.5, 0.99) == 1
+    assert sample(L, np.array([1, 5, 5, 2], np.float32), 0.0, 0.9, 0.5) == 1
+    # lower temperature sharpens: at T = 0.25 token 1 holds 3^4 / (3^4 + 1)
+    tok, idx, p, last = sample(L, x, 0.25, 1.0, 0.5, True)
+    assert abs(p[0] - 81 / 82) < 1e-6
+
+
+SAMPLE_CASES = [  # vocab, logit scale, temperature, top_p
+    (7, 1.0, 1.0, 1.0), (64, 3.0, 0.7, 0.9), (1000, 0.05, 1.0, 0.9), (4096, 2.0, 1.3, 0.5),
+    (32000, 0.02, 0.8, 0.95), (151936, 1.0, 1.0, 0.9),
+]
+
+
+@needs_ref
+@pytest.mark.parametrize("n,scale,temp,top_p", SAMPLE_CASES)
+def test_sample_logits_matches_reference(n, scale, temp, top_p):
+    """The oracle's sampler, fed the reference's own draws, picks the reference's tokens
+    (main.cpp:109-116: one generator, one draw per token)."""
+    L, R = oracle_lib(), ref_lib()
+    rng = np.random.default_rng(n)
+    logits = (rng.standard_normal(n) * scale).astype(np.float32)
+    k = 40 if n > 10000 else 200
+    want = np.zeros(k, np.int32)
+    R.ref_sample_logits_seq(F(logits), n, temp, top_p, 1234 + n, k, want.ctypes.data_as(C.POINTER(C.c_int32)))
+    got = [sample(L, logits, temp, top_p, float(r)) for r in draws(L, 1234 + n, k)]
+    assert got == want.tolist()
