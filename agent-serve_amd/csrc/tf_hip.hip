@@ -986,6 +986,14 @@ int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out) {
         const long v = std::strtol(sf, &end, 10);
         if (end != sf && *end == 0 && v >= 0 && v <= kSplitFromMax) c->split_from = (int)v;
     }
+    // TF_HIP_DECODE_PATH=step|graph|stream: the initial decode path, for callers that do not
+    // call tf_hip_set_decode_path (other values are ignored)
+    if (const char* dp = std::getenv("TF_HIP_DECODE_PATH")) {
+        const std::string v(dp);
+        if (v == "step") c->path_opt = TF_HIP_PATH_STEP;
+        if (v == "graph") c->path_opt = TF_HIP_PATH_GRAPH;
+        if (v == "stream") c->path_opt = TF_HIP_PATH_STREAM;
+    }
     c->hp = p;
     c->H = p.n_head * p.head_dim;
     c->KVd = p.n_kv_head * p.head_dim;

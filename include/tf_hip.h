@@ -120,7 +120,10 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
  * per-layer kernels replayed per token. Both compute the same function; neither has a
  * counterpart in the reference (a backend choice below Model::decode, model.cpp:197-208).
  * tf_hip_get_decode_path returns the path the next call will take (needs every tensor
- * uploaded). */
+ * uploaded). The environment variable TF_HIP_DECODE_PATH (step, graph or stream), read by
+ * tf_hip_create, sets the initial path for callers that never call the setter. The step
+ * and stream paths launch cooperatively: one process at a time can hold the GPU's
+ * cooperative-launch resource, so a second process on the same GPU needs the graph path. */
 #define TF_HIP_PATH_GRAPH 0
 #define TF_HIP_PATH_STEP 1
 /* TF_HIP_PATH_STREAM: the persistent kernel with every wave streaming its weight tiles

@@ -358,3 +358,26 @@ def test_long_context_workload_vs_reference_fixture(pkg, gguf):
         print(f"qwen15b 4096 + {len(ids)}: ids identical, top-8 logits rel err {worst:.2e}")
     finally:
         hip.close()
+
+
+@pytest.mark.parametrize("preset,layout", [("tiny_q8", "seq"), ("tiny_qwen", "head"), ("tiny_mixq4", "seq")])
+def test_reference_cli_with_gpu_backend(pkg, gguf, preset, layout):
+    """The reference's own CLI and Model with the backend switch patched in
+    (oracle/backend_patch.py): `--backend hip` prints the same greedy tokens as its CPU path.
+    (This process holds the cooperative-launch resource, so the child runs the graph path.)"""
+    import os
+    import pathlib
+    import subprocess
+
+    exe = pathlib.Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "tinferno_backend"
+    if not exe.exists():
+        pytest.skip("oracle/_ref/tinferno_backend not built (needs the reference sources)")
+    info = pkg.synth_preset_info(preset)
+    toks = ",".join(str(t) for t in pkg.synth_prompt(info["seed"], 6, info["n_vocab"]))
+    args = [str(exe), "--model", gguf(preset), "--tokens", toks, "--n-predict", "16", "--max-seq", "64",
+            "--kv-layout", layout, "--threads", "4"]
+    env = dict(os.environ, TF_HIP_DECODE_PATH="graph")
+    cpu = subprocess.run(args, capture_output=True, text=True, timeout=300, env=env)
+    gpu = subprocess.run(args + ["--backend", "hip"], capture_output=True, text=True, timeout=300, env=env)
+    assert cpu.returncode == 0 and gpu.returncode == 0, cpu.stderr[-500:] + gpu.stderr[-500:]
+    assert gpu.stdout == cpu.stdout and cpu.stdout.strip()
