@@ -68,6 +68,60 @@ def step_counters(fetch_csv: str, write_csv: str) -> None:
     print(f"traffic_bytes_per_token k_step {fm * 1024 * 2.0 + wm * 1024 * 1.0:.0f}")
 
 
+def pf_classifier():
+    """Kernel name -> prefill class, for dispatches in launch order (the attn_output and
+    ffn_down GEMMs share a kernel and alternate); None for kernels outside the prefill."""
+    resid = [0]
+
+    def classify(k: str):
+        if "k_pf_" not in k and "k_embed_rows" not in k:
+            return None
+        if "k_pf_reduce" in k:
+            return "splitk_reduce"
+        if re.search(r"k_pf_gemm_(q8|big|split)<0", k):
+            return "qkv_gemm"
+        if re.search(r"k_pf_gemm_(q8|big|split)<1", k):
+            resid[0] += 1
+            return "wo_gemm" if resid[0] % 2 == 1 else "down_gemm"
+        if re.search(r"k_pf_gemm_(q8|big|split)<2", k):
+            return "gateup_gemm"
+        if "k_pf_attn" in k:
+            return "attention"
+        return re.sub(r"^_ZN3tfk12_GLOBAL__N_1\d+", "", short(k)).split("(")[0].split("E")[0]
+
+    return classify
+
+
+def mfma(counter_csv: str, simds: int, xcds: int) -> None:
+    """Matrix-core work per prefill class from one --pmc pass with SQ_INSTS_VALU_MFMA_MOPS_F16,
+    SQ_INSTS_VALU_MFMA_MOPS_F32, SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE: MFMA FLOP
+    (MOPS x 512) per call and the share of SIMD cycles the matrix cores were busy
+    (busy cycles / (one XCD's active cycles x SIMDs), as rocprofv3's MfmaUtil)."""
+    rows = collections.defaultdict(dict)  # dispatch id -> counter -> value
+    names = {}
+    for r in csv.DictReader(open(counter_csv)):
+        d, c, v = int(r["Dispatch_Id"]), r["Counter_Name"], float(r["Counter_Value"])
+        rows[d][c] = rows[d].get(c, 0.0) + v
+        names[d] = r["Kernel_Name"]
+    classify = pf_classifier()
+    acc = collections.defaultdict(lambda: [0, 0.0, 0.0, 0.0, 0.0])
+    for d in sorted(rows):
+        c = classify(names[d])
+        if c is None:
+            continue
+        v = rows[d]
+        a = acc[c]
+        a[0] += 1
+        a[1] += v.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) * 512
+        a[2] += v.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0) * 512
+        a[3] += v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+        # GRBM_GUI_ACTIVE comes summed over the XCDs: one XCD's active cycles are value / xcds
+        a[4] += v.get("GRBM_GUI_ACTIVE", 0.0) / xcds * simds
+    print(f"{'class':16s} {'calls':>6s} {'F16 GFLOP/call':>15s} {'F32 GFLOP/call':>15s} {'MFMA busy':>10s}")
+    for c, (n, f16, f32, busy, active) in sorted(acc.items(), key=lambda kv: -kv[1][3]):
+        print(f"{c:16s} {n:6d} {f16 / n / 1e9:15.2f} {f32 / n / 1e9:15.2f} {busy / max(active, 1):10.1%}")
+
+
 def prefill(trace_csv: str, n: int, dims: str) -> None:
     """Per kernel class of one prompt prefill (the k_pf_* dispatches of the trace): launches,
     average and total microseconds, algorithmic FLOP per launch and TFLOP/s. Dense GEMM
@@ -83,26 +137,12 @@ def prefill(trace_csv: str, n: int, dims: str) -> None:
         "attention": 4.0 * hd * (n * (n + 1) / 2) * H,
     }
     acc: dict[str, list[float]] = collections.defaultdict(list)
-    resid = 0
+    classify = pf_classifier()
     for r in csv.DictReader(open(trace_csv)):
-        k = r["Kernel_Name"]
-        if "k_pf_" not in k and "k_embed_rows" not in k:
+        c = classify(r["Kernel_Name"])
+        if c is None:
             continue
-        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-        if "k_pf_reduce" in k:
-            c = "splitk_reduce"
-        elif re.search(r"k_pf_gemm_(q8|big|split)<0", k):
-            c = "qkv_gemm"
-        elif re.search(r"k_pf_gemm_(q8|big|split)<1", k):
-            c = "wo_gemm" if resid % 2 == 0 else "down_gemm"
-            resid += 1
-        elif re.search(r"k_pf_gemm_(q8|big|split)<2", k):
-            c = "gateup_gemm"
-        elif "k_pf_attn" in k:
-            c = "attention"
-        else:
-            c = re.sub(r"^_ZN3tfk12_GLOBAL__N_1\d+", "", short(k)).split("(")[0].split("E")[0]
-        acc[c].append(us)
+        acc[c].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     total = sum(sum(v) for v in acc.values())
     print(f"prefill of {n} tokens, {L} layers: {total / 1e3:.3f} ms in k_pf_* kernels")
     print(f"{'class':16s} {'calls':>6s} {'avg_us':>9s} {'total_ms':>9s} {'share':>6s} {'GFLOP/call':>11s} {'TFLOP/s':>8s}")
@@ -155,17 +195,21 @@ def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> None:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["trace", "traffic", "steps", "stepcounters", "prefill"])
+    ap.add_argument("what", choices=["trace", "traffic", "steps", "stepcounters", "prefill", "mfma"])
     ap.add_argument("files", nargs="+")
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--tokens", type=int, default=512)
     ap.add_argument("--dims", default="2048,8192,16,32,8", help="D,F,L,H,G")
+    ap.add_argument("--simds", type=int, default=1024, help="SIMDs of the GPU (MI355X: 256 CUs x 4)")
+    ap.add_argument("--xcds", type=int, default=8, help="XCDs of the GPU (MI355X: 8)")
     a = ap.parse_args()
     if a.what == "trace":
         trace(a.files[0], a.steps)
     elif a.what == "prefill":
         prefill(a.files[0], a.tokens, a.dims)
+    elif a.what == "mfma":
+        mfma(a.files[0], a.simds, a.xcds)
     elif a.what == "stepcounters":
         step_counters(a.files[0], a.files[1])
     elif a.what == "steps":
