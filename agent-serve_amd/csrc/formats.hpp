@@ -62,6 +62,19 @@ struct Fmt<TF_HIP_TYPE_Q8_0> {
         }
         return h2f(w.d) * t;
     }
+    // dot() with the step's 16 inputs already loaded (the same operations in the same order)
+    __device__ static float dot_x(const Raw& w, const float4 (&x)[4]) {
+        float t = 0.0f;
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            t = fmaf(x[i].x, sb0(q[i]), t);
+            t = fmaf(x[i].y, sb1(q[i]), t);
+            t = fmaf(x[i].z, sb2(q[i]), t);
+            t = fmaf(x[i].w, sb3(q[i]), t);
+        }
+        return h2f(w.d) * t;
+    }
     __device__ static void dequant(const Raw& w, float* out) {
         const float d = h2f(w.d);
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};

@@ -53,7 +53,9 @@ size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg,
     const size_t table = ((size_t)n_layer * sizeof(StepLayer) + 15) / 16 * 16;
     const size_t floats = (size_t)(D + 3) / 4 * 4 + (size_t)(region + 3) / 4 * 4 + (size_t)(n_rep + 2) * hd +
                           (size_t)n_rep * (hd + 2);
-    const size_t staged = (stage_lds & 1) ? 16 + (size_t)step_detail::kNW * step_detail::row_slot_bytes(F) : 0;
+    const size_t staged = (stage_lds & 2)   ? 16 + (size_t)step_detail::kNW * step_detail::down_slot_bytes(D, F, n_wg)
+                          : (stage_lds & 1) ? 16 + (size_t)step_detail::kNW * step_detail::row_slot_bytes(F)
+                                            : 0;
     return table + 4 * floats + staged;
 }
 
@@ -63,29 +65,16 @@ int step_stage_lds(int tl, int n_layer, int D, int F, int H, int G, int hd, int 
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
         return 0;
-    if (D > n_wg * step_detail::kNW) return 0;
     // the kernel's static LDS (StepConst, reductions) stays under 2 KiB
-    return step_lds_bytes(n_layer, D, F, H, G, hd, n_wg, 1) + 2048 <= (size_t)max_lds ? 1 : 0;
+    auto fits = [&](int mode) { return step_lds_bytes(n_layer, D, F, H, G, hd, n_wg, mode) + 2048 <= (size_t)max_lds; };
+    // fewer down rows than half the waves: split each workgroup's rows over K (every wave
+    // busy) instead of leaving most waves without a row (measured on the Qwen2.5-0.5B shape,
+    // 896 rows: 0.668 against 0.688 ms per token; with 1536 and 2048 rows the row per wave is
+    // faster)
+    if (2 * D < n_wg * step_detail::kNW && step_detail::down_split_ok(D, F, n_wg) && fits(2)) return 2;
+    if (D <= n_wg * step_detail::kNW && fits(1)) return 1;
+    return 0;
 }
-
-namespace {
-
-template <int TL, int TO, int HDM, int TA = TL>
-hipError_t launch_t(const StepArgs& a, int n_wg, hipStream_t st) {
-    const void* fn = (const void*)step_detail::k_step<TL, TO, HDM, TA>;
-    const size_t lds = step_lds_bytes(a.n_layer, a.D, a.F, a.H, a.G, a.hd, n_wg, a.stage_lds);
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    int per_cu = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kStepThreads, lds);
-    if (e != hipSuccess) return e;
-    if (per_cu < 1 || n_wg > per_cu * device_cu_count()) return hipErrorCooperativeLaunchTooLarge;
-    StepArgs arg = a;
-    void* params[] = {(void*)&arg};
-    return hipLaunchCooperativeKernel(fn, dim3(n_wg), dim3(kStepThreads), params, (unsigned)lds, st);
-}
-
-}  // namespace
 
 int step_alt_type(int tl) { return tl == TF_HIP_TYPE_Q4_0 ? TF_HIP_TYPE_Q4_1 : tl; }
 
@@ -97,9 +86,12 @@ bool step_supported(int tl, int to, int hd, int n_rep) {
 }
 
 hipError_t launch_step(const StepArgs& a, int tl, int to, int n_wg, hipStream_t st) {
-    if (tl == TF_HIP_TYPE_Q8_0 && to == TF_HIP_TYPE_Q8_0)
-        return a.hd <= 64 ? launch_t<TF_HIP_TYPE_Q8_0, TF_HIP_TYPE_Q8_0, 64>(a, n_wg, st)
-                          : launch_t<TF_HIP_TYPE_Q8_0, TF_HIP_TYPE_Q8_0, 128>(a, n_wg, st);
+    using step_detail::launch_t;
+    constexpr int Q8 = TF_HIP_TYPE_Q8_0;
+    if (tl == Q8 && to == Q8) {
+        if (a.stage_lds & 2) return launch_step_split(a, n_wg, st);
+        return a.hd <= 64 ? launch_t<Q8, Q8, 64>(a, n_wg, st) : launch_t<Q8, Q8, 128>(a, n_wg, st);
+    }
     if (tl == TF_HIP_TYPE_F32 && to == TF_HIP_TYPE_F32 && a.hd <= 64)
         return launch_t<TF_HIP_TYPE_F32, TF_HIP_TYPE_F32, 64>(a, n_wg, st);
     if (tl == TF_HIP_TYPE_Q4_0 && to == TF_HIP_TYPE_Q6_K && a.hd <= 64)

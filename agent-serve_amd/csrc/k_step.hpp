@@ -663,10 +663,32 @@ __host__ __device__ inline int split_all_parts(int H, int hd, int n_wg) {
     return parts;
 }
 
-// LDS bytes of one staged Q8_0 row of K elements: the q bytes padded to whole 1 KiB load
-// instructions, then the fp16 scales padded to 256-byte ones.
+// LDS bytes of one staged Q8_0 row of K elements (ffn_down staged one row per wave): the q
+// bytes padded to whole 1 KiB load instructions, then the fp16 scales padded to 256-byte ones.
 __host__ __device__ inline int row_slot_bytes(int K) {
     return (K + 1023) / 1024 * 1024 + (K / 16 + 255) / 256 * 256;
+}
+
+// ffn_down staged in LDS, split over K inside each workgroup (models with fewer down rows
+// than half the waves, where one row per wave would leave most waves idle): workgroup w takes rows
+// [w * R, w * R + R) of the D rows (R = down_rows), wave v a run of the F columns in units
+// of 64 (two Q8_0 blocks, so a wave's fp16 scales are whole 4-byte words): the first F/64 % 8
+// waves take one unit more. The waves of a workgroup thus read one eighth of the FFN's
+// hidden vector each instead of all of it; the 8 partial sums of a row are added in wave
+// order. A wave's slot: the R rows' q bytes (the largest run each), then their scales
+// (4 bytes per unit, 16-byte aligned per row).
+constexpr int kDownRowsMax = 4;  // R limit (d_model <= 4 x workgroups: the layout is for few rows)
+__host__ __device__ inline int down_rows(int D, int n_wg) { return (D + n_wg - 1) / n_wg; }
+__host__ __device__ inline int down_units_max(int F) { return (F / 64 + kNW - 1) / kNW; }
+__host__ __device__ inline int down_unit0(int F, int v) { return v * (F / 64 / kNW) + min(v, F / 64 % kNW); }
+__host__ __device__ inline int down_units(int F, int v) { return F / 64 / kNW + (v < F / 64 % kNW ? 1 : 0); }
+__host__ __device__ inline int down_qstride(int F) { return 64 * down_units_max(F); }
+__host__ __device__ inline int down_dstride(int F) { return (4 * down_units_max(F) + 15) / 16 * 16; }
+__host__ __device__ inline int down_slot_bytes(int D, int F, int n_wg) {
+    return down_rows(D, n_wg) * (down_qstride(F) + down_dstride(F));
+}
+__host__ __device__ inline bool down_split_ok(int D, int F, int n_wg) {
+    return F % 64 == 0 && F / 64 >= kNW && down_units_max(F) <= kWave && down_rows(D, n_wg) <= kDownRowsMax;
 }
 
 // Launch constants, kept in LDS: phases re-read what they need after their barriers
@@ -686,7 +708,9 @@ struct StepConst {
 
 // TL: the layer matrices' format; TA: a second format wo and ffn_down may have, layer by
 // layer (the runtime type picks the instantiation); TO: the lm_head's (and embedding's).
-template <int TL, int TO, int HDM, int TA>
+// DSPLIT: ffn_down staged split over K in each workgroup (else a row per wave, when staged);
+// a template argument so that the row-per-wave build carries none of the split's code.
+template <int TL, int TO, int HDM, int TA, bool DSPLIT>
 __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
     using FE = Fmt<TO>;  // the embedding table has the lm_head's format (checked by the host)
     constexpr bool kSums = Fmt<TL>::kNeedSums || Fmt<TA>::kNeedSums;  // inputs of wo and ffn_down
@@ -700,6 +724,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
     StepConst& sc = *reinterpret_cast<StepConst*>(sc_raw);
     __shared__ double red[kNW];
     __shared__ u64 wbest[kNW];
+    __shared__ float dpart[DSPLIT ? kNW * kDownRowsMax : 1];  // split ffn_down: partial sums [wave][row]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -731,8 +756,8 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         c.o_x16 = c.o_xs + 4 * kmax;
         c.o_qkv = c.o_xs + 4 * ((region_floats(c.D, c.F, c.n_rep, c.hd, c.nwg) + 3) / 4 * 4);
         c.o_att = c.o_qkv + 4 * c.HB;
-        c.down_slot = row_slot_bytes(c.F);
-        c.o_down = (args.stage_lds & 1) ? (c.o_att + 4 * c.n_rep * (c.hd + 2) + 15) / 16 * 16 : 0;
+        c.down_slot = DSPLIT ? down_slot_bytes(c.D, c.F, c.nwg) : row_slot_bytes(c.F);
+        c.o_down = (args.stage_lds & 3) ? (c.o_att + 4 * c.n_rep * (c.hd + 2) + 15) / 16 * 16 : 0;
         c.e0 = args.ctl->epoch;
         c.pos0 = args.ctl->pos;
         c.key0 = args.ctl->key;
@@ -793,15 +818,84 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         }
         return wave_sum(acc);
     };
-    // Wave wid's ffn_down row: row wid.
+    // Staged ffn_down (Q8_0), split layout: wave v copies its run of columns of its workgroup's R rows into
+    // its own LDS slot with direct global->LDS loads, ahead of the down phase (lane i of a
+    // load lands at +16 i for the q bytes, +4 i for the scales). Lanes past the run load
+    // nothing.
     auto issue_down = [&](const StepLayer& ly) {
         if constexpr (TL == TF_HIP_TYPE_Q8_0) {
-            const int wid = wg * kNW + wave;
-            if (sc.o_down == 0 || wid >= (int)ly.wd.N) return;
-            const int K = sc.F;
-            stage_row(ly.wd.q + (int64_t)wid * K, ly.wd.s + (int64_t)wid * (K / 16), K,
-                      smem + sc.o_down + wave * sc.down_slot);
+            if constexpr (!DSPLIT) {
+                // one row per wave: row wid. (One return for both conditions: with two, the
+                // compiler's wait-count pass put an s_waitcnt vmcnt(0) after the staging, for
+                // the LDS reads that follow, and the gate/up phase then waited for the row;
+                // measured as 2% of the Qwen2.5-1.5B shape's token time.)
+                const int wid = wg * kNW + wave;
+                if (sc.o_down == 0 || wid >= (int)ly.wd.N) return;
+                const int K = sc.F;
+                stage_row(ly.wd.q + (int64_t)wid * K, ly.wd.s + (int64_t)wid * (K / 16), K,
+                          smem + sc.o_down + wave * sc.down_slot);
+                return;
+            }
+            if (sc.o_down == 0) return;
+            const int F = sc.F, R = down_rows(sc.D, sc.nwg), u0 = down_unit0(F, wave), nu = down_units(F, wave);
+            const int r0 = wg * R, nr = min(R, (int)ly.wd.N - r0);
+            const int qs = down_qstride(F), ds = down_dstride(F);
+            unsigned char* slot = smem + sc.o_down + wave * sc.down_slot;
+            unsigned char* dslot = slot + R * qs;
+            for (int r = 0; r < nr; ++r) {
+                const uint8_t* q = ly.wd.q + (int64_t)(r0 + r) * F + 64 * u0;
+                const uint8_t* d = ly.wd.s + (int64_t)(r0 + r) * (F / 16) + 4 * u0;
+                for (int i = 0; i < 64 * nu; i += 1024)
+                    if (i + 16 * lane < 64 * nu)
+                        __builtin_amdgcn_global_load_lds((const TF_GLOBAL void*)(q + i + 16 * lane),
+                                                         (__attribute__((address_space(3))) void*)(slot + r * qs + i),
+                                                         16, 0, 0);
+                if (lane < nu)
+                    __builtin_amdgcn_global_load_lds((const TF_GLOBAL void*)(d + 4 * lane),
+                                                     (__attribute__((address_space(3))) void*)(dslot + r * ds), 4, 0,
+                                                     0);
+            }
         }
+    };
+    // The down phase on the staged slices: wave v's partial sums of its rows over its
+    // columns (lane steps of 16 elements in order, each a Q8_0 step dot as in the GEMV, then
+    // the wave reduction), into dpart[v][r]; the caller adds the 8 partials of a row. RM is
+    // a compile-time row count >= the workgroup's rows: each step's inputs are read once for
+    // all rows, and rows past nr re-read the last row (no branch between the LDS reads).
+    auto staged_down_rm = [&](float* dpart, auto rm) {
+        constexpr int RM = decltype(rm)::value;
+        using F8 = Fmt<TF_HIP_TYPE_Q8_0>;
+        const int F = sc.F, R = down_rows(sc.D, sc.nwg), u0 = down_unit0(F, wave), nu = down_units(F, wave);
+        const int nr = min(R, sc.D - wg * R);
+        if (nr <= 0) return;
+        const int qs = down_qstride(F), ds = down_dstride(F);
+        const unsigned char* slot = smem + sc.o_down + wave * sc.down_slot;
+        const unsigned char* dslot = slot + R * qs;
+        float acc[RM];
+#pragma unroll
+        for (int r = 0; r < RM; ++r) acc[r] = 0.0f;
+        for (int j = lane; j < 4 * nu; j += kWave) {
+            const float4* x4 = (const float4*)(xs + 16 * (4 * u0 + j));  // the step's inputs in the whole row
+            const float4 x[4] = {x4[0], x4[1], x4[2], x4[3]};
+#pragma unroll
+            for (int r = 0; r < RM; ++r) {
+                const int rr = r < nr ? r : nr - 1;
+                typename F8::Raw w;
+                w.q = *(const uint4*)(slot + rr * qs + 16 * j);
+                w.d = ((const uint16_t*)(dslot + rr * ds))[j >> 1];
+                acc[r] += F8::dot_x(w, x);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RM; ++r) {
+            const float v = wave_sum(acc[r]);
+            if (lane == 0 && r < nr) dpart[wave * kDownRowsMax + r] = v;
+        }
+    };
+    auto staged_down = [&](float* dpart) {
+        const int R = down_rows(sc.D, sc.nwg);
+        if (R <= 2) staged_down_rm(dpart, std::integral_constant<int, 2>());
+        else staged_down_rm(dpart, std::integral_constant<int, kDownRowsMax>());
     };
 
     for (int t = 0; t < n_tokens; ++t) {
@@ -1081,18 +1175,29 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 bool staged = false;
                 if constexpr (TL == TF_HIP_TYPE_Q8_0) {
                     if (sc.o_down) {
-                        // the row was staged in LDS during gate/up: the same lane steps and
-                        // order as gemv_phase's, read from the wave's slot
+                        // the slices were staged in LDS during gate/up
                         staged = true;
                         __syncthreads();
                         prep();
-                        const int wid = wg * kNW + wave;
-                        if (wid < (int)ly.wd.N) {
-                            // this wave's loads complete in order and the exchange loads of prep
-                            // came after the staged row: this wait is already satisfied
+                        // a wave's loads complete in order and the exchange loads of prep came
+                        // after its staged slices or row: the waits below are already satisfied
+                        if constexpr (DSPLIT) {
                             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                            const float acc = staged_dot(smem + sc.o_down + wave * sc.down_slot, F);
-                            if (lane == 0) epi(0, wid, acc, 0.0f, 0.0f);
+                            staged_down(dpart);
+                            __syncthreads();
+                            const int R = down_rows(sc.D, sc.nwg), r0 = wg * R;
+                            if (tid < R && r0 + tid < sc.D) {
+                                float v = dpart[tid];
+                                for (int w = 1; w < kNW; ++w) v += dpart[w * kDownRowsMax + tid];
+                                epi(0, r0 + tid, v, 0.0f, 0.0f);
+                            }
+                        } else {
+                            const int wid = wg * kNW + wave;
+                            if (wid < (int)ly.wd.N) {  // waves without a row do not wait
+                                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                                const float acc = staged_dot(smem + sc.o_down + wave * sc.down_slot, F);
+                                if (lane == 0) epi(0, wid, acc, 0.0f, 0.0f);
+                            }
                         }
                     }
                 }
@@ -1167,6 +1272,22 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             ctl->epoch = sc.e0 + (uint32_t)(n_tokens * sc.P);
         }
     }
+}
+
+// Cooperative launch of one build, with the dynamic LDS the launch's arguments need.
+template <int TL, int TO, int HDM, int TA = TL, bool DSPLIT = false>
+hipError_t launch_t(const StepArgs& a, int n_wg, hipStream_t st) {
+    const void* fn = (const void*)k_step<TL, TO, HDM, TA, DSPLIT>;
+    const size_t lds = step_lds_bytes(a.n_layer, a.D, a.F, a.H, a.G, a.hd, n_wg, a.stage_lds);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    int per_cu = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kStepThreads, lds);
+    if (e != hipSuccess) return e;
+    if (per_cu < 1 || n_wg > per_cu * device_cu_count()) return hipErrorCooperativeLaunchTooLarge;
+    StepArgs arg = a;
+    void* params[] = {(void*)&arg};
+    return hipLaunchCooperativeKernel(fn, dim3(n_wg), dim3(kStepThreads), params, (unsigned)lds, st);
 }
 
 }  // namespace step_detail

@@ -1,0 +1,14 @@
+// The step kernel's Q8_0 builds with ffn_down staged split over K (k_step.hpp, DSPLIT), in
+// a translation unit of their own: each translation unit is a code object of its own, so
+// the other builds' code keeps its place.
+#include "k_step.hpp"
+
+namespace tfk {
+
+hipError_t launch_step_split(const StepArgs& a, int n_wg, hipStream_t st) {
+    constexpr int Q8 = TF_HIP_TYPE_Q8_0;
+    return a.hd <= 64 ? step_detail::launch_t<Q8, Q8, 64, Q8, true>(a, n_wg, st)
+                      : step_detail::launch_t<Q8, Q8, 128, Q8, true>(a, n_wg, st);
+}
+
+}  // namespace tfk

@@ -143,7 +143,7 @@ struct StepArgs {
     int greedy;                // 0: tokens from hist (prefill, decode); 1: each token is the previous argmax
     int lm_every;              // 1: lm_head for every token; 0: for the last one only (prefill)
     int att_start;             // first cache position attention covers (0, or the prefill chunk's start)
-    int stage_lds;             // bit 0: ffn_down rows staged in LDS (step_stage_lds)
+    int stage_lds;             // ffn_down staged in LDS (step_stage_lds): 1 a row per wave, 2 split over K per workgroup
     int split;                 // > 0: split attention on the trailing workgroups, splits per kv head (step_split)
     int split_all;             // > 0: splits per kv head when every workgroup splits (step_split_all)
     int split_all_from;        // spans longer than this use split_all (step_split_all_from)
@@ -232,6 +232,8 @@ bool step_supported(int type_layers, int type_out, int hd, int n_rep);
 // there is none).
 int step_alt_type(int tl);
 hipError_t launch_step(const StepArgs& a, int type_layers, int type_out, int n_wg, hipStream_t st);
+// the Q8_0 builds with ffn_down split over K (stage_lds 2)
+hipError_t launch_step_split(const StepArgs& a, int n_wg, hipStream_t st);
 
 // ---------------------------------------------------------------- streaming step kernel (k_stream.hpp)
 struct StepLayer;
