@@ -9,8 +9,10 @@
 //                (add_inplace, layers.cpp:21-23), silu(gate) * up (layers.cpp:14-19)
 // k_pf_rope_store apply_rope_many of q and k (attention.cpp:48-53) and KVCache::store
 //                (kvcache.cpp:31-36) of every row
+// k_pf_pack_kv   the keys and values attention covers, per 32-key tile, as scaled fp16
+//                pairs in MFMA fragment order
 // k_pf_attn      causal GQA attention of the chunk (attn_prefill, attention.cpp:82-111)
-//                on v_mfma_f32_16x16x4_f32 with an online softmax
+//                on v_mfma_f32_16x16x32_f16 with fp16 operand pairs and an online softmax
 //
 // Numerics. A Q8_0 weight q is an integer in [-128, 127] and exact in fp16; a
 // 32-element block's products with the fp16 pair (hi, lo) of an activation are exact
@@ -584,125 +586,314 @@ __global__ __launch_bounds__(kBlock) void k_pf_rope_store(float* qkv, int64_t ld
 }
 
 // ---------------------------------------------------------------- causal attention
+//
+// Both products of attention run on v_mfma_f32_16x16x32_f16 with every fp32 operand as an
+// fp16 pair hi + lo (22 significant bits): x . y = hi_x hi_y + hi_x lo_y + lo_x hi_y, the
+// dropped lo_x lo_y being 2^-22 of the product. Rows are scaled by powers of two so that
+// hi and lo stay in fp16 range and off its subnormals (max |row| in [2^14, 2^15)), and
+// the scales come back out exactly:
+//   S^T = K Q^T: each key row k_j by 2^ek_j, each query row by 2^eq; a score is the
+//     product times 2^-(ek_j + eq) / sqrt(hd).
+//   O^T = V^T P^T: each value row v_j by 2^ev_j; the probability p_ij enters as
+//     p_ij 2^(e_i - ev_j), with e_i per query and tile putting the largest of the tile's
+//     p_ij 2^-ev_j in [2^14, 2^15): the tile's products come out in units of 2^e_i, the
+//     query's running output carries its unit and is rescaled by 2^(e_i - unit) with the
+//     softmax's exp(m_old - m_new). Each term keeps 22 bits down to 2^-18 of the tile's
+//     largest term |p v| (below that, fp16's subnormal step: at most 2^-40 of it).
+// k_pf_pack_kv writes each 32-key tile of a kv head once per layer, already in fragment
+// order and scaled (a tile record); k_pf_attn's workgroups stage the records through LDS,
+// shared by the query heads of the kv head.
 
-// Workgroup: 16 consecutive queries of one kv head, one wave per query head of the
-// group. Per tile of 16 keys a wave computes S^T = K Q^T with HD/4 MFMAs (lane group
-// l/16 holds HD/4 consecutive dims of its key row and its query row), so a lane ends up
-// with 4 keys of query l%16; the softmax statistics of a query combine the 4 lanes
-// l%16 + 16 j. O^T = V^T P^T then takes P^T straight from those registers: MFMA r of a
-// tile feeds key 4 (l/16) + r, and V^T as one scalar per lane. Keys run from att_start to
-// the last query of the tile; keys past a query's position score -inf.
+constexpr int kAttnTile = 32;  // keys per tile record
+
+// Tile record of head size HD: K fragments [16-key half][32-dim chunk][hi, lo][lane][8],
+// V^T fragments [16-dim tile][hi, lo][lane][8], then 2^-ek_j [32] and 2^-ev_j [32] (0 for
+// a zero value row).
+// A V^T fragment's lane l holds dim l % 16 and the 8 keys of P^T's lane l: keys
+// 4 (l / 16) + 0..3 and 16 + 4 (l / 16) + 0..3, the keys whose scores S^T leaves there.
+__host__ __device__ constexpr int attn_rec_bytes(int hd) { return 256 * hd + 512; }
+
+constexpr int kZeroRow = 1000;  // row exponent of an all-zero row
+
+__device__ __forceinline__ int pow2_exp(float amax, int if_zero) {
+    int ex = 0;
+    (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
+    int e = amax > 0.0f ? 15 - ex : if_zero;
+    return e < -100 ? -100 : (e > 100 ? 100 : e);
+}
+
+// Grid (tiles, kv heads), 256 threads: tile t of kv head g covers positions key0 + 32 t ..;
+// positions past key0 + n_keys are zero rows.
 template <int HD>
-__global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, const float* kc, const float* vc,
-                                                 int layout, int G, int max_seq, int n_rep, int n, int pos0,
-                                                 int att_start, float* out, int64_t ldo) {
-    constexpr int DQ = HD / 4;   // dims per lane group in S^T
-    constexpr int NT = HD / 16;  // output dim tiles
-    const int lane = threadIdx.x & 63, r_head = threadIdx.x >> 6;
-    const int qt = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest tiles first
-    const int g = blockIdx.y;
-    const int h = g * n_rep + r_head;
-    const int l16 = lane & 15, grp = lane >> 4;
-    const int qi = qt * 16 + l16;
-    const int qrow = qi < n ? qi : n - 1;
-    const int qpos = pos0 + qrow;
-    const int last = qt * 16 + 15 < n ? qt * 16 + 15 : n - 1;
-    const int k_hi = pos0 + last;  // last key any query of the tile sees
+__global__ __launch_bounds__(kBlock) void k_pf_pack_kv(const float* kc, const float* vc, int layout, int G,
+                                                       int max_seq, int key0, int n_keys, unsigned char* recs) {
+    constexpr int NC = HD / 32;
+    __shared__ float ks[kAttnTile][HD + 1], vs[kAttnTile][HD + 1];
+    __shared__ int ex[2][kAttnTile];
+    const int t = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    unsigned char* rec = recs + ((int64_t)g * gridDim.x + t) * attn_rec_bytes(HD);
+    for (int i = tid; i < kAttnTile * HD / 4; i += kBlock) {
+        const int key = i / (HD / 4), d = 4 * (i % (HD / 4));
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+        if (kAttnTile * t + key < n_keys) {
+            const int64_t o = kv_offset(layout, G, max_seq, HD, g, key0 + kAttnTile * t + key) + d;
+            a = gload_f4(kc + o);
+            b = gload_f4(vc + o);
+        }
+        ks[key][d] = a.x; ks[key][d + 1] = a.y; ks[key][d + 2] = a.z; ks[key][d + 3] = a.w;
+        vs[key][d] = b.x; vs[key][d + 1] = b.y; vs[key][d + 2] = b.z; vs[key][d + 3] = b.w;
+    }
+    __syncthreads();
+    {  // row exponents: 4 threads per (K or V, key)
+        const int which = tid >> 7, key = (tid >> 2) & 31, part = tid & 3;
+        const float* row = which ? vs[key] : ks[key];
+        float m = 0.0f;
+        for (int d = part; d < HD; d += 4) m = fmaxf(m, fabsf(row[d]));
+        m = fmaxf(m, __shfl_xor(m, 1));
+        m = fmaxf(m, __shfl_xor(m, 2));
+        if (part == 0) ex[which][key] = m > 0.0f ? pow2_exp(m, 0) : kZeroRow;
+    }
+    __syncthreads();
+    h8_t* kf = (h8_t*)rec;
+    for (int i = tid; i < 2 * NC * 64; i += kBlock) {
+        const int lane = i & 63, hc = i >> 6;
+        const int key = 16 * (hc / NC) + (lane & 15), d0 = 32 * (hc % NC) + 8 * (lane >> 4);
+        const float sc = ex[0][key] == kZeroRow ? 0.0f : ldexpf(1.0f, ex[0][key]);
+        h8_t hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float x = ks[key][d0 + j] * sc;
+            hi[j] = (_Float16)x;
+            lo[j] = (_Float16)(x - (float)hi[j]);
+        }
+        kf[hc * 128 + lane] = hi;
+        kf[hc * 128 + 64 + lane] = lo;
+    }
+    h8_t* vf = (h8_t*)(rec + 128 * HD);
+    for (int i = tid; i < (HD / 16) * 64; i += kBlock) {
+        const int lane = i & 63, dt = i >> 6;
+        const int d = 16 * dt + (lane & 15), k0 = 4 * (lane >> 4);
+        h8_t hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int key = (j < 4 ? k0 : 16 + k0 - 4) + j;
+            const float x = ex[1][key] == kZeroRow ? 0.0f : vs[key][d] * ldexpf(1.0f, ex[1][key]);
+            hi[j] = (_Float16)x;
+            lo[j] = (_Float16)(x - (float)hi[j]);
+        }
+        vf[dt * 128 + lane] = hi;
+        vf[dt * 128 + 64 + lane] = lo;
+    }
+    float* fk = (float*)(rec + 256 * HD);
+    if (tid < kAttnTile) {
+        fk[tid] = ex[0][tid] == kZeroRow ? 0.0f : ldexpf(1.0f, -ex[0][tid]);
+        fk[kAttnTile + tid] = ex[1][tid] == kZeroRow ? 0.0f : ldexpf(1.0f, -ex[1][tid]);
+    }
+}
+
+// Workgroup: QG query blocks of 16 QS queries of one kv head, times its n_rep query
+// heads: wave w takes head w % n_rep of block w / n_rep (4 to 8 waves). Per tile record
+// (staged through LDS, the next one loaded into registers meanwhile) a wave computes, for
+// each of its 16-query subtiles, S^T of 32 keys (lane l: query l % 16, keys 4 (l / 16) + r
+// and 16 + 4 (l / 16) + r), the online softmax of those scores, and O^T += V^T P^T with
+// P^T straight from the same lanes. Keys run from att_start to the workgroup's last query;
+// keys past a query's position score -inf.
+template <int HD, int QS>
+__global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, const unsigned char* recs, int T,
+                                                 int n_rep, int QG, int n, int pos0, int att_start, float* out,
+                                                 int64_t ldo) {
+    extern __shared__ uint4 lds_rec[];
+    constexpr int NC = HD / 32, NT = HD / 16;
+    constexpr int RU = attn_rec_bytes(HD) / 16;  // uint4 per record
+    constexpr int PF = (RU + 255) / 256;         // per thread, at least 256 threads
+    const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
+    const int w = tid >> 6;
+    const int g = blockIdx.y, h = g * n_rep + w % n_rep;
+    const int blk = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
+    const int q_base = (blk * QG + w / n_rep) * 16 * QS;
+    const int wg_last = min(n - 1, (blk + 1) * QG * 16 * QS - 1);
+    const int n_tiles = (pos0 + wg_last - att_start) / kAttnTile + 1;
+    const int l16 = lane & 15, gq = lane >> 4;
     const float scale = 1.0f / sqrtf((float)HD);
 
-    float qv[DQ];
-    {
-        const float* qr = q + (int64_t)qrow * ldq + (int64_t)h * HD + grp * DQ;
+    h8_t qh[QS][NC], ql[QS][NC];
+    float fq[QS];
+    int qpos[QS];
 #pragma unroll
-        for (int s = 0; s < DQ; s += 4) {
-            const float4 t = gload_f4(qr + s);
-            qv[s] = t.x;
-            qv[s + 1] = t.y;
-            qv[s + 2] = t.z;
-            qv[s + 3] = t.w;
+    for (int qs = 0; qs < QS; ++qs) {
+        const int qi = q_base + 16 * qs + l16;
+        const int qrow = qi < n ? qi : n - 1;
+        qpos[qs] = pos0 + qrow;
+        const float* qr = q + (int64_t)qrow * ldq + (int64_t)h * HD + 8 * gq;
+        float v[NC][8];
+        float amax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const float4 a = gload_f4(qr + 32 * c), b = gload_f4(qr + 32 * c + 4);
+            v[c][0] = a.x; v[c][1] = a.y; v[c][2] = a.z; v[c][3] = a.w;
+            v[c][4] = b.x; v[c][5] = b.y; v[c][6] = b.z; v[c][7] = b.w;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
         }
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        const int e = pow2_exp(amax, 0);
+        const float sc = ldexpf(1.0f, e);
+        fq[qs] = ldexpf(scale, -e);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = v[c][j] * sc;
+                qh[qs][c][j] = (_Float16)x;
+                ql[qs][c][j] = (_Float16)(x - (float)qh[qs][c][j]);
+            }
     }
-    f4_t ot[NT];
+    f4_t acc[QS][NT];
+    float m_run[QS], l_run[QS];
 #pragma unroll
-    for (int d = 0; d < NT; ++d) ot[d] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run = -INFINITY, l_run = 0.0f;
+    for (int qs = 0; qs < QS; ++qs) {
+        m_run[qs] = -INFINITY;
+        l_run[qs] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < NT; ++d) acc[qs][d] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    int unit[QS];  // acc holds O times 2^unit (times l_run), per query
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) unit[qs] = 0;
 
-    // K rows (lane's key kt + l16, dims grp*DQ ..) and V scalars (MFMA r of dim tile d
-    // needs V[kt + 4 grp + r][16 d + l16]) of the tile at kt; keys past k_hi re-read key
-    // k_hi (masked). The next tile's loads are issued before the current tile's MFMAs.
-    auto load_kv = [&](int kt, float (&kv_)[DQ], float (&vv_)[4][NT]) {
-        int key = kt + l16;
-        key = key <= k_hi ? key : k_hi;
-        const float* kr = kc + kv_offset(layout, G, max_seq, HD, g, key) + grp * DQ;
+    // two records in flight in registers: a record is loaded two tiles before its use
+    uint4 pa[PF], pb[PF];
+    const uint4* src = (const uint4*)(recs + (int64_t)g * T * attn_rec_bytes(HD));
+    auto gload = [&](uint4 (&pf)[PF], int t) {
 #pragma unroll
-        for (int s = 0; s < DQ; s += 4) {
-            const float4 t = gload_f4(kr + s);
-            kv_[s] = t.x;
-            kv_[s + 1] = t.y;
-            kv_[s + 2] = t.z;
-            kv_[s + 3] = t.w;
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            int vkey = kt + 4 * grp + r;
-            vkey = vkey <= k_hi ? vkey : k_hi;
-            const float* vr = vc + kv_offset(layout, G, max_seq, HD, g, vkey) + l16;
-#pragma unroll
-            for (int d = 0; d < NT; ++d) vv_[r][d] = *gptr(vr + 16 * d);
+        for (int i = 0; i < PF; ++i) {
+            const int idx = tid + i * nthr;
+            if (idx < RU) pf[i] = gload_u4(src + (int64_t)t * RU + idx);
         }
     };
-    auto tile = [&](int kt, const float (&kv_)[DQ], const float (&vv_)[4][NT]) {
-        f4_t st = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto lstore = [&](const uint4 (&pf)[PF], int buf) {
 #pragma unroll
-        for (int s = 0; s < DQ; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kv_[s], qv[s], st, 0, 0, 0);
-        float p[4];
-        float mt = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int key = kt + 4 * grp + r;
-            p[r] = key <= qpos ? st[r] * scale : -INFINITY;
-            mt = fmaxf(mt, p[r]);
+        for (int i = 0; i < PF; ++i) {
+            const int idx = tid + i * nthr;
+            if (idx < RU) lds_rec[buf * RU + idx] = pf[i];
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = expf(m_run - m_new);  // 0 on the first tile
-        float ls = 0.0f;
+    };
+    auto tile = [&](const unsigned char* rec, int t) {
+        const h8_t* kf = (const h8_t*)rec;
+        const h8_t* vf = (const h8_t*)(rec + 128 * HD);
+        const float* fk = (const float*)(rec + 256 * HD);
+        f4_t s[QS][2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            p[r] = p[r] == -INFINITY ? 0.0f : expf(p[r] - m_new);
-            ls += p[r];
+        for (int qs = 0; qs < QS; ++qs) s[qs][0] = s[qs][1] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const h8_t kh = kf[(half * NC + c) * 128 + lane], kl = kf[(half * NC + c) * 128 + 64 + lane];
+#pragma unroll
+                for (int qs = 0; qs < QS; ++qs) {
+                    f4_t x = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[qs][c], s[qs][half], 0, 0, 0);
+                    x = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[qs][c], x, 0, 0, 0);
+                    s[qs][half] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[qs][c], x, 0, 0, 0);
+                }
+            }
+        const float4 k0 = *(const float4*)(fk + 4 * gq), k1 = *(const float4*)(fk + 16 + 4 * gq);
+        const float4 v0 = *(const float4*)(fk + kAttnTile + 4 * gq), v1 = *(const float4*)(fk + kAttnTile + 16 + 4 * gq);
+        const float fkj[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        const float fvj[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        const int kpos = att_start + kAttnTile * t + 4 * gq;  // key j of the lane: kpos + 16 (j / 4) + j % 4
+        h8_t ph[QS], pl[QS];
+        float resc[QS];
+        int unit_new[QS];
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) {
+            float p[8];
+            float mt = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = kpos + 16 * (j >> 2) + (j & 3);
+                p[j] = key <= qpos[qs] ? s[qs][j >> 2][j & 3] * fq[qs] * fkj[j] : -INFINITY;
+                mt = fmaxf(mt, p[j]);
+            }
+            mt = fmaxf(mt, __shfl_xor(mt, 16));
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float m_new = fmaxf(m_run[qs], mt);
+            const float alpha = expf(m_run[qs] - m_new);  // 0 on the first tile
+            float ls = 0.0f, x[8], mx = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                p[j] = p[j] == -INFINITY ? 0.0f : expf(p[j] - m_new);
+                ls += p[j];
+                x[j] = p[j] * fvj[j];
+                mx = fmaxf(mx, x[j]);
+            }
+            ls += __shfl_xor(ls, 16);
+            ls += __shfl_xor(ls, 32);
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            l_run[qs] = fmaf(l_run[qs], alpha, ls);
+            m_run[qs] = m_new;
+            // the tile's unit: its largest term in [2^14, 2^15); no change when it adds
+            // nothing, and never so far above the running unit that the rescaled output
+            // (below 2^43 in its unit, times alpha) could leave fp32's range
+            int e = unit[qs];
+            if (mx > 0.0f) {
+                e = 15 - __builtin_amdgcn_frexp_expf(mx);
+                if (alpha > 0.0f) e = min(e, unit[qs] + 76 - __builtin_amdgcn_frexp_expf(alpha));
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float y = ldexpf(x[j], e);
+                ph[qs][j] = (_Float16)y;
+                pl[qs][j] = (_Float16)(y - (float)ph[qs][j]);
+            }
+            resc[qs] = ldexpf(alpha, e - unit[qs]);
+            unit_new[qs] = e;
         }
-        ls += __shfl_xor(ls, 16);
-        ls += __shfl_xor(ls, 32);
-        l_run = fmaf(l_run, alpha, ls);
-        m_run = m_new;
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) unit[qs] = unit_new[qs];
 #pragma unroll
         for (int d = 0; d < NT; ++d) {
-            f4_t o = ot[d] * alpha;
+            const h8_t vh = vf[d * 128 + lane], vl = vf[d * 128 + 64 + lane];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o = __builtin_amdgcn_mfma_f32_16x16x4f32(vv_[r][d], p[r], o, 0, 0, 0);
-            ot[d] = o;
+            for (int qs = 0; qs < QS; ++qs) {
+                f4_t x = acc[qs][d] * resc[qs];
+                x = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[qs], x, 0, 0, 0);
+                x = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl[qs], x, 0, 0, 0);
+                acc[qs][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[qs], x, 0, 0, 0);
+            }
         }
     };
-    float kva[DQ], vva[4][NT], kvb[DQ], vvb[4][NT];
-    load_kv(att_start, kva, vva);
-    for (int kt = att_start; kt <= k_hi;) {
-        load_kv(kt + 16, kvb, vvb);
-        tile(kt, kva, vva);
-        kt += 16;
-        if (kt > k_hi) break;
-        load_kv(kt + 16, kva, vva);
-        tile(kt, kvb, vvb);
-        kt += 16;
+
+    gload(pa, 0);
+    if (1 < n_tiles) gload(pb, 1);
+    lstore(pa, 0);
+    __syncthreads();
+    for (int t = 0; t < n_tiles; t += 2) {
+        // tile t in buffer 0; pa is free, pb holds tile t + 1
+        if (t + 2 < n_tiles) gload(pa, t + 2);
+        tile((const unsigned char*)lds_rec, t);
+        if (t + 1 < n_tiles) lstore(pb, 1);
+        __syncthreads();
+        if (t + 1 >= n_tiles) break;
+        // tile t + 1 in buffer 1; pb is free, pa holds tile t + 2
+        if (t + 3 < n_tiles) gload(pb, t + 3);
+        tile((const unsigned char*)(lds_rec + RU), t + 1);
+        if (t + 2 < n_tiles) lstore(pa, 0);
+        __syncthreads();
     }
-    // lane holds O[query l16][dims 16 d + 4 grp + 0..3]; the 4 lanes of a query share l_run
-    if (qi < n) {
-        float* orow = out + (int64_t)qi * ldo + (int64_t)h * HD + 4 * grp;
-        const float il = 1.0f / l_run;
+    // lane holds O[query l16][dims 16 d + 4 gq + 0..3] times 2^unit l_run
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) {
+        const int qi = q_base + 16 * qs + l16;
+        if (qi >= n) continue;
+        float* orow = out + (int64_t)qi * ldo + (int64_t)h * HD + 4 * gq;
+        const float il = ldexpf(1.0f / l_run[qs], -unit[qs]);
 #pragma unroll
         for (int d = 0; d < NT; ++d)
-            *(float4*)(orow + 16 * d) = make_float4(ot[d][0] * il, ot[d][1] * il, ot[d][2] * il, ot[d][3] * il);
+            *(float4*)(orow + 16 * d) =
+                make_float4(acc[qs][d][0] * il, acc[qs][d][1] * il, acc[qs][d][2] * il, acc[qs][d][3] * il);
     }
 }
 
@@ -844,30 +1035,63 @@ bool pf_attn_supported(int hd, int n_rep) {
     return (hd == 32 || hd == 64 || hd == 128) && n_rep >= 1 && n_rep <= 8;
 }
 
+size_t pf_attn_ws_bytes(int hd, int G, int n_keys) {
+    return (size_t)((n_keys + kAttnTile - 1) / kAttnTile) * G * attn_rec_bytes(hd);
+}
+
+namespace {
+
+template <int HD, int QS>
+hipError_t launch_attn_t(const float* q, int64_t ldq, const unsigned char* recs, int T, int G, int n_rep, int QG,
+                         int n, int pos0, int att_start, float* out, int64_t ldo, hipStream_t st) {
+    const size_t lds = 2 * (size_t)attn_rec_bytes(HD);
+    static hipError_t attr = hipFuncSetAttribute((const void*)k_pf_attn<HD, QS>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    const int per_blk = 16 * QS * QG;
+    const dim3 grid((unsigned)((n + per_blk - 1) / per_blk), (unsigned)G), block((unsigned)(64 * n_rep * QG));
+    hipLaunchKernelGGL((k_pf_attn<HD, QS>), grid, block, lds, st, q, ldq, recs, T, n_rep, QG, n, pos0, att_start,
+                       out, ldo);
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_attn_hd(const float* q, int64_t ldq, const float* kc, const float* vc, int layout, int G,
+                          int max_seq, int n_rep, int n, int pos0, int att_start, float* out, int64_t ldo,
+                          unsigned char* recs, hipStream_t st) {
+    const int n_keys = pos0 + n - att_start, T = (n_keys + kAttnTile - 1) / kAttnTile;
+    hipLaunchKernelGGL(k_pf_pack_kv<HD>, dim3((unsigned)T, (unsigned)G), dim3(kBlock), 0, st, kc, vc, layout, G,
+                       max_seq, att_start, n_keys, recs);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // 4 to 8 waves per workgroup, one 16-query subtile per wave (a prompt chunk of 2048
+    // rows gives 128 query blocks per kv head)
+    const int QG = (4 + n_rep - 1) / n_rep;
+    return launch_attn_t<HD, 1>(q, ldq, recs, T, G, n_rep, QG, n, pos0, att_start, out, ldo, st);
+}
+
+}  // namespace
+
 hipError_t launch_pf_attn(const float* q, int64_t ldq, const float* kc, const float* vc, int layout, int H, int G,
-                          int hd, int max_seq, int n, int pos0, int att_start, float* out, int64_t ldo,
-                          hipStream_t st) {
+                          int hd, int max_seq, int n, int pos0, int att_start, float* out, int64_t ldo, void* ws,
+                          size_t ws_bytes, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     const int n_rep = H / G;
     if (H % G != 0 || !pf_attn_supported(hd, n_rep) || att_start < 0 || att_start > pos0 || pos0 + n > max_seq ||
-        ldq % 4 != 0 || ldo % 4 != 0)
+        ldq % 4 != 0 || ldo % 4 != 0 || !ws || ws_bytes < pf_attn_ws_bytes(hd, G, pos0 + n - att_start))
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((n + 15) / 16), (unsigned)G), block((unsigned)(64 * n_rep));
+    unsigned char* recs = (unsigned char*)ws;
     switch (hd) {
         case 32:
-            hipLaunchKernelGGL(k_pf_attn<32>, grid, block, 0, st, q, ldq, kc, vc, layout, G, max_seq, n_rep, n, pos0,
-                               att_start, out, ldo);
-            break;
+            return launch_attn_hd<32>(q, ldq, kc, vc, layout, G, max_seq, n_rep, n, pos0, att_start, out, ldo, recs,
+                                      st);
         case 64:
-            hipLaunchKernelGGL(k_pf_attn<64>, grid, block, 0, st, q, ldq, kc, vc, layout, G, max_seq, n_rep, n, pos0,
-                               att_start, out, ldo);
-            break;
+            return launch_attn_hd<64>(q, ldq, kc, vc, layout, G, max_seq, n_rep, n, pos0, att_start, out, ldo, recs,
+                                      st);
         default:
-            hipLaunchKernelGGL(k_pf_attn<128>, grid, block, 0, st, q, ldq, kc, vc, layout, G, max_seq, n_rep, n, pos0,
-                               att_start, out, ldo);
-            break;
+            return launch_attn_hd<128>(q, ldq, kc, vc, layout, G, max_seq, n_rep, n, pos0, att_start, out, ldo, recs,
+                                       st);
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_pf_tail(Ctl* ctl, int pos_last, const int32_t* hist, const float* xrow, float* x, int D,

@@ -103,6 +103,8 @@ struct tf_hip_ctx {
     uint16_t* pxa = nullptr;            // activation fragments (hi, lo) of one chunk
     float* ppart = nullptr;             // split-K partial sums of the prefill GEMMs
     size_t ppart_floats = 0;
+    void* pattn_ws = nullptr;           // packed key/value tiles of prefill attention
+    size_t pattn_ws_bytes = 0;
     std::vector<uint16_t*> pf_wf;       // per slot: the matrix's integers as fp16 fragments
     std::string err;
 };
@@ -831,6 +833,9 @@ int ensure_pf(tf_hip_ctx* c) {
         // up to 8 K slices of the widest non-SILU output (QKV or d_model)
         c->ppart_floats = 8 * (size_t)cap * std::max(NQ, D);
         if ((rc = dalloc(c, &c->ppart, c->ppart_floats * 4))) return rc;
+        // attention of a chunk covers at most max_seq positions
+        c->pattn_ws_bytes = pf_attn_ws_bytes(p.head_dim, p.n_kv_head, p.max_seq);
+        if ((rc = dalloc(c, &c->pattn_ws, c->pattn_ws_bytes))) return rc;
         c->pf_cap = cap;
     }
     // every layer matrix's integers as fp16 fragments (2 bytes per weight, kept for the
@@ -910,7 +915,7 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
             chk(launch_pf_rope_store(c->pqkv, NQ, nc, p.n_head, p.n_kv_head, p.head_dim, c->rope_cos, c->rope_sin,
                                      pos0, kc, vc, p.kv_layout, p.max_seq, c->st));
             chk(launch_pf_attn(c->pqkv, NQ, kc, vc, p.kv_layout, p.n_head, p.n_kv_head, p.head_dim, p.max_seq, nc,
-                               pos0, start, c->patt, Hd, c->st));
+                               pos0, start, c->patt, Hd, c->pattn_ws, c->pattn_ws_bytes, c->st));
             chk(launch_pf_split(c->patt, Hd, nullptr, 0.0f, Hd, nc, Mpad, c->pxa, c->prs, c->st));
             {
                 PfGemmArgs a = base(Hd);
@@ -1600,8 +1605,11 @@ int tf_hip_attn_prefill(int device, const float* q, const float* k, const float*
     OPCHK(hipMemcpy(dk, k, nk * 4, hipMemcpyHostToDevice));
     OPCHK(hipMemcpy(dv, v, nk * 4, hipMemcpyHostToDevice));
     // k and v rows [seq][n_kv][hd] are a sequence-major cache of seq positions
+    const size_t ws_bytes = pf_attn_ws_bytes(hd, n_kv, seq);
+    void* ws = nullptr;
+    OPCHK(s.alloc(&ws, ws_bytes));
     OPCHK(launch_pf_attn(dq, (int64_t)n_heads * hd, dk, dv, TF_HIP_KV_SEQ_MAJOR, n_heads, n_kv, hd, seq, seq, 0, 0,
-                         dout, (int64_t)n_heads * hd, s.st));
+                         dout, (int64_t)n_heads * hd, ws, ws_bytes, s.st));
     OPCHK(hipMemcpyAsync(out, dout, nq * 4, hipMemcpyDeviceToHost, s.st));
     OPCHK(hipStreamSynchronize(s.st));
     return 0;

@@ -203,9 +203,12 @@ hipError_t launch_pf_rope_store(float* qkv, int64_t ld, int n, int H, int G, int
                                 const float* rope_sin, int pos0, float* kc, float* vc, int layout, int max_seq,
                                 hipStream_t st);
 bool pf_attn_supported(int hd, int n_rep);
+// Workspace of launch_pf_attn for attention over n_keys positions: the packed key/value
+// tile records.
+size_t pf_attn_ws_bytes(int hd, int G, int n_keys);
 hipError_t launch_pf_attn(const float* q, int64_t ldq, const float* kc, const float* vc, int layout, int H, int G,
-                          int hd, int max_seq, int n, int pos0, int att_start, float* out, int64_t ldo,
-                          hipStream_t st);
+                          int hd, int max_seq, int n, int pos0, int att_start, float* out, int64_t ldo, void* ws,
+                          size_t ws_bytes, hipStream_t st);
 hipError_t launch_pf_tail(Ctl* ctl, int pos_last, const int32_t* hist, const float* xrow, float* x, int D,
                           hipStream_t st);
 
