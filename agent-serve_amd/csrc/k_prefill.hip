@@ -321,18 +321,42 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
     }
 }
 
+// Direct global -> LDS loads (global_load_lds), issued from inline assembly: lane i of a
+// 16-byte load writes LDS at m0 + 16 i (4 i for a dword load), m0 saved and restored around
+// it. Written as assembly so that the compiler does not count these loads: it would wait
+// for all of them before every LDS read (it cannot tell the buffer a load targets); the
+// kernel waits for them itself (s_waitcnt vmcnt with the count of its later loads).
+__device__ __forceinline__ void lds_dma16(const TF_GLOBAL void* g, uint32_t m0) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(m0), "v"(g)
+                 : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const TF_GLOBAL void* g, uint32_t m0) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(m0), "v"(g)
+                 : "memory");
+}
+
 // Large tiles for GEMMs with enough of them to fill the CUs: a workgroup of 8 waves
 // (2 rows x 4 columns of waves) owns 128 rows x 16 weight-column subtiles (256 weight rows;
-// GEMV_SILU: 8 gate and the 8 matching up subtiles, 128 output columns). A stage (two
-// 32-element blocks) of both operands and the scales is staged in LDS, loaded once per
-// workgroup (8 fragments per wave) through registers one stage ahead of its use; each wave
-// then runs 4 x 4 tiles of 16 x 16 per block, reading its fragments from LDS. The per-block
-// arithmetic and its order are those of k_pf_gemm_q8, so the two give the same bits.
+// GEMV_SILU: 8 gate and the 8 matching up subtiles, 128 output columns). A stage (one
+// 32-element block) of both operands and the scales goes straight from global memory into
+// one of four LDS buffers, five loads per wave, three stages ahead of its use; each wave
+// then runs 4 x 4 tiles of 16 x 16, reading its fragments from LDS (4 waves of 4 x 8 tiles,
+// a third fewer LDS reads per MFMA, measured 12% slower: one wave per SIMD leaves the
+// MFMA-to-scale dependencies exposed). The per-block arithmetic and its order are those of
+// k_pf_gemm_q8, so the two give the same bits.
 constexpr int kBigThreads = 512;
+constexpr int kBigWaves = kBigThreads / 64;
 constexpr int kBigRows = 128;
-constexpr int kBigStageH8 = 64 * 64;  // h8 per stage: 32 A fragments + 32 B fragments of 64 lanes
-constexpr int kBigStageBytes = kBigStageH8 * 16 + 256 * 4;
-constexpr size_t kBigLdsBytes = 2 * (size_t)kBigStageBytes;
+constexpr int kBigFragBytes = 32 * 1024;                 // 16 A fragments (8 row tiles, hi and lo) + 16 B fragments
+constexpr int kBigStageBytes = kBigFragBytes + 256 * 4;  // + the fp16 scale pairs of the 256 weight columns
+constexpr int kBigStages = 4;                            // LDS buffers: one in use, three loading
+constexpr size_t kBigLdsBytes = kBigStages * (size_t)kBigStageBytes;
 
 // SPLIT: the grid also splits K into a.ks slices; slice ks writes its row-scaled partial
 // sums to a.part[ks][row][output column] and k_pf_reduce applies the epilogue.
@@ -350,8 +374,8 @@ __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a)
     const int MT = a.Mpad / kBigRows;
     const int mt = b % MT, nt = b / MT;
     const int K = a.K, nblk = K / 32;
-    const int S = SPLIT ? K / 64 / a.ks : K / 64;  // stages of this slice
-    const int s0 = kslice * S;                      // its first stage
+    const int S = SPLIT ? nblk / a.ks : nblk;  // stages (blocks) of this slice
+    const int s0 = kslice * S;                 // its first block
     const int l16 = lane & 15;
     constexpr bool SILU = MODE == GEMV_SILU;
 
@@ -362,53 +386,49 @@ __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a)
         u = u < a.n_sub ? u : a.n_sub - 1;
         seg = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
     };
-    // this wave's 8 fragment loads per stage: i < 4 A fragments, i >= 4 B fragments
-    const TF_GLOBAL h8_t* src[8];
-    int step[8];  // h8 per stage
+    // this wave's 4 fragments per stage, f = wave + 8 i: f < 16 the A fragment (row tile f / 2,
+    // hi or lo), else the B fragment of weight-column subtile f - 16; one block per stage
+    const TF_GLOBAL h8_t* src[4];
+    int step[4];  // h8 per block
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int f = wave + 8 * i;
-        if (i < 4) {
-            const int T = f / 4, blk = (f / 2) % 2, hl = f % 2;
-            src[i] = (const TF_GLOBAL h8_t*)a.xa + ((int64_t)(mt * 8 + T) * nblk + blk) * 128 + hl * 64 + lane;
-            step[i] = 256;
+    for (int i = 0; i < 4; ++i) {
+        const int f = wave + kBigWaves * i;
+        if (i < 2) {
+            src[i] = (const TF_GLOBAL h8_t*)a.xa + (int64_t)(mt * 8 + f / 2) * nblk * 128 + (f % 2) * 64 + lane;
+            step[i] = 128;
         } else {
-            const int g = f - 32, q = g / 2, blk = g % 2;
             int u, seg;
             bool up;
-            resolve(q, u, seg, up);
+            resolve(f - 16, u, seg, up);
             const int tile = u - PF_SEL(seg, sub0);
             const uint16_t* wf = up ? PF_SEL(seg, wf2) : PF_SEL(seg, wf);
-            src[i] = (const TF_GLOBAL h8_t*)wf + ((int64_t)tile * nblk + blk) * 64 + lane;
-            step[i] = 128;
+            src[i] = (const TF_GLOBAL h8_t*)wf + (int64_t)tile * nblk * 64 + lane;
+            step[i] = 64;
         }
     }
-    // the scales: thread t (mod 256) loads column j = t of the 256 weight columns
-    const uint16_t* dsrc;
+    // the scales: lane i < 32 of wave w loads the fp16 pair (blocks 2p, 2p + 1) of weight
+    // column 32 w + i
+    const TF_GLOBAL uint32_t* dsrc;
     {
-        const int j = tid & 255, q = j / 16;
+        const int j = 32 * wave + (lane & 31), q = j / 16;
         int u, seg;
         bool up;
         resolve(q, u, seg, up);
         const int c = (u - PF_SEL(seg, sub0)) * 16 + (j & 15);
         const uint8_t* ws = up ? PF_SEL(seg, w2.s) : PF_SEL(seg, w.s);
-        dsrc = (const uint16_t*)ws + (int64_t)c * nblk;
+        dsrc = (const TF_GLOBAL uint32_t*)((const uint16_t*)ws + (int64_t)c * nblk);
     }
-    h8_t stg[8];
-    uint32_t dstg;
-    auto gload = [&](int s) {
-        s = s0 + (s < S ? s : S - 1);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+    auto issue = [&](int s) {  // stage s into buffer s % 4: 5 loads per wave
+        const int blk = s0 + s;
+        const uint32_t base = lds0 + (uint32_t)((s % kBigStages) * kBigStageBytes);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) stg[i] = src[i][(int64_t)s * step[i]];
-        dstg = *(const TF_GLOBAL uint32_t*)(dsrc + 2 * s);
+        for (int i = 0; i < 4; ++i)
+            lds_dma16(src[i] + (int64_t)blk * step[i],
+                      __builtin_amdgcn_readfirstlane(base + (uint32_t)((wave + kBigWaves * i) * 1024)));
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(base + (uint32_t)(kBigFragBytes + 128 * wave));
+        if (lane < 32) lds_dma4(dsrc + blk / 2, m0);
     };
-    auto lds_write = [&](int buf) {
-        h8_t* st = (h8_t*)(lds + buf * kBigStageBytes);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) st[(wave + 8 * i) * 64 + lane] = stg[i];
-        ((uint32_t*)(lds + buf * kBigStageBytes + kBigStageH8 * 16))[tid & 255] = dstg;
-    };
-    auto barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
     const int wm = wave & 1, wn = wave >> 1;
     int qb[4];  // this wave's weight-column subtiles
@@ -421,61 +441,76 @@ __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a)
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](int buf) {
+    // Software-pipelined: a half's block sums are scaled into acc after the next half's
+    // MFMAs are issued (the last half of a block after the first of the next block), so the
+    // scaling never waits on MFMAs just issued. Same operations, same order per acc.
+    f4_t tp[2][4];  // pending block sums: rows half 1 of the previous block
+    float dvp[4];
+    auto scale_in = [&](int half, const f4_t (&t)[2][4], const float (&dv)[4]) {
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[half * 2 + mm][ni][r] = fmaf(dv[ni], t[mm][ni][r], acc[half * 2 + mm][ni][r]);
+    };
+    auto compute = [&](int buf, int blk, bool pending) {
         const h8_t* st = (const h8_t*)(lds + buf * kBigStageBytes);
-        const uint32_t* sd = (const uint32_t*)(lds + buf * kBigStageBytes + kBigStageH8 * 16);
-        uint32_t dd[4];
+        const uint32_t* sd = (const uint32_t*)(lds + buf * kBigStageBytes + kBigFragBytes);
+        float dv[4];
+        h8_t bh[4];
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) dd[ni] = sd[qb[ni] * 16 + l16];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            h8_t bh[4];
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) bh[ni] = st[(32 + qb[ni] * 2 + j) * 64 + lane];
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                h8_t ah[2], al[2];
-#pragma unroll
-                for (int mm = 0; mm < 2; ++mm) {
-                    const int T = wm * 4 + half * 2 + mm;
-                    ah[mm] = st[((T * 2 + j) * 2 + 0) * 64 + lane];
-                    al[mm] = st[((T * 2 + j) * 2 + 1) * 64 + lane];
-                }
-                f4_t t[2][4];
-#pragma unroll
-                for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-                    for (int ni = 0; ni < 4; ++ni)
-                        t[mm][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mm], bh[ni],
-                                                                          (f4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-                for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-                    for (int ni = 0; ni < 4; ++ni)
-                        t[mm][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mm], bh[ni], t[mm][ni], 0, 0, 0);
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni) {
-                    const float dv = h2f(dd[ni] >> (16 * j));
-#pragma unroll
-                    for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            acc[half * 2 + mm][ni][r] = fmaf(dv, t[mm][ni][r], acc[half * 2 + mm][ni][r]);
-                }
-            }
+        for (int ni = 0; ni < 4; ++ni) {
+            dv[ni] = h2f(sd[qb[ni] * 16 + l16] >> (16 * (blk & 1)));
+            bh[ni] = st[(16 + qb[ni]) * 64 + lane];
         }
+        auto mfmas = [&](int half, f4_t (&t)[2][4]) {
+            h8_t ah[2], al[2];
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm) {
+                const int T = wm * 4 + half * 2 + mm;
+                ah[mm] = st[(T * 2 + 0) * 64 + lane];
+                al[mm] = st[(T * 2 + 1) * 64 + lane];
+            }
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+                    t[mm][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mm], bh[ni], (f4_t){0.0f, 0.0f, 0.0f, 0.0f},
+                                                                      0, 0, 0);
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+                    t[mm][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mm], bh[ni], t[mm][ni], 0, 0, 0);
+        };
+        f4_t t0[2][4];
+        mfmas(0, t0);
+        if (pending) scale_in(1, tp, dvp);
+        mfmas(1, tp);
+        scale_in(0, t0, dv);
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) dvp[ni] = dv[ni];
     };
 
-    gload(0);
-    lds_write(0);
-    gload(1);
-    barrier();
+    const int pre = S < kBigStages - 1 ? S : kBigStages - 1;
+    for (int s = 0; s < pre; ++s) issue(s);
     for (int s = 0; s < S; ++s) {
-        compute(s & 1);
-        lds_write((s + 1) & 1);  // stage s + 1 (the buffer of stage s - 1, read before the last barrier)
-        gload(s + 2);
-        barrier();
+        // this wave's loads of stage s are done when at most those of the (up to two) stages
+        // issued after it are in flight; the barrier then makes every wave's done, and every
+        // wave has left compute(s - 1), whose buffer stage s + 3 takes
+        const int after = S - 1 - s;
+        if (after >= 2)
+            asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else if (after == 1)
+            asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (s + kBigStages - 1 < S) issue(s + kBigStages - 1);
+        compute(s % kBigStages, s0 + s, s > 0);
     }
+    if (S > 0) scale_in(1, tp, dvp);
 
     // epilogue: lane holds rows 16 T + 4 (lane / 16) + r of weight column 16 q + l16
 #pragma unroll
