@@ -126,10 +126,12 @@ def prefill(trace_csv: str, n: int, dims: str) -> None:
     """Per kernel class of one prompt prefill (the k_pf_* dispatches of the trace): launches,
     average and total microseconds, algorithmic FLOP per launch and TFLOP/s. Dense GEMM
     FLOP are 2 per weight per row; attention's are q.k and p.v over i + 1 positions for
-    row i. The attn_output and ffn_down GEMMs share a kernel and alternate in launch order."""
+    row i. FLOP and TFLOP/s come from the prompt's total per class over the class's total
+    time, so a prompt run in several chunks (one launch per chunk and layer) counts right.
+    The attn_output and ffn_down GEMMs share a kernel and alternate in launch order."""
     D, F, L, H, G = (int(v) for v in dims.split(","))
     hd = D // H
-    flop = {
+    flop = {  # per layer, the whole prompt
         "qkv_gemm": 2.0 * n * D * (H * hd + 2 * G * hd),
         "wo_gemm": 2.0 * n * H * hd * D,
         "gateup_gemm": 2.0 * n * D * 2 * F,
@@ -149,7 +151,7 @@ def prefill(trace_csv: str, n: int, dims: str) -> None:
     for c, v in sorted(acc.items(), key=lambda kv: -sum(kv[1])):
         avg = sum(v) / len(v)
         f = flop.get(c)
-        fs = f"{f / 1e9:11.2f} {f / (avg * 1e-6) / 1e12:8.1f}" if f else f"{'':11s} {'':8s}"
+        fs = (f"{f * L / len(v) / 1e9:11.2f} {f * L / (sum(v) * 1e-6) / 1e12:8.1f}" if f else f"{'':11s} {'':8s}")
         print(f"{c:16s} {len(v):6d} {avg:9.2f} {sum(v) / 1e3:9.3f} {sum(v) / total:6.1%} {fs}")
 
 
