@@ -71,21 +71,26 @@ __global__ __launch_bounds__(kBlock) void k_pf_pack_q8(const uint8_t* q, int K, 
 
 constexpr int kSplitGroups = 8;  // 8-element groups per thread: rows up to 256 * 8 * 8 = 16384
 
-// One workgroup per row, the row held in registers (thread t owns the 8-element groups
-// t, t + 256, ...): the rmsnorm scale inv (when w is given), a power of two sc putting
-// max |row| in [2^14, 2^15) (rs = 1 / sc), then every element as hi + lo into the
-// fragment layout (16 bytes of a hi and of a lo fragment per group). Rows M.. are zeros
-// with rs = 0.
+// WPR waves per row (1: a workgroup takes 4 consecutive rows, a wave each, and reduces
+// within the wave; 4: a workgroup per row), the row held in registers (thread t of the row
+// owns the 8-element groups t, t + 64 WPR, ..., NG of them: the fewest that cover the row):
+// the rmsnorm scale inv (when w is given), a power of two sc putting max |row| in
+// [2^14, 2^15) (rs = 1 / sc), then every element as hi + lo into the fragment layout (16
+// bytes of a hi and of a lo fragment per group; with a wave per row, the 4 rows of a
+// workgroup fill whole 64-byte lines of a fragment). Rows M.. are zeros with rs = 0.
+template <int NG, int WPR>
 __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx, const float* w, float eps, int K,
                                                      int M, h8_t* xa, float* rs) {
+    constexpr int ST = 64 * WPR;  // threads per row
     __shared__ double red_d[kWavesPerBlock];
     __shared__ float red_f[kWavesPerBlock];
-    const int m = blockIdx.x, tid = threadIdx.x;
+    const int m = WPR == 1 ? blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6) : blockIdx.x;
+    const int tid = WPR == 1 ? threadIdx.x & 63 : threadIdx.x;
     const int ng = K / 8, nblk = K / 32;
     h8_t* tile = xa + (int64_t)(m / 16) * nblk * 128 + (m % 16);
     if (m >= M) {
         const h8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (int j = tid; j < ng; j += kBlock) {
+        for (int j = tid; j < ng; j += ST) {
             h8_t* o = tile + (j / 4) * 128 + 16 * (j % 4);
             o[0] = z;
             o[64] = z;
@@ -95,10 +100,10 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
     }
     const float4* xr = (const float4*)(x + (int64_t)m * ldx);
     const float4* wr = (const float4*)w;
-    float v[kSplitGroups][8];
+    float v[NG][8];
 #pragma unroll
-    for (int i = 0; i < kSplitGroups; ++i) {
-        const int j = tid + i * kBlock;
+    for (int i = 0; i < NG; ++i) {
+        const int j = tid + i * ST;
         const int jj = j < ng ? j : ng - 1;  // a clamped re-read, masked below
         const float4 a = xr[2 * jj], b = xr[2 * jj + 1];
         v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
@@ -108,18 +113,20 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
     if (w) {
         double ss = 0;
 #pragma unroll
-        for (int i = 0; i < kSplitGroups; ++i)
-            if (tid + i * kBlock < ng)
+        for (int i = 0; i < NG; ++i)
+            if (tid + i * ST < ng)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) ss += (double)v[i][e] * v[i][e];
         ss = wave_sum_d(ss);
-        if ((tid & 63) == 0) red_d[tid >> 6] = ss;
-        __syncthreads();
-        ss = (red_d[0] + red_d[1]) + (red_d[2] + red_d[3]);
+        if (WPR > 1) {
+            if ((tid & 63) == 0) red_d[tid >> 6] = ss;
+            __syncthreads();
+            ss = (red_d[0] + red_d[1]) + (red_d[2] + red_d[3]);
+        }
         inv = 1.0f / sqrtf((float)(ss / K) + eps);
 #pragma unroll
-        for (int i = 0; i < kSplitGroups; ++i) {
-            int j = tid + i * kBlock;
+        for (int i = 0; i < NG; ++i) {
+            int j = tid + i * ST;
             j = j < ng ? j : ng - 1;
             const float4 a = wr[2 * j], b = wr[2 * j + 1];
             const float g[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -129,14 +136,16 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
     }
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kSplitGroups; ++i)
-        if (tid + i * kBlock < ng)
+    for (int i = 0; i < NG; ++i)
+        if (tid + i * ST < ng)
 #pragma unroll
             for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
     amax = wave_max(amax);
-    if ((tid & 63) == 0) red_f[tid >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    if (WPR > 1) {
+        if ((tid & 63) == 0) red_f[tid >> 6] = amax;
+        __syncthreads();
+        amax = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    }
     int ex = 0;
     (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
     int e2 = amax > 0.0f ? 15 - ex : 0;
@@ -144,8 +153,8 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
     const float sc = ldexpf(1.0f, e2);
     if (tid == 0) rs[m] = ldexpf(1.0f, -e2);
 #pragma unroll
-    for (int i = 0; i < kSplitGroups; ++i) {
-        const int j = tid + i * kBlock;
+    for (int i = 0; i < NG; ++i) {
+        const int j = tid + i * ST;
         if (j < ng) {
             h8_t hi, lo;
 #pragma unroll
@@ -954,7 +963,22 @@ hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, flo
                            uint16_t* xa, float* rs, hipStream_t st) {
     if (K % 32 != 0 || K > kBlock * 8 * kSplitGroups || ldx % 4 != 0 || Mpad % kPfTileM != 0 || M > Mpad)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_split, dim3(Mpad), dim3(kBlock), 0, st, x, ldx, norm_w, eps, K, M, (h8_t*)xa, rs);
+    // a wave per row while a lane holds at most 16 groups (rows up to 8192), else a workgroup
+    const int per1 = (K / 8 + 63) / 64;
+#define TF_SPLIT(NG, WPR, rows)                                                                              \
+    hipLaunchKernelGGL((k_pf_split<NG, WPR>), dim3((unsigned)(Mpad / (rows))), dim3(kBlock), 0, st, x, ldx, \
+                       norm_w, eps, K, M, (h8_t*)xa, rs)
+    if (per1 <= 2)
+        TF_SPLIT(2, 1, kWavesPerBlock);
+    else if (per1 <= 4)
+        TF_SPLIT(4, 1, kWavesPerBlock);
+    else if (per1 <= 8)
+        TF_SPLIT(8, 1, kWavesPerBlock);
+    else if (per1 <= 16)
+        TF_SPLIT(16, 1, kWavesPerBlock);
+    else
+        TF_SPLIT(kSplitGroups, 4, 1);  // per4 <= 8: K was checked above
+#undef TF_SPLIT
     return hipGetLastError();
 }
 
