@@ -650,6 +650,27 @@ __global__ __launch_bounds__(kBlock) void k_pf_rope_store(float* qkv, int64_t ld
 
 constexpr int kAttnTile = 32;  // keys per tile record
 
+// Max and sum of v over lanes l, l ^ 16, l ^ 32, l ^ 48 (the 4 lanes of one query in the
+// MFMA layout) with gfx950's lane swaps, no LDS: a swap leaves each lane its own value in
+// one register and its partner's in the other, and every lane adds the lower lane's value
+// first, so the 4 lanes get the same bits.
+__device__ __forceinline__ float quad_max(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t w = __float_as_uint(m);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const uint32_t w = __float_as_uint(s);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Tile record of head size HD: K fragments [16-key half][32-dim chunk][hi, lo][lane][8],
 // V^T fragments [16-dim tile][hi, lo][lane][8], then 2^-ek_j [32] and 2^-ev_j [32] (0 for
 // a zero value row).
@@ -779,8 +800,7 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
 #pragma unroll
             for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        amax = quad_max(amax);
         const int e = pow2_exp(amax, 0);
         const float sc = ldexpf(1.0f, e);
         fq[qs] = ldexpf(scale, -e);
@@ -860,8 +880,7 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
                 p[j] = key <= qpos[qs] ? s[qs][j >> 2][j & 3] * fq[qs] * fkj[j] : -INFINITY;
                 mt = fmaxf(mt, p[j]);
             }
-            mt = fmaxf(mt, __shfl_xor(mt, 16));
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            mt = quad_max(mt);
             const float m_new = fmaxf(m_run[qs], mt);
             const float alpha = expf(m_run[qs] - m_new);  // 0 on the first tile
             float ls = 0.0f, x[8], mx = 0.0f;
@@ -872,10 +891,8 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
                 x[j] = p[j] * fvj[j];
                 mx = fmaxf(mx, x[j]);
             }
-            ls += __shfl_xor(ls, 16);
-            ls += __shfl_xor(ls, 32);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            ls = quad_sum(ls);
+            mx = quad_max(mx);
             l_run[qs] = fmaf(l_run[qs], alpha, ls);
             m_run[qs] = m_new;
             // the tile's unit: its largest term in [2^14, 2^15); no change when it adds
