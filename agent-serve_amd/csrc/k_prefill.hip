@@ -829,11 +829,15 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
     // two records in flight in registers: a record is loaded two tiles before its use
     uint4 pa[PF], pb[PF];
     const uint4* src = (const uint4*)(recs + (int64_t)g * T * attn_rec_bytes(HD));
+    // unconditional loads (tile and index clamped; the stores skip the copies): a load
+    // behind a branch makes the compiler's next wait drain every load in flight, the other
+    // record's included
     auto gload = [&](uint4 (&pf)[PF], int t) {
+        t = t < n_tiles ? t : n_tiles - 1;  // past the last tile: a re-read, never stored
 #pragma unroll
         for (int i = 0; i < PF; ++i) {
             const int idx = tid + i * nthr;
-            if (idx < RU) pf[i] = gload_u4(src + (int64_t)t * RU + idx);
+            pf[i] = gload_u4(src + (int64_t)t * RU + (idx < RU ? idx : RU - 1));
         }
     };
     auto lstore = [&](const uint4 (&pf)[PF], int buf) {
@@ -928,18 +932,18 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
     };
 
     gload(pa, 0);
-    if (1 < n_tiles) gload(pb, 1);
+    gload(pb, 1);
     lstore(pa, 0);
     __syncthreads();
     for (int t = 0; t < n_tiles; t += 2) {
         // tile t in buffer 0; pa is free, pb holds tile t + 1
-        if (t + 2 < n_tiles) gload(pa, t + 2);
+        gload(pa, t + 2);
         tile((const unsigned char*)lds_rec, t);
         if (t + 1 < n_tiles) lstore(pb, 1);
         __syncthreads();
         if (t + 1 >= n_tiles) break;
         // tile t + 1 in buffer 1; pb is free, pa holds tile t + 2
-        if (t + 3 < n_tiles) gload(pb, t + 3);
+        gload(pb, t + 3);
         tile((const unsigned char*)(lds_rec + RU), t + 1);
         if (t + 2 < n_tiles) lstore(pa, 0);
         __syncthreads();
