@@ -274,7 +274,8 @@ def prefill_leg(pkg, threads, reps=5):
         "achieved_tflop_s": round(tflops, 2), "mfma_peak_tflop_s": MFMA_F16_PEAK_TFLOPS,
         "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
         "mfma_note": "algorithmic FLOP/s over the dense fp16 MFMA peak; the GEMMs issue two fp16 MFMAs "
-                     "(activation hi and lo) per algorithmic product, attention runs on fp32 MFMA",
+                     "(activation hi and lo) per algorithmic product, attention three fp16 MFMAs per "
+                     "product (fp16 operand pairs)",
         "weight_pack": {"ms": round(first_wall * 1e3 - statistics.median(wall), 1),
                         "bytes": 2 * weights,
                         "note": "one-time per context, excluded from device_ms: layer matrices' integers as fp16 "
