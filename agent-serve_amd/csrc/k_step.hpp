@@ -997,7 +997,13 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 const int D = sc.D;
                 float wr[NWR];
                 load_norm(ly.ffn_norm, D, wr);
-                const int gu_groups[3] = {(int)((ly.wg.N + 1) / 2), 0, 0};
+                // gate/up rows per group: one for Q8_0 (gate/up rows are then dealt one at a
+                // time, so no wave holds a whole group more than another: 8960 rows on 2048
+                // waves give 5 or 4 instead of 3 or 2 pairs, and two streams per wave keep
+                // enough loads in flight), two for the 4-bit formats (their rows are half the
+                // bytes; one row per group measured 1.8% slower on the mixed-Q4 model)
+                constexpr int kGuR = TL == TF_HIP_TYPE_Q8_0 ? 1 : 2;
+                const int gu_groups[3] = {(int)((ly.wg.N + kGuR - 1) / kGuR), 0, 0};
                 auto gu_seg = [&](int, int what) -> const DevMat& { return what == 1 ? ly.wu : ly.wg; };
                 auto gu_epi = [&](int, int row, float v, float up, float) {
                     put(X(sc.HH) + par * sc.F + row, (v / (1.0f + expf(-v))) * up, E(t, l, 4));
@@ -1107,7 +1113,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         issue_down(ly);
                         gu_input();
                     };
-                    gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                    gemv_phase<TL, kGuR, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, down_then_input, gu_epi);
                 } else if (!split && wg >= attn_wg0) {
                     const int g = wg - attn_wg0;
@@ -1129,7 +1135,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         issue_down(ly);
                         gu_input();
                     };
-                    gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                    gemv_phase<TL, kGuR, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, down_then_input, gu_epi);
                 } else if (all) {
                     // Every workgroup split the attention: the merged output comes right after
@@ -1139,7 +1145,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     issue_down(ly);
                     wo_phase(sc.nwg * kNW);
                     STEP_STAMP(l, 5);
-                    gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                    gemv_phase<TL, kGuR, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, gu_input, gu_epi);
                 } else {
                     // The attention runs on other workgroups for several microseconds: gate/up's
@@ -1151,7 +1157,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         __syncthreads();  // every wave's wo rows are read out of xs before the input is staged
                         gu_input();
                     };
-                    gemv_phase<TL, 2, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
+                    gemv_phase<TL, kGuR, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, wo_then_input, gu_epi);
                 }
             }
