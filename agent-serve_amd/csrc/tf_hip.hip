@@ -627,39 +627,44 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
         for (int i = 0; i < 13; ++i)
             if (cnt[i] > 0)
                 std::fprintf(stderr, "  %-16s med %6.2f max %6.2f\n", nm[i], med[i] / cnt[i], mx[i] / cnt[i]);
-        // the workgroups that finish gate/up last (mean over layers of gate/up's input and end,
-        // relative to the layer's earliest start), and the mean end per eighth of the grid
+        // per phase end (qkv, wo, gate/up, down): the mean stamp per eighth of the grid and the
+        // last workgroups (means over layers, relative to the layer's earliest start)
         {
-            std::vector<double> gin(W, 0.0), gdone(W, 0.0);
-            int nl = 0;
-            for (int l = 1; l + 1 < L; ++l) {
-                unsigned long long t0 = ~0ull;
-                for (int w = 0; w < W; ++w) {
-                    const unsigned long long st = h[((size_t)l * W + w) * 16];
-                    if (st) t0 = std::min(t0, st);
+            const int ends[4] = {2, 5, 7, 9};
+            const char* en[4] = {"qkv done", "wo done", "gu done", "down done"};
+            for (int k = 0; k < 4; ++k) {
+                std::vector<double> v(W, 0.0);
+                std::vector<int> n_l(W, 0);
+                for (int l = 1; l + 1 < L; ++l) {
+                    unsigned long long t0 = ~0ull;
+                    for (int w = 0; w < W; ++w) {
+                        const unsigned long long st = h[((size_t)l * W + w) * 16];
+                        if (st) t0 = std::min(t0, st);
+                    }
+                    if (t0 == ~0ull) continue;
+                    for (int w = 0; w < W; ++w) {
+                        const unsigned long long q = h[((size_t)l * W + w) * 16 + ends[k]];
+                        if (q) {
+                            v[w] += (double)(q - t0) / 100.0;
+                            ++n_l[w];
+                        }
+                    }
                 }
-                if (t0 == ~0ull) continue;
-                ++nl;
-                for (int w = 0; w < W; ++w) {
-                    const unsigned long long* q = &h[((size_t)l * W + w) * 16];
-                    if (q[6]) gin[w] += (double)(q[6] - t0) / 100.0;
-                    if (q[7]) gdone[w] += (double)(q[7] - t0) / 100.0;
-                }
-            }
-            if (nl > 0) {
-                std::vector<int> idx(W);
-                for (int w = 0; w < W; ++w) idx[w] = w;
-                std::sort(idx.begin(), idx.end(), [&](int x, int y) { return gdone[x] > gdone[y]; });
-                std::fprintf(stderr, "  gate/up last:");
-                for (int i = 0; i < std::min(W, 8); ++i)
-                    std::fprintf(stderr, " wg %d in %.2f done %.2f;", idx[i], gin[idx[i]] / nl, gdone[idx[i]] / nl);
-                std::fprintf(stderr, "\n  gate/up done by grid eighth:");
+                std::fprintf(stderr, "  %-10s by eighth:", en[k]);
                 for (int e = 0; e < 8; ++e) {
                     double sum = 0;
-                    int k = 0;
-                    for (int w = e * W / 8; w < (e + 1) * W / 8; ++w, ++k) sum += gdone[w] / nl;
-                    std::fprintf(stderr, " %.2f", k ? sum / k : 0.0);
+                    int cnt_w = 0;
+                    for (int w = e * W / 8; w < (e + 1) * W / 8; ++w)
+                        if (n_l[w]) {
+                            sum += v[w] / n_l[w];
+                            ++cnt_w;
+                        }
+                    std::fprintf(stderr, " %6.2f", cnt_w ? sum / cnt_w : 0.0);
                 }
+                int last = -1;
+                for (int w = 0; w < W; ++w)
+                    if (n_l[w] && (last < 0 || v[w] / n_l[w] > v[last] / n_l[last])) last = w;
+                if (last >= 0) std::fprintf(stderr, "  last wg %d %.2f", last, v[last] / n_l[last]);
                 std::fprintf(stderr, "\n");
             }
         }
