@@ -60,7 +60,8 @@ size_t step_lds_bytes(int n_layer, int D, int F, int H, int G, int hd, int n_wg,
 }
 
 int step_stage_lds(int tl, int n_layer, int D, int F, int H, int G, int hd, int n_wg) {
-    if (tl != TF_HIP_TYPE_Q8_0 || F % 32 != 0 || D % 32 != 0 || D < 64 || F < 64) return 0;
+    if ((tl != TF_HIP_TYPE_Q8_0 && tl != TF_HIP_TYPE_Q4_0) || F % 32 != 0 || D % 32 != 0 || D < 64 || F < 64)
+        return 0;
     int dev = 0, max_lds = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
@@ -71,7 +72,8 @@ int step_stage_lds(int tl, int n_layer, int D, int F, int H, int G, int hd, int 
     // busy) instead of leaving most waves without a row (measured on the Qwen2.5-0.5B shape,
     // 896 rows: 0.668 against 0.688 ms per token; with 1536 and 2048 rows the row per wave is
     // faster)
-    if (2 * D < n_wg * step_detail::kNW && step_detail::down_split_ok(D, F, n_wg) && fits(2)) return 2;
+    if (tl == TF_HIP_TYPE_Q8_0 && 2 * D < n_wg * step_detail::kNW && step_detail::down_split_ok(D, F, n_wg) && fits(2))
+        return 2;
     if (D <= n_wg * step_detail::kNW && fits(1)) return 1;
     return 0;
 }

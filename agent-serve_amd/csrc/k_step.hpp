@@ -785,19 +785,21 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
     auto no_bias = [](int) -> const float* { return nullptr; };
     const int n_tokens = args.n_tokens;
     int tok = 0;
-    // Staged weight rows: a wave copies a Q8_0 row (q bytes, then fp16 scales) into an LDS
-    // slot of its own with direct global->LDS loads, ahead of the phase that reads it: lane
-    // i of a load lands at slot + 16 i (4 i for the scales). Lanes past the row's end re-read
-    // its last bytes; what they write past the row is never read.
-    auto stage_row = [&](const uint8_t* q, const uint8_t* d, int K, unsigned char* slot) {
-        const int qsteps = (K + 1023) / 1024, dbytes = K / 16, dsteps = (dbytes + 255) / 256;
+    // Staged weight rows: a wave copies a Q8_0 or Q4_0 row (qbytes of quants, then its fp16
+    // scales, K / 16 bytes for both formats) into an LDS slot of its own with direct
+    // global->LDS loads, ahead of the phase that reads it: lane i of a load lands at slot +
+    // 16 i (4 i for the scales). The scales start at the slot's Q8_0 offset (K rounded up to
+    // 1 KiB) for both formats. Lanes past the row's end re-read its last bytes; what they
+    // write past the row is never read.
+    auto stage_row = [&](const uint8_t* q, int qbytes, const uint8_t* d, int K, unsigned char* slot) {
+        const int qsteps = (qbytes + 1023) / 1024, dbytes = K / 16, dsteps = (dbytes + 255) / 256;
         for (int i = 0; i < qsteps; ++i) {
             int o = 1024 * i + 16 * lane;
-            o = o < K ? o : K - 16;
+            o = o < qbytes ? o : qbytes - 16;
             __builtin_amdgcn_global_load_lds((const TF_GLOBAL void*)(q + o),
                                              (__attribute__((address_space(3))) void*)(slot + 1024 * i), 16, 0, 0);
         }
-        unsigned char* dslot = slot + qsteps * 1024;
+        unsigned char* dslot = slot + (K + 1023) / 1024 * 1024;
         for (int i = 0; i < dsteps; ++i) {
             int o = 256 * i + 4 * lane;
             o = o < dbytes ? o : dbytes - 4;
@@ -805,16 +807,17 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                                              (__attribute__((address_space(3))) void*)(dslot + 256 * i), 4, 0, 0);
         }
     };
-    // Dot of the staged row in `slot` with xs, in gemv_phase's lane-step order and reduction.
+    // Dot of the staged row in `slot` with xs (format TL), in gemv_phase's lane-step order
+    // and reduction, so the same bits as the register path.
     auto staged_dot = [&](const unsigned char* slot, int K) -> float {
-        using F8 = Fmt<TF_HIP_TYPE_Q8_0>;
+        using FS = Fmt<TL == TF_HIP_TYPE_Q4_0 ? TF_HIP_TYPE_Q4_0 : TF_HIP_TYPE_Q8_0>;
         const uint16_t* dsl = (const uint16_t*)(slot + (K + 1023) / 1024 * 1024);
         float acc = 0.0f;
-        for (int s = lane; s < K / 16; s += kWave) {
-            typename F8::Raw w;
+        for (int s = lane; s < K / FS::E; s += kWave) {
+            typename FS::Raw w;
             w.q = *(const uint4*)(slot + 16 * s);
-            w.d = dsl[s >> 1];
-            acc += F8::dot(w, xs, x16, s);
+            w.d = FS::E == 16 ? dsl[s >> 1] : dsl[s];  // one fp16 scale per 32 elements
+            acc += FS::dot(w, xs, x16, s);
         }
         return wave_sum(acc);
     };
@@ -823,16 +826,17 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
     // load lands at +16 i for the q bytes, +4 i for the scales). Lanes past the run load
     // nothing.
     auto issue_down = [&](const StepLayer& ly) {
-        if constexpr (TL == TF_HIP_TYPE_Q8_0) {
+        if constexpr (TL == TF_HIP_TYPE_Q8_0 || TL == TF_HIP_TYPE_Q4_0) {
             if constexpr (!DSPLIT) {
                 // one row per wave: row wid. (One return for both conditions: with two, the
                 // compiler's wait-count pass put an s_waitcnt vmcnt(0) after the staging, for
                 // the LDS reads that follow, and the gate/up phase then waited for the row;
                 // measured as 2% of the Qwen2.5-1.5B shape's token time.)
+                // A layer whose ffn_down has the other format (TA) is not staged.
                 const int wid = wg * kNW + wave;
-                if (sc.o_down == 0 || wid >= (int)ly.wd.N) return;
-                const int K = sc.F;
-                stage_row(ly.wd.q + (int64_t)wid * K, ly.wd.s + (int64_t)wid * (K / 16), K,
+                if (sc.o_down == 0 || wid >= (int)ly.wd.N || (int)ly.wd.type != TL) return;
+                const int K = sc.F, qbytes = TL == TF_HIP_TYPE_Q8_0 ? K : K / 2;
+                stage_row(ly.wd.q + (int64_t)wid * qbytes, qbytes, ly.wd.s + (int64_t)wid * (K / 16), K,
                           smem + sc.o_down + wave * sc.down_slot);
                 return;
             }
@@ -1179,8 +1183,8 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     if (last && sc.a.taps) *gptr(sc.a.taps + (size_t)l * sc.D + row) = nv;
                 };
                 bool staged = false;
-                if constexpr (TL == TF_HIP_TYPE_Q8_0) {
-                    if (sc.o_down) {
+                if constexpr (TL == TF_HIP_TYPE_Q8_0 || TL == TF_HIP_TYPE_Q4_0) {
+                    if (sc.o_down && (int)ly.wd.type == TL) {
                         // the slices were staged in LDS during gate/up
                         staged = true;
                         __syncthreads();
