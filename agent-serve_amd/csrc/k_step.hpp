@@ -710,10 +710,10 @@ struct StepConst {
 // layer (the runtime type picks the instantiation); TO: the lm_head's (and embedding's).
 // DSPLIT: ffn_down staged split over K in each workgroup (else a row per wave, when staged);
 // a template argument so that the row-per-wave build carries none of the split's code.
-// UQ: lane steps per tile of the d_model-long Q8_0 rows (QKV, wo, gate/up): 2 covers a
+// UQ: lane steps per tile of the d_model-long Q8_0 rows (QKV, wo, gate/up, lm_head): 2 covers a
 // 2048-element row in one tile; 1 for rows of at most 1024 elements (one tile of 64 lanes
 // already covers them, and a second step would be masked out on most lanes: the
-// Qwen2.5-0.5B shape's 896-element rows decode 5% faster with 1, the 2048-element rows of
+// Qwen2.5-0.5B shape's 896-element rows decode 7% faster with 1, the 2048-element rows of
 // Llama-3.2-1B 3% slower).
 template <int TL, int TO, int HDM, int TA, bool DSPLIT, int UQ>
 __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
@@ -722,7 +722,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
     // lane steps per tile of the d_model-long rows (QKV, wo, gate/up, lm_head): one for the
     // 32-element formats, whose 2048-element rows are 64 steps (a second would be masked
     // out on every lane); ffn_down's n_ff-long rows keep two
-    constexpr int UL = Fmt<TL>::E >= 32 ? 1 : UQ, UA = Fmt<TA>::E >= 32 ? 1 : UQ, UO = Fmt<TO>::E >= 32 ? 1 : 2;
+    constexpr int UL = Fmt<TL>::E >= 32 ? 1 : UQ, UA = Fmt<TA>::E >= 32 ? 1 : UQ, UO = Fmt<TO>::E >= 32 ? 1 : UQ;
     constexpr int NWR = 8;  // norm weights per thread: d_model <= 4096
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ __align__(16) unsigned char sc_raw[sizeof(StepConst)];  // StepConst is not trivially constructible
