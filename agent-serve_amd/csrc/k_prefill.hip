@@ -568,28 +568,42 @@ __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a)
     }
 }
 
-// Sums the a.ks partial rows of a split-K GEMM in slice order and applies the epilogue:
-// thread per output column of row blockIdx.y.
-template <int MODE>
+// Sums the KS (= a.ks) partial rows of a split-K GEMM in slice order and applies the
+// epilogue: thread per 4 output columns of row blockIdx.y, the KS slices' loads issued
+// together (a loop over a run-time count would wait for each before the next).
+template <int MODE, int KS>
 __global__ __launch_bounds__(kBlock) void k_pf_reduce(const PfGemmArgs a) {
     const int row = blockIdx.y;
-    const int col = blockIdx.x * kBlock + threadIdx.x;
+    const int col0 = (blockIdx.x * kBlock + threadIdx.x) * 4;
     const int ntot = a.n_sub * 16;
-    if (col >= ntot) return;
-    const float* p = a.part + (int64_t)row * ntot + col;
-    float v = 0.0f;
-    for (int k = 0; k < a.ks; ++k) v += p[(int64_t)k * a.Mpad * ntot];
-    const int u = col / 16;
+    if (col0 >= ntot) return;
+    const float* p = a.part + (int64_t)row * ntot + col0;
+    float4 pv[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) pv[k] = *(const float4*)(p + (int64_t)k * a.Mpad * ntot);
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        v[0] += pv[k].x;
+        v[1] += pv[k].y;
+        v[2] += pv[k].z;
+        v[3] += pv[k].w;
+    }
+    // a 16-column subtile never straddles two segments, so neither do the 4 columns
+    const int u = col0 / 16;
     const int seg = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
-    const int c = col - PF_SEL(seg, sub0) * 16;
-    float* y = PF_SEL(seg, y) + (int64_t)row * PF_SEL(seg, ldy) + c;
-    if (MODE == GEMV_STORE) {
-        const float* bias = PF_SEL(seg, bias);
-        *y = bias ? v + bias[c] : v;
-    } else {
-        const float nv = *y + v;
-        *y = nv;
-        if (row == a.tap_row && a.tap) a.tap[c] = nv;
+    const int c0 = col0 - PF_SEL(seg, sub0) * 16;
+    float* y = PF_SEL(seg, y) + (int64_t)row * PF_SEL(seg, ldy) + c0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (MODE == GEMV_STORE) {
+            const float* bias = PF_SEL(seg, bias);
+            y[e] = bias ? v[e] + bias[c0 + e] : v[e];
+        } else {
+            const float nv = y[e] + v[e];
+            y[e] = nv;
+            if (row == a.tap_row && a.tap) a.tap[c0 + e] = nv;
+        }
     }
 }
 
@@ -1072,11 +1086,20 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st) {
             }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess || ks == 1) return e;
-            const dim3 rgrid((unsigned)((a.n_sub * 16 + kBlock - 1) / kBlock), (unsigned)a.M);
-            if (a.mode == GEMV_STORE)
-                hipLaunchKernelGGL(k_pf_reduce<GEMV_STORE>, rgrid, dim3(kBlock), 0, st, b);
-            else
-                hipLaunchKernelGGL(k_pf_reduce<GEMV_RESID>, rgrid, dim3(kBlock), 0, st, b);
+            const dim3 rgrid((unsigned)((a.n_sub * 4 + kBlock - 1) / kBlock), (unsigned)a.M);
+#define PF_REDUCE(MODE, KS) hipLaunchKernelGGL((k_pf_reduce<MODE, KS>), rgrid, dim3(kBlock), 0, st, b)
+            switch ((a.mode == GEMV_STORE ? 0 : 32) + ks) {  // ks is 2, 4, 8 or 16 here
+                case 2: PF_REDUCE(GEMV_STORE, 2); break;
+                case 4: PF_REDUCE(GEMV_STORE, 4); break;
+                case 8: PF_REDUCE(GEMV_STORE, 8); break;
+                case 16: PF_REDUCE(GEMV_STORE, 16); break;
+                case 34: PF_REDUCE(GEMV_RESID, 2); break;
+                case 36: PF_REDUCE(GEMV_RESID, 4); break;
+                case 40: PF_REDUCE(GEMV_RESID, 8); break;
+                case 48: PF_REDUCE(GEMV_RESID, 16); break;
+                default: return hipErrorInvalidValue;
+            }
+#undef PF_REDUCE
             return hipGetLastError();
         }
     }
