@@ -71,44 +71,16 @@ __global__ __launch_bounds__(kBlock) void k_pf_pack_q8(const uint8_t* q, int K, 
 
 constexpr int kSplitGroups = 8;  // 8-element groups per thread: rows up to 256 * 8 * 8 = 16384
 
-// WPR waves per row (1: a workgroup takes 4 consecutive rows, a wave each, and reduces
-// within the wave; 4: a workgroup per row), the row held in registers (thread t of the row
-// owns the 8-element groups t, t + 64 WPR, ..., NG of them: the fewest that cover the row):
-// the rmsnorm scale inv (when w is given), a power of two sc putting max |row| in
-// [2^14, 2^15) (rs = 1 / sc), then every element as hi + lo into the fragment layout (16
-// bytes of a hi and of a lo fragment per group; with a wave per row, the 4 rows of a
-// workgroup fill whole 64-byte lines of a fragment). Rows M.. are zeros with rs = 0.
+// The split of row m whose values thread tid holds as v[i] = 8-element group tid + i ST
+// (ST = 64 WPR threads per row; groups past K / 8 hold clamped re-reads, masked here):
+// rmsnorm with weight w when given, the power-of-two scale, hi + lo into the fragments.
 template <int NG, int WPR>
-__global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx, const float* w, float eps, int K,
-                                                     int M, h8_t* xa, float* rs) {
-    constexpr int ST = 64 * WPR;  // threads per row
-    __shared__ double red_d[kWavesPerBlock];
-    __shared__ float red_f[kWavesPerBlock];
-    const int m = WPR == 1 ? blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6) : blockIdx.x;
-    const int tid = WPR == 1 ? threadIdx.x & 63 : threadIdx.x;
+__device__ __forceinline__ void split_emit(float (&v)[NG][8], int tid, int m, int K, const float* w, float eps,
+                                           h8_t* xa, float* rs, double* red_d, float* red_f) {
+    constexpr int ST = 64 * WPR;
     const int ng = K / 8, nblk = K / 32;
     h8_t* tile = xa + (int64_t)(m / 16) * nblk * 128 + (m % 16);
-    if (m >= M) {
-        const h8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (int j = tid; j < ng; j += ST) {
-            h8_t* o = tile + (j / 4) * 128 + 16 * (j % 4);
-            o[0] = z;
-            o[64] = z;
-        }
-        if (tid == 0) rs[m] = 0.0f;
-        return;
-    }
-    const float4* xr = (const float4*)(x + (int64_t)m * ldx);
     const float4* wr = (const float4*)w;
-    float v[NG][8];
-#pragma unroll
-    for (int i = 0; i < NG; ++i) {
-        const int j = tid + i * ST;
-        const int jj = j < ng ? j : ng - 1;  // a clamped re-read, masked below
-        const float4 a = xr[2 * jj], b = xr[2 * jj + 1];
-        v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
-        v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
-    }
     float inv = 1.0f;
     if (w) {
         double ss = 0;
@@ -168,6 +140,53 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
             o[64] = lo;
         }
     }
+}
+
+// Zeros of padding row m's fragments (rs = 0), ST threads.
+template <int ST>
+__device__ __forceinline__ void split_zero(int tid, int m, int K, h8_t* xa, float* rs) {
+    const int ng = K / 8, nblk = K / 32;
+    h8_t* tile = xa + (int64_t)(m / 16) * nblk * 128 + (m % 16);
+    const h8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = tid; j < ng; j += ST) {
+        h8_t* o = tile + (j / 4) * 128 + 16 * (j % 4);
+        o[0] = z;
+        o[64] = z;
+    }
+    if (tid == 0) rs[m] = 0.0f;
+}
+
+// WPR waves per row (1: a workgroup takes 4 consecutive rows, a wave each, and reduces
+// within the wave; 4: a workgroup per row), the row held in registers (thread t of the row
+// owns the 8-element groups t, t + 64 WPR, ..., NG of them: the fewest that cover the row):
+// the rmsnorm scale inv (when w is given), a power of two sc putting max |row| in
+// [2^14, 2^15) (rs = 1 / sc), then every element as hi + lo into the fragment layout (16
+// bytes of a hi and of a lo fragment per group; with a wave per row, the 4 rows of a
+// workgroup fill whole 64-byte lines of a fragment). Rows M.. are zeros with rs = 0.
+template <int NG, int WPR>
+__global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx, const float* w, float eps, int K,
+                                                     int M, h8_t* xa, float* rs) {
+    constexpr int ST = 64 * WPR;  // threads per row
+    __shared__ double red_d[kWavesPerBlock];
+    __shared__ float red_f[kWavesPerBlock];
+    const int m = WPR == 1 ? blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6) : blockIdx.x;
+    const int tid = WPR == 1 ? threadIdx.x & 63 : threadIdx.x;
+    const int ng = K / 8;
+    if (m >= M) {
+        split_zero<ST>(tid, m, K, xa, rs);
+        return;
+    }
+    const float4* xr = (const float4*)(x + (int64_t)m * ldx);
+    float v[NG][8];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const int j = tid + i * ST;
+        const int jj = j < ng ? j : ng - 1;  // a clamped re-read, masked below
+        const float4 a = xr[2 * jj], b = xr[2 * jj + 1];
+        v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+        v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+    }
+    split_emit<NG, WPR>(v, tid, m, K, w, eps, xa, rs, red_d, red_f);
 }
 
 // ---------------------------------------------------------------- Q8_0 GEMM
@@ -609,6 +628,56 @@ __global__ __launch_bounds__(kBlock) void k_pf_reduce(const PfGemmArgs a) {
 
 #undef PF_SEL
 
+// k_pf_reduce of a GEMV_RESID GEMM with one segment, fused with the split of the
+// updated rows (k_pf_split with a workgroup per row): thread t owns the 8-column groups
+// t, t + 256, ..., adds the KS slices in slice order and then the residual, as
+// k_pf_reduce does, stores the row and splits it. Rows M.. get the padding zeros.
+template <int KS, int NG>
+__global__ __launch_bounds__(kBlock) void k_pf_reduce_split(const PfGemmArgs a) {
+    __shared__ double red_d[kWavesPerBlock];
+    __shared__ float red_f[kWavesPerBlock];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const int K = a.n_sub * 16, ng = K / 8;
+    if (m >= a.M) {
+        split_zero<kBlock>(tid, m, K, (h8_t*)a.split_xa, a.split_rs);
+        return;
+    }
+    const float* p = a.part + (int64_t)m * K;
+    float* y = a.seg[0].y + (int64_t)m * a.seg[0].ldy;
+    const int64_t sstride = (int64_t)a.Mpad * K;
+    float v[NG][8];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const int j = tid + i * kBlock;
+        const int jj = j < ng ? j : ng - 1;  // a clamped re-read, masked below
+        float4 pv[KS][2];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            pv[k][0] = *(const float4*)(p + k * sstride + 8 * jj);
+            pv[k][1] = *(const float4*)(p + k * sstride + 8 * jj + 4);
+        }
+        const float4 y0 = *(const float4*)(y + 8 * jj), y1 = *(const float4*)(y + 8 * jj + 4);
+        float sm[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            sm[0] += pv[k][0].x; sm[1] += pv[k][0].y; sm[2] += pv[k][0].z; sm[3] += pv[k][0].w;
+            sm[4] += pv[k][1].x; sm[5] += pv[k][1].y; sm[6] += pv[k][1].z; sm[7] += pv[k][1].w;
+        }
+        const float yv[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = yv[e] + sm[e];
+        if (j < ng) {
+            *(float4*)(y + 8 * j) = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+            *(float4*)(y + 8 * j + 4) = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+            if (m == a.tap_row && a.tap)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) a.tap[8 * j + e] = v[i][e];
+        }
+    }
+    split_emit<NG, 4>(v, tid, m, K, a.split_w, a.split_eps, (h8_t*)a.split_xa, a.split_rs, red_d, red_f);
+}
+
+
 // ---------------------------------------------------------------- RoPE and KV store
 
 // Row i is position pos0 + i: q heads rotated in place, k heads rotated into the cache,
@@ -1026,7 +1095,8 @@ hipError_t launch_pf_pack_q8(const DevMat& m, uint16_t* wf, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st) {
+hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* split_done) {
+    if (split_done) *split_done = false;
     if (a.K % 64 != 0 || a.Mpad % kPfTileM != 0 || a.M > a.Mpad || a.M <= 0 || a.n_sub <= 0 || a.n_seg < 1 ||
         a.n_seg > 3)
         return hipErrorInvalidValue;
@@ -1086,6 +1156,31 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st) {
             }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess || ks == 1) return e;
+            const int ngr = a.n_sub * 2;  // 8-column groups of an output row
+            if (a.mode == GEMV_RESID && a.split_xa && a.split_rs && a.n_seg == 1 && a.seg[0].ldy % 4 == 0 && a.seg[0].ldy >= ngr * 8 &&
+                ((uintptr_t)a.seg[0].y & 15) == 0 && ngr <= 4 * kBlock) {
+                const int ng = ngr <= kBlock ? 1 : (ngr <= 2 * kBlock ? 2 : 4);
+#define PF_RSPLIT(KS, NG) hipLaunchKernelGGL((k_pf_reduce_split<KS, NG>), dim3((unsigned)a.Mpad), dim3(kBlock), 0, st, b)
+                switch (ks * 8 + ng) {  // ks is 2, 4, 8 or 16 here
+                    case 17: PF_RSPLIT(2, 1); break;
+                    case 18: PF_RSPLIT(2, 2); break;
+                    case 20: PF_RSPLIT(2, 4); break;
+                    case 33: PF_RSPLIT(4, 1); break;
+                    case 34: PF_RSPLIT(4, 2); break;
+                    case 36: PF_RSPLIT(4, 4); break;
+                    case 65: PF_RSPLIT(8, 1); break;
+                    case 66: PF_RSPLIT(8, 2); break;
+                    case 68: PF_RSPLIT(8, 4); break;
+                    case 129: PF_RSPLIT(16, 1); break;
+                    case 130: PF_RSPLIT(16, 2); break;
+                    case 132: PF_RSPLIT(16, 4); break;
+                    default: return hipErrorInvalidValue;
+                }
+#undef PF_RSPLIT
+                e = hipGetLastError();
+                if (e == hipSuccess && split_done) *split_done = true;
+                return e;
+            }
             const dim3 rgrid((unsigned)((a.n_sub * 4 + kBlock - 1) / kBlock), (unsigned)a.M);
 #define PF_REDUCE(MODE, KS) hipLaunchKernelGGL((k_pf_reduce<MODE, KS>), rgrid, dim3(kBlock), 0, st, b)
             switch ((a.mode == GEMV_STORE ? 0 : 32) + ks) {  // ks is 2, 4, 8 or 16 here

@@ -938,13 +938,24 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
             s.sub0 = a.n_sub;
             a.n_sub += (int)(w.N / 16);
         };
+        // the residual GEMMs' split-K reduce also splits their rows for the next GEMM when it
+        // can (launch_pf_gemm says whether it did)
+        auto fuse_split = [&](PfGemmArgs& a, const float* norm_w) {
+            a.split_xa = c->pxa;
+            a.split_rs = c->prs;
+            a.split_w = norm_w;
+            a.split_eps = p.rms_eps;
+        };
+        bool x_split = false;  // the attention-norm split of px is in pxa already
         for (int l = 0; l < p.n_layer && e == hipSuccess; ++l) {
             auto M = [&](int k) { return TF_HIP_SLOT_LAYER(l, k); };
             auto V = [&](int k) { return vec(c, TF_HIP_SLOT_LAYER(l, k)); };
             float* kc = c->kc + (size_t)l * c->kv_layer;
             float* vc = c->vc + (size_t)l * c->kv_layer;
-            chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_ATTN_NORM), p.rms_eps, D, nc, Mpad, c->pxa, c->prs,
-                                c->st));
+            if (!x_split)
+                chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_ATTN_NORM), p.rms_eps, D, nc, Mpad, c->pxa, c->prs,
+                                    c->st));
+            x_split = false;
             {
                 PfGemmArgs a = base(D);
                 a.mode = GEMV_STORE;
@@ -962,10 +973,13 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                 PfGemmArgs a = base(Hd);
                 a.mode = GEMV_RESID;
                 seg(a, M(TF_HIP_LAYER_O), c->px, D, nullptr);
-                chk(launch_pf_gemm(a, c->st));
+                fuse_split(a, V(TF_HIP_LAYER_FFN_NORM));
+                bool done = false;
+                chk(launch_pf_gemm(a, c->st, &done));
+                if (!done)
+                    chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_FFN_NORM), p.rms_eps, D, nc, Mpad, c->pxa,
+                                        c->prs, c->st));
             }
-            chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_FFN_NORM), p.rms_eps, D, nc, Mpad, c->pxa, c->prs,
-                                c->st));
             {
                 PfGemmArgs a = base(D);
                 a.mode = GEMV_SILU;
@@ -983,7 +997,8 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                     a.tap = c->taps + (size_t)l * D;
                     a.tap_row = nc - 1;
                 }
-                chk(launch_pf_gemm(a, c->st));
+                if (l + 1 < p.n_layer) fuse_split(a, vec(c, TF_HIP_SLOT_LAYER(l + 1, TF_HIP_LAYER_ATTN_NORM)));
+                chk(launch_pf_gemm(a, c->st, &x_split));
             }
         }
     }
