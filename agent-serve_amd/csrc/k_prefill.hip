@@ -628,6 +628,62 @@ __global__ __launch_bounds__(kBlock) void k_pf_reduce(const PfGemmArgs a) {
 
 #undef PF_SEL
 
+// k_pf_reduce of the q, k and v segments (GEMV_STORE, K split) fused with
+// k_pf_rope_store: thread per rotated pair (j, j + hd / 2) of a q or k head, or per v
+// element, of row blockIdx.y. The slices add in slice order and the bias after them, as
+// k_pf_reduce does, then the rotation of k_pf_rope_store; q goes back to its segment's
+// rows, k and v only to the cache.
+template <int KS>
+__global__ __launch_bounds__(kBlock) void k_pf_reduce_rope(const PfGemmArgs a) {
+    const int i = blockIdx.y, pos = a.pos0 + i;
+    const int hd = a.hd, d2 = hd / 2, G = a.n_kv;
+    const int nq = a.n_head * d2, nk = G * d2, nv = G * hd;
+    const int t = blockIdx.x * kBlock + threadIdx.x;
+    if (t >= nq + nk + nv) return;
+    const int ntot = a.n_sub * 16;
+    const float* p = a.part + (int64_t)i * ntot;
+    const int64_t ss = (int64_t)a.Mpad * ntot;
+    if (t < nq + nk) {
+        const bool isq = t < nq;
+        const int u = isq ? t : t - nq, h = u / d2, j = u % d2, c0 = h * hd + j;
+        const float* bias = isq ? a.seg[0].bias : a.seg[1].bias;
+        const float* ps = p + (isq ? a.seg[0].sub0 : a.seg[1].sub0) * 16 + c0;
+        float p0[KS], p1[KS];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            p0[k] = ps[k * ss];
+            p1[k] = ps[k * ss + d2];
+        }
+        float x0 = 0.0f, x1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            x0 += p0[k];
+            x1 += p1[k];
+        }
+        if (bias) {
+            x0 = x0 + bias[c0];
+            x1 = x1 + bias[c0 + d2];
+        }
+        const float c = a.rope_cos[(int64_t)pos * d2 + j], s = a.rope_sin[(int64_t)pos * d2 + j];
+        const float r0 = fmaf(x0, c, -(x1 * s)), r1 = fmaf(x0, s, x1 * c);
+        float* o = isq ? a.seg[0].y + (int64_t)i * a.seg[0].ldy + h * hd
+                       : a.kc + kv_offset(a.kv_layout, G, a.max_seq, hd, h, pos);
+        o[j] = r0;
+        o[j + d2] = r1;
+    } else {
+        const int u = t - nq - nk, g = u / hd, j = u % hd;
+        const float* ps = p + a.seg[2].sub0 * 16 + u;
+        float pv[KS];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) pv[k] = ps[k * ss];
+        float v = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) v += pv[k];
+        if (a.seg[2].bias) v = v + a.seg[2].bias[u];
+        a.vc[kv_offset(a.kv_layout, G, a.max_seq, hd, g, pos) + j] = v;
+    }
+}
+
 // k_pf_reduce of a GEMV_RESID GEMM with one segment, fused with the split of the
 // updated rows (k_pf_split with a workgroup per row): thread t owns the 8-column groups
 // t, t + 256, ..., adds the KS slices in slice order and then the residual, as
@@ -1095,8 +1151,8 @@ hipError_t launch_pf_pack_q8(const DevMat& m, uint16_t* wf, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* split_done) {
-    if (split_done) *split_done = false;
+hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused) {
+    if (fused) *fused = false;
     if (a.K % 64 != 0 || a.Mpad % kPfTileM != 0 || a.M > a.Mpad || a.M <= 0 || a.n_sub <= 0 || a.n_seg < 1 ||
         a.n_seg > 3)
         return hipErrorInvalidValue;
@@ -1156,6 +1212,24 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* split_done)
             }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess || ks == 1) return e;
+            if (a.mode == GEMV_STORE && a.rope_cos && a.rope_sin && a.kc && a.vc && a.n_seg == 3 && a.hd % 2 == 0 &&
+                a.seg[0].w.N == (int64_t)a.n_head * a.hd && a.seg[1].w.N == (int64_t)a.n_kv * a.hd &&
+                a.seg[2].w.N == (int64_t)a.n_kv * a.hd) {
+                const int items = (a.n_head + a.n_kv) * (a.hd / 2) + a.n_kv * a.hd;
+                const dim3 qgrid((unsigned)((items + kBlock - 1) / kBlock), (unsigned)a.M);
+#define PF_RROPE(KS) hipLaunchKernelGGL((k_pf_reduce_rope<KS>), qgrid, dim3(kBlock), 0, st, b)
+                switch (ks) {
+                    case 2: PF_RROPE(2); break;
+                    case 4: PF_RROPE(4); break;
+                    case 8: PF_RROPE(8); break;
+                    case 16: PF_RROPE(16); break;
+                    default: return hipErrorInvalidValue;
+                }
+#undef PF_RROPE
+                e = hipGetLastError();
+                if (e == hipSuccess && fused) *fused = true;
+                return e;
+            }
             const int ngr = a.n_sub * 2;  // 8-column groups of an output row
             if (a.mode == GEMV_RESID && a.split_xa && a.split_rs && a.n_seg == 1 && a.seg[0].ldy % 4 == 0 && a.seg[0].ldy >= ngr * 8 &&
                 ((uintptr_t)a.seg[0].y & 15) == 0 && ngr <= 4 * kBlock) {
@@ -1178,7 +1252,7 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* split_done)
                 }
 #undef PF_RSPLIT
                 e = hipGetLastError();
-                if (e == hipSuccess && split_done) *split_done = true;
+                if (e == hipSuccess && fused) *fused = true;
                 return e;
             }
             const dim3 rgrid((unsigned)((a.n_sub * 4 + kBlock - 1) / kBlock), (unsigned)a.M);

@@ -962,10 +962,22 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                 seg(a, M(TF_HIP_LAYER_Q), c->pqkv, NQ, V(TF_HIP_LAYER_BQ));
                 seg(a, M(TF_HIP_LAYER_K), c->pqkv + Hd, NQ, V(TF_HIP_LAYER_BK));
                 seg(a, M(TF_HIP_LAYER_V), c->pqkv + Hd + KVd, NQ, V(TF_HIP_LAYER_BV));
-                chk(launch_pf_gemm(a, c->st));
+                a.rope_cos = c->rope_cos;
+                a.rope_sin = c->rope_sin;
+                a.kc = kc;
+                a.vc = vc;
+                a.pos0 = pos0;
+                a.n_head = p.n_head;
+                a.n_kv = p.n_kv_head;
+                a.hd = p.head_dim;
+                a.kv_layout = p.kv_layout;
+                a.max_seq = p.max_seq;
+                bool done = false;
+                chk(launch_pf_gemm(a, c->st, &done));
+                if (!done)
+                    chk(launch_pf_rope_store(c->pqkv, NQ, nc, p.n_head, p.n_kv_head, p.head_dim, c->rope_cos,
+                                             c->rope_sin, pos0, kc, vc, p.kv_layout, p.max_seq, c->st));
             }
-            chk(launch_pf_rope_store(c->pqkv, NQ, nc, p.n_head, p.n_kv_head, p.head_dim, c->rope_cos, c->rope_sin,
-                                     pos0, kc, vc, p.kv_layout, p.max_seq, c->st));
             chk(launch_pf_attn(c->pqkv, NQ, kc, vc, p.kv_layout, p.n_head, p.n_kv_head, p.head_dim, p.max_seq, nc,
                                pos0, start, c->patt, Hd, c->pattn_ws, c->pattn_ws_bytes, c->st));
             chk(launch_pf_split(c->patt, Hd, nullptr, 0.0f, Hd, nc, Mpad, c->pxa, c->prs, c->st));

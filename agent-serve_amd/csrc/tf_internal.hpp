@@ -189,13 +189,21 @@ struct PfGemmArgs {
     float* part = nullptr;         // optional workspace for split-K partial sums (GEMV_STORE, GEMV_RESID)
     size_t part_floats = 0;
     int ks = 1;                    // K slices (set by launch_pf_gemm)
-    // GEMV_RESID over one segment: when split_xa is set and K is split, the reduce also
-    // writes the split of every updated row (launch_pf_split of the output rows, rmsnorm
-    // with split_w when given) to split_xa / split_rs; launch_pf_gemm reports whether it did
+    // Work the split-K reduce can take over from the kernel that follows the GEMM
+    // (launch_pf_gemm reports through *fused whether it did):
+    // GEMV_RESID over one segment, split_xa set: the split of every updated row
+    // (launch_pf_split of the output rows, rmsnorm with split_w when given)
     uint16_t* split_xa = nullptr;
     float* split_rs = nullptr;
     const float* split_w = nullptr;
     float split_eps = 0.0f;
+    // GEMV_STORE of the q, k and v segments, rope_cos set: launch_pf_rope_store of the rows
+    // (q rotated into its segment's rows, k rotated and v into the cache at pos0 + row)
+    const float* rope_cos = nullptr;
+    const float* rope_sin = nullptr;
+    float* kc = nullptr;
+    float* vc = nullptr;
+    int pos0 = 0, n_head = 0, n_kv = 0, hd = 0, kv_layout = 0, max_seq = 0;
 };
 
 bool pf_gemm_supported(int type, int64_t K, int64_t N);
@@ -204,7 +212,7 @@ hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, flo
                            uint16_t* xa, float* rs, hipStream_t st);
 // wf needs m.N * m.K halves.
 hipError_t launch_pf_pack_q8(const DevMat& m, uint16_t* wf, hipStream_t st);
-hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* split_done = nullptr);
+hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused = nullptr);
 hipError_t launch_embed_rows(const DevMat& emb, const int32_t* tok, int n, float* x, int D, hipStream_t st);
 hipError_t launch_pf_rope_store(float* qkv, int64_t ld, int n, int H, int G, int hd, const float* rope_cos,
                                 const float* rope_sin, int pos0, float* kc, float* vc, int layout, int max_seq,
