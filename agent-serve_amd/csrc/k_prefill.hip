@@ -1175,11 +1175,14 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused) {
         if (n_big < cus && a.mode != GEMV_SILU && a.part) {
             // the fewest slices that fill the CUs, each at least 8 stages long (shorter
             // slices spend more on filling their pipeline and on the partial rows they
-            // write than they save); worth it from half the CUs on
+            // write than they save), or 4 when that fills the CUs with one workgroup each;
+            // worth it from half the CUs on
             const int S = a.K / 64;
             const size_t per_slice = (size_t)a.Mpad * a.n_sub * 16;
             for (int k = 2; k <= 16; k *= 2) {
-                if (S % k != 0 || S / k < 8 || (size_t)k * per_slice > a.part_floats) break;
+                if (S % k != 0 || S / k < 4 || (S / k < 8 && n_big * k > cus) ||
+                    (size_t)k * per_slice > a.part_floats)
+                    break;
                 ks = k;
                 if (n_big * k >= cus) break;
             }
