@@ -9,6 +9,9 @@
 //                (add_inplace, layers.cpp:21-23), silu(gate) * up (layers.cpp:14-19)
 // k_pf_rope_store apply_rope_many of q and k (attention.cpp:48-53) and KVCache::store
 //                (kvcache.cpp:31-36) of every row
+// k_pf_reduce    the slices of a GEMM with K split, added in slice order, + its epilogue;
+//                k_pf_reduce_rope / k_pf_reduce_split do that and then k_pf_rope_store's
+//                or k_pf_split's work on the rows they hold
 // k_pf_pack_kv   the keys and values attention covers, per 32-key tile, as scaled fp16
 //                pairs in MFMA fragment order
 // k_pf_attn      causal GQA attention of the chunk (attn_prefill, attention.cpp:82-111)
