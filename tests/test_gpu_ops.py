@@ -164,7 +164,7 @@ PF_ATTN_CASES = [  # seq, heads, kv heads, head_dim
     (512, 32, 8, 64), (300, 9, 3, 64), (200, 8, 1, 128), (77, 10, 2, 32),
     # enough query blocks for two 16-query subtiles per wave
     (1024, 32, 8, 64), (1024, 48, 8, 128),
-    # few query blocks of 8+ key tiles: 4, 2 and 1 query heads per kv head (4, 2 and 1
+    # few query blocks of 8+ key tiles: 1, 2 and 4 query heads per kv head (4, 2 and 1
     # 16-query subtiles per workgroup), rows not a multiple of 16, head sizes 32 / 128
     (256, 4, 4, 32), (400, 4, 2, 128), (333, 8, 2, 64), (260, 2, 2, 64),
 ]
