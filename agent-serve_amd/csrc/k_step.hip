@@ -5,11 +5,12 @@
 namespace tfk {
 
 using step_detail::attn_lds_floats;
+using step_detail::kXRep;
 
 size_t step_exchange_words(int D, int F, int H, int G, int hd, int n_wg, int split) {
     const size_t n_rep = (size_t)(H / G);
-    return 2 * ((size_t)D + (size_t)D + (size_t)G * (n_rep + 2) * hd + (size_t)H * hd + (size_t)F + (size_t)n_wg +
-                2 * (size_t)n_wg + (size_t)H * split * (hd + 2));
+    return 2 * ((size_t)D + (size_t)kXRep * D + (size_t)G * (n_rep + 2) * hd + (size_t)H * hd + (size_t)F +
+                (size_t)n_wg + 2 * (size_t)n_wg + (size_t)H * split * (hd + 2));
 }
 
 int step_split(int D, int F, int H, int G, int hd, int n_wg) {

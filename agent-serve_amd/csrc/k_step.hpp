@@ -33,6 +33,10 @@ typedef unsigned long long u64;
 constexpr int kT = kStepThreads;   // threads per workgroup
 constexpr int kNW = kT / kWave;    // waves per workgroup
 constexpr int kGD = 8;             // exchange words per thread for d_model-sized inputs (<= 4096)
+// Copies of the wo output's exchange words at most; a build writes RX of them and workgroup w
+// reads copy w % RX, so that the workgroups' polls of that d_model vector spread over RX
+// times the memory lines
+constexpr int kXRep = 8;
 constexpr int kGF = 20;            // and for d_ff-sized ones (<= 10240)
 constexpr int kGW = 2;             // and for per-workgroup words (<= 1024)
 constexpr int kMaxRep = 8;         // query heads per kv head
@@ -754,6 +758,11 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
     // 32-element formats, whose 2048-element rows are 64 steps (a second would be masked
     // out on every lane); ffn_down's n_ff-long rows keep two
     constexpr int UL = Fmt<TL>::E >= 32 ? 1 : UQ, UA = Fmt<TA>::E >= 32 ? 1 : UQ, UO = Fmt<TO>::E >= 32 ? 1 : UQ;
+    // copies of the wo output words: measured faster for the Q8_0 head-size-64 builds
+    // (Llama-3.2-1B shape 0.511 -> 0.501, Qwen2.5-0.5B 0.599 -> 0.589 ms per token), slower for
+    // the others (mixed Q4, Qwen2.5-1.5B: +0.9 %); copies of the ffn_down output words too
+    // gave most of the gain back
+    constexpr int RX = TL == TF_HIP_TYPE_Q8_0 && HDM == 64 ? kXRep : 1;
     constexpr int NWR = 8;  // norm weights per thread: d_model <= 4096
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ __align__(16) unsigned char sc_raw[sizeof(StepConst)];  // StepConst is not trivially constructible
@@ -799,7 +808,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
         c.key0 = args.ctl->key;
         c.XA = 0;
         c.XB = c.XA + 2 * c.D;
-        c.QKV = c.XB + 2 * c.D;
+        c.QKV = c.XB + 2 * RX * c.D;
         c.ATT = c.QKV + 2 * c.G * c.HB;
         c.HH = c.ATT + 2 * c.Hd;
         c.DONE = c.HH + 2 * c.F;
@@ -949,6 +958,9 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             // short spans attend on one workgroup per kv head (attn_head), longer ones split
             const bool split = sc.A && (all || span > sc.a.split_from);
             const int attn_wg0 = split ? sc.attn_wg0 : sc.nwg - sc.G;
+            // copies of the wo output words this token (one when every workgroup splits the
+            // attention: measured slower with copies, Llama-3.2-1B shape after 2,000 tokens)
+            const int rx = all ? 1 : RX;
             STEP_STAMP(l, 0);
             // ---- 1: QKV (attn_norm fused)
             {
@@ -1049,7 +1061,7 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     put(X(sc.HH) + par * sc.F + row, (v / (1.0f + expf(-v))) * up, E(t, l, 4));
                 };
                 auto gu_input = [&]() {
-                    gather<kGD, 1>(X(sc.XB) + par * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl);
+                    gather<kGD, 1>(X(sc.XB) + (par * RX + wg % rx) * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl);
                     stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
                     STEP_STAMP(l, 6);
                 };
@@ -1069,7 +1081,10 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         STEP_STAMP(l, 4);
                     };
                     auto epi = [&](int, int row, float v, float, float) {
-                        put(X(sc.XB) + par * sc.D + row, xr[row] + v, E(t, l, 3));
+                        const float nv = xr[row] + v;
+#pragma unroll
+                        for (int r = 0; r < RX; ++r)
+                            if (r < rx) put(X(sc.XB) + (par * RX + r) * sc.D + row, nv, E(t, l, 3));
                     };
                     if (TA != TL && ly.wo.type == TA)
                         gemv_phase<TA, 1, GEMV_RESID, UA>(1, groups, seg, no_bias, Hd, wid, nw, xs, x16, prep, epi);
