@@ -1342,8 +1342,8 @@ hipError_t launch_attn_hd(const float* q, int64_t ldq, const float* kc, const fl
                        max_seq, att_start, n_keys, recs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // 4 to 8 waves per workgroup, one 16-query subtile per wave (a prompt chunk of 2048
-    // rows gives 128 query blocks per kv head)
+    // 4 to 8 waves per workgroup, one 16-query subtile per wave (a prompt chunk of 4096
+    // rows gives 256 query blocks per kv head)
     const int QG = (4 + n_rep - 1) / n_rep;
     return launch_attn_t<HD, 1>(q, ldq, recs, T, G, n_rep, QG, n, pos0, att_start, out, ldo, st);
 }

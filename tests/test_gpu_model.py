@@ -202,12 +202,12 @@ def test_prefill_paths_agree(pkg, gguf):
 
 
 def test_long_prompt_runs_in_chunks(pkg, gguf):
-    """A prompt longer than one prefill chunk (2048 rows): later chunks attend to the earlier
+    """A prompt longer than one prefill chunk (4096 rows): later chunks attend to the earlier
     ones through the cache, as one attn_prefill over the whole prompt does."""
     info = pkg.synth_preset_info("tiny_q8")
-    prompt = pkg.synth_prompt(info["seed"] + 2, 2100, info["n_vocab"])
-    ids, worst, worst_tap, margin = model_parity(pkg, gguf("tiny_q8"), prompt, 4, 2176, 1)
-    print(f"tiny_q8 2100-token prompt: ids {ids} logits {worst:.2e} taps {worst_tap:.2e}")
+    prompt = pkg.synth_prompt(info["seed"] + 2, 4200, info["n_vocab"])
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf("tiny_q8"), prompt, 4, 4352, 1)
+    print(f"tiny_q8 4200-token prompt: ids {ids} logits {worst:.2e} taps {worst_tap:.2e}")
 
 
 def test_step_and_graph_agree(pkg, gguf):
@@ -309,7 +309,7 @@ GOLDEN =__import__("pathlib").Path(__file__).resolve().parent / "golden"
 
 def test_long_context_workload_vs_reference_fixture(pkg, gguf):
     """The Qwen2.5-1.5B-shape workload at full size: a 4096-token prompt (matrix-core
-    prefill in two chunks), head-major cache of 8192 positions, then 256 greedy tokens,
+    prefill in one chunk), head-major cache of 8192 positions, then 256 greedy tokens,
     against the reference's own run (tests/golden/qwen15b_4096.npz, written by
     make_golden_long.py from the compiled reference; the taps from the oracle run whose
     logits equal the reference's bit for bit). Per step: the device argmax is the
