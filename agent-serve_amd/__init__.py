@@ -26,6 +26,7 @@ KERNEL_CLASSES = ("embed", "qkv_gemv", "attention", "wo_gemv", "gateup_gemv", "d
 _i32p = C.POINTER(C.c_int32)
 _f32p = C.POINTER(C.c_float)
 _f64p = C.POINTER(C.c_double)
+_u32p = C.POINTER(C.c_uint32)
 _u64p = C.POINTER(C.c_uint64)
 
 _hip = None
@@ -61,6 +62,8 @@ def hip_lib() -> C.CDLL:
         "tf_hip_set_split_from": (C.c_int, [vp, C.c_int32]),
         "tf_hip_get_step_config": (C.c_int, [vp, _i32p, C.c_int32]),
         "tf_hip_set_exchange_epoch": (C.c_int, [vp, C.c_uint32]),
+        "tf_hip_test_refuse_cooperative": (C.c_int, [vp, C.c_int32]),
+        "tf_hip_get_hparams": (C.c_int, [vp, C.POINTER(HParams)]),
         "tf_hip_set_prefill_path": (C.c_int, [vp, C.c_int32]),
         "tf_hip_get_prefill_path": (C.c_int, [vp]),
         "tf_hip_get_pos": (C.c_int, [vp]),
@@ -83,14 +86,20 @@ def hip_lib() -> C.CDLL:
         "tf_hip_attn_decode_noalloc": (C.c_int, [C.c_int, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                                  C.c_int32, C.c_int32, vp, vp]),
         "tf_hip_argmax": (C.c_int, [C.c_int, _f32p, C.c_int32, _i32p]),
-        "tf_hip_read_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p]),
-        "tf_hip_copy_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p]),
+        "tf_hip_read_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p, _u32p]),
+        "tf_hip_copy_stream": (C.c_int, [C.c_int, C.c_size_t, C.c_int32, _f64p, _f64p, _u32p]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
         f.restype, f.argtypes = res, args
     _hip = L
     return L
+
+
+class HParams(C.Structure):
+    """tf_hip_hparams (include/tf_hip.h)."""
+    _fields_ = [(n, C.c_int32) for n in ("n_vocab", "n_embd", "n_ff", "n_layer", "n_head", "n_kv_head", "head_dim",
+                                         "max_seq", "kv_layout")] + [("rms_eps", C.c_float)]
 
 
 def host_lib() -> C.CDLL:
@@ -110,6 +119,7 @@ def host_lib() -> C.CDLL:
         "tfh_decode": (C.c_int, [vp, C.c_int32, _f32p, _i32p]),
         "tfh_generate": (C.c_int, [vp, C.c_int32, _i32p]),
         "tfh_reset": (C.c_int, [vp]),
+        "tfh_greedy_host": (C.c_int, [vp, C.c_int32, C.c_int32, _i32p]),
         "tfh_info": (C.c_int, [vp, _i32p]),
         "tfh_weight_bytes": (C.c_uint64, [vp]),
         "tfh_decode_bytes": (C.c_double, [vp, C.c_int32]),
@@ -290,6 +300,13 @@ class HipModel:
         self._check(self._L.tfh_generate(self._h, n, _i(out)))
         return out
 
+    def greedy_host(self, first: int, n: int) -> np.ndarray:
+        """The drop-in caller's greedy loop (tfh_greedy_host): n decodes, each copying the
+        logits to the host and taking their first maximum there; returns the tokens fed."""
+        out = np.zeros(n, np.int32)
+        self._check(self._L.tfh_greedy_host(self._h, int(first), n, _i(out)))
+        return out
+
     def sample(self, temperature: float, top_p: float, r: float) -> int:
         """sample_logits (sampler.cpp:15-52) of the last step's logits on the GPU for the draw r."""
         tok = np.zeros(1, np.int32)
@@ -301,13 +318,11 @@ class HipModel:
     def reset(self):
         self._check(self._L.tfh_reset(self._h))
 
-    PATH_GRAPH, PATH_STEP, PATH_STREAM = 0, 1, 2
+    PATH_GRAPH, PATH_STEP = 0, 1
 
     def set_decode_path(self, path: int):
         """PATH_STEP: one persistent kernel per call where the model allows it (default);
-        PATH_GRAPH: the captured per-layer graph, replayed per token; PATH_STREAM: the
-        persistent kernel with each wave streaming its weights through an LDS ring (Q8_0
-        models, head size <= 128; others take PATH_STEP's choice)."""
+        PATH_GRAPH: the captured per-layer graph, replayed per token."""
         H = hip_lib()
         rc = H.tf_hip_set_decode_path(self._L.tfh_ctx(self._h), int(path))
         if rc != 0:
@@ -344,6 +359,21 @@ class HipModel:
         rc = hip_lib().tf_hip_set_exchange_epoch(self._L.tfh_ctx(self._h), int(epoch) & 0xFFFFFFFF)
         if rc != 0:
             raise RuntimeError(f"tf_hip_set_exchange_epoch failed: {rc}")
+
+    def device_hparams(self) -> dict:
+        """The hyperparameters the device context was created with (tf_hip_get_hparams);
+        kv_layout is the device KV cache's layout (0 seq-major, 1 head-major)."""
+        hp = HParams()
+        rc = hip_lib().tf_hip_get_hparams(self._L.tfh_ctx(self._h), C.byref(hp))
+        if rc != 0:
+            raise RuntimeError(f"tf_hip_get_hparams failed: {rc}")
+        return {n: getattr(hp, n) for n, _ in HParams._fields_}
+
+    def test_refuse_cooperative(self, n: int):
+        """Test hook: the next n step-kernel launches report a cooperative-launch refusal."""
+        rc = hip_lib().tf_hip_test_refuse_cooperative(self._L.tfh_ctx(self._h), int(n))
+        if rc != 0:
+            raise RuntimeError(f"tf_hip_test_refuse_cooperative failed: {rc}")
 
     def decode_path(self) -> int:
         H = hip_lib()
@@ -501,14 +531,28 @@ def argmax(x: np.ndarray, device: int = 0) -> int:
     return int(out.value)
 
 
-def read_stream(nbytes: int, iters: int = 10, device: int = 0):
-    best, med = C.c_double(0), C.c_double(0)
-    _op(hip_lib().tf_hip_read_stream(device, nbytes, iters, C.byref(best), C.byref(med)), "tf_hip_read_stream")
-    return float(best.value), float(med.value)
+def stream_checksum(nbytes: int) -> int:
+    """The sum (mod 2^32) of the streams' fill pattern over nbytes (rounded down to 16):
+    word i holds i * 0x9E3779B1, so n words sum to 0x9E3779B1 * n (n - 1) / 2."""
+    n = nbytes // 16 * 4
+    return (0x9E3779B1 * (n * (n - 1) // 2)) % (1 << 32)
 
 
-def copy_stream(nbytes: int, iters: int = 10, device: int = 0):
-    """Device-to-device copy of nbytes; GB/s counts bytes read plus bytes written."""
-    best, med = C.c_double(0), C.c_double(0)
-    _op(hip_lib().tf_hip_copy_stream(device, nbytes, iters, C.byref(best), C.byref(med)), "tf_hip_copy_stream")
-    return float(best.value), float(med.value)
+def read_stream(nbytes: int, iters: int = 10, device: int = 0, with_checksum: bool = False):
+    """Read-only stream over nbytes of device memory: (best GB/s, median GB/s), plus the
+    integer sum of every word read when with_checksum."""
+    best, med, cs = C.c_double(0), C.c_double(0), C.c_uint32(0)
+    _op(hip_lib().tf_hip_read_stream(device, nbytes, iters, C.byref(best), C.byref(med), C.byref(cs)),
+        "tf_hip_read_stream")
+    r = (float(best.value), float(med.value))
+    return r + (int(cs.value),) if with_checksum else r
+
+
+def copy_stream(nbytes: int, iters: int = 10, device: int = 0, with_checksum: bool = False):
+    """Device-to-device copy of nbytes; GB/s counts bytes read plus bytes written. With
+    with_checksum also the integer sum of the destination after the copies."""
+    best, med, cs = C.c_double(0), C.c_double(0), C.c_uint32(0)
+    _op(hip_lib().tf_hip_copy_stream(device, nbytes, iters, C.byref(best), C.byref(med), C.byref(cs)),
+        "tf_hip_copy_stream")
+    r = (float(best.value), float(med.value))
+    return r + (int(cs.value),) if with_checksum else r

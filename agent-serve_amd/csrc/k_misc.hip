@@ -170,18 +170,29 @@ __global__ __launch_bounds__(kBlock) void k_argmax(const float* x, int n, Ctl* c
 }
 
 // Read-only stream (bench/stream.c:128-141 on the GPU): every byte read once per launch.
-__global__ __launch_bounds__(kBlock) void k_read_stream(const float4* p, size_t n4, double* out) {
-    float acc = 0.0f;
+// The words are summed as integers (mod 2^32), so the total does not depend on the order
+// and says whether every word was read: out[wave] holds each wave's partial sum.
+__global__ __launch_bounds__(kBlock) void k_read_stream(const uint4* p, size_t n4, uint32_t* out) {
+    uint32_t acc = 0;
     for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (size_t)gridDim.x * kBlock) {
-        const float4 v = p[i];
+        const uint4 v = p[i];
         acc += (v.x + v.y) + (v.z + v.w);
     }
-    acc = wave_sum(acc);
+    acc = wave_sum_u32(acc);
     if ((threadIdx.x & 63) == 0) out[(size_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)] = acc;
 }
 
+// The streams' fill pattern: 32-bit word i holds i * kStreamMul (mod 2^32), so the sum of
+// n words is kStreamMul * n (n - 1) / 2 (mod 2^32).
+__global__ __launch_bounds__(kBlock) void k_fill_stream(uint4* p, size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (size_t)gridDim.x * kBlock) {
+        const uint32_t w = (uint32_t)(4 * i);
+        p[i] = make_uint4(w * kStreamMul, (w + 1) * kStreamMul, (w + 2) * kStreamMul, (w + 3) * kStreamMul);
+    }
+}
+
 // Copy stream (bench/stream.c:106-115 on the GPU): every byte read once and written once.
-__global__ __launch_bounds__(kBlock) void k_copy_stream(float4* __restrict__ dst, const float4* __restrict__ src,
+__global__ __launch_bounds__(kBlock) void k_copy_stream(uint4* __restrict__ dst, const uint4* __restrict__ src,
                                                         size_t n4) {
     for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (size_t)gridDim.x * kBlock) dst[i] = src[i];
 }
@@ -260,13 +271,18 @@ hipError_t launch_argmax(const float* x, int n, Ctl* ctl, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_copy_stream(float4* dst, const float4* src, size_t n4, int blocks, hipStream_t st) {
+hipError_t launch_copy_stream(uint4* dst, const uint4* src, size_t n4, int blocks, hipStream_t st) {
     hipLaunchKernelGGL(k_copy_stream, dim3(blocks), dim3(kBlock), 0, st, dst, src, n4);
     return hipGetLastError();
 }
 
-hipError_t launch_read_stream(const float4* p, size_t n4, double* out, int blocks, hipStream_t st) {
+hipError_t launch_read_stream(const uint4* p, size_t n4, uint32_t* out, int blocks, hipStream_t st) {
     hipLaunchKernelGGL(k_read_stream, dim3(blocks), dim3(kBlock), 0, st, p, n4, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_stream(uint4* p, size_t n4, int blocks, hipStream_t st) {
+    hipLaunchKernelGGL(k_fill_stream, dim3(blocks), dim3(kBlock), 0, st, p, n4);
     return hipGetLastError();
 }
 

@@ -45,37 +45,6 @@ constexpr int kSpinLimit = 1 << 20;  // about a second of polling
 constexpr int kErrToken = 1;
 constexpr int kErrTimeout = 2;
 
-// Builds with -DTF_STEP_PROBE record wall-clock stamps (10 ns ticks) of one token's phases
-// per layer and workgroup into StepArgs::dbg: [layer][workgroup][16], layer n_layer = lm_head.
-#ifdef TF_STEP_PROBE
-#define STEP_STAMP(layer, i)                                                                              \
-    do {                                                                                                  \
-        if (threadIdx.x == 0 && sc.a.dbg && t == sc.a.n_tokens / 2)                                       \
-            sc.a.dbg[((size_t)(layer) * sc.nwg + blockIdx.x) * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
-    } while (0)
-// attention sub-phases: ticks since the previous mark, stored (no read: a load would wait
-// for the wave's loads in flight) per workgroup into the lm_head row's slots 12..15 (slot
-// 11 set to 1); the launch's last call of each workgroup remains
-#define ATTN_MARK(i)                                                                                  \
-    do {                                                                                              \
-        if constexpr (std::is_same<A, StepArgs>::value) {                                             \
-            if (threadIdx.x == 0 && a.dbg) {                                                          \
-                const unsigned long long now_ = __builtin_amdgcn_s_memrealtime();                      \
-                unsigned long long* row_ = a.dbg + ((size_t)a.n_layer * gridDim.x + blockIdx.x) * 16; \
-                if ((i) > 0) row_[11 + (i)] = now_ - probe_t_;                                        \
-                if ((i) == 4) row_[11] = 1;                                                           \
-                probe_t_ = now_;                                                                      \
-            }                                                                                         \
-        }                                                                                             \
-    } while (0)
-#else
-#define ATTN_MARK(i) \
-    do {             \
-    } while (0)
-#define STEP_STAMP(layer, i) \
-    do {                     \
-    } while (0)
-#endif
 
 __device__ __forceinline__ void put(u64* p, float v, uint32_t e) {
     __hip_atomic_store(gptr(p), ((u64)e << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -462,10 +431,8 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
         rs[k] = sn[j];
     }
 #ifdef TF_STEP_PROBE
-    unsigned long long probe_t_ = 0;
 #endif
     fetch();
-    ATTN_MARK(0);
     // RoPE (rope_one, with the reference build's contractions)
 #pragma unroll
     for (int k = 0; k < kRope; ++k) {
@@ -489,7 +456,6 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
             __hip_atomic_store(gptr(ly.vc + o + j), vn[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    ATTN_MARK(1);
     const float scale = 1.0f / sqrtf((float)hd);
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // Query head r = wave (n_rep <= kNW): its online-softmax state and its outputs (dims
@@ -518,7 +484,6 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
             if constexpr (NB == 4) load_tile(tile_at(ti + 4), kr, vr);
             if (tn > 0) {
                 bar();
-                if (ti == 0) ATTN_MARK(2);
                 if (head_wave) {
                     // score of position lane in dot_f32's 8-lane order (quant.cpp:198-214).
                     // Unguarded and fully unrolled when hd is the instantiation's head size,
@@ -625,7 +590,6 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
         step(0, kr0, vr0);
         if constexpr (NB == 2) step(1, kr1, vr1);
     }
-    ATTN_MARK(3);
     if (head_wave) {
         const int r = wave;
 #pragma unroll
@@ -648,7 +612,6 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
     // the row's stores are done before this workgroup's next puts
     if (stores_row && wait_row) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     bar();
-    ATTN_MARK(4);
 }
 
 template <int HDM, class A, class Ly, class Fetch, class Bar>
@@ -961,7 +924,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             // copies of the wo output words this token (one when every workgroup splits the
             // attention: measured slower with copies, Llama-3.2-1B shape after 2,000 tokens)
             const int rx = all ? 1 : RX;
-            STEP_STAMP(l, 0);
             // ---- 1: QKV (attn_norm fused)
             {
                 const int D = sc.D;
@@ -1021,7 +983,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                                          X(sc.DONE) + ((l - 1) & 1) * sc.nwg, sc.nwg, E(t, l - 1, 5), a.ctl);
                     }
                     stage(xr, D, true, wr, a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
-                    STEP_STAMP(l, 1);
                 };
                 auto epi = [&](int si, int row, float v, float, float extra) {
                     const int hd = sc.hd, n_rep = sc.n_rep, HB = sc.HB;
@@ -1036,7 +997,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 };
                 gemv_phase<TL, 1, GEMV_STORE, UL>(3, groups, seg, bias, D, wg * kNW + wave, sc.nwg * kNW, xs, x16,
                                                  prep, epi);
-                STEP_STAMP(l, 2);
             }
             // ---- 2: attention (kv head g on workgroup attn_wg0 + g), then 4: gate/up
             // ---- 3: wo + residual (workgroups without an attention head), then 4: gate/up
@@ -1063,7 +1023,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 auto gu_input = [&]() {
                     gather<kGD, 1>(X(sc.XB) + (par * RX + wg % rx) * D, D, E(t, l, 3), xr, nullptr, 0, 0, sc.a.ctl);
                     stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TL>::kNeedSums, red);
-                    STEP_STAMP(l, 6);
                 };
                 // ---- 3: wo + residual, rows dealt over nw waves from wave 0
                 auto wo_phase = [&](int nw) {
@@ -1078,7 +1037,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     auto prep = [&]() {
                         gather<kGD, 1>(X(sc.ATT) + par * Hd, Hd, E(t, l, 2), xs, nullptr, 0, 0, sc.a.ctl);
                         stage(xs, Hd, false, wo_wr, 0.0f, xs, x16, kSums, red);
-                        STEP_STAMP(l, 4);
                     };
                     auto epi = [&](int, int row, float v, float, float) {
                         const float nv = xr[row] + v;
@@ -1121,11 +1079,9 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                             gather<kGD, 1>(X(sc.QKV) + par * G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0,
                                            sc.a.ctl);
                             __syncthreads();
-                            STEP_STAMP(l, 3);
                         }, [] { __syncthreads(); }, all);
                         u64* pw_base = pb + (size_t)(g * A + s) * n_rep * ho;
                         for (int i = tid; i < n_rep * ho; i += kT) put(pw_base + i, part[i], E(t, l, 6));
-                        STEP_STAMP(l, 10);
                     }
                     if (aw < sc.a.H * parts) {
                         const int sz = hd / parts;
@@ -1138,7 +1094,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                             return (size_t)((g * A + s) * n_rep + r) * ho + (k < sz ? d0 + k : hd + k - sz);
                         }, A * w, E(t, l, 6), buf, sc.a.ctl);
                         __syncthreads();
-                        STEP_STAMP(l, 11);
                         for (int k = wave; k < sz; k += kNW) {
                             float m = -INFINITY;
                             for (int s = lane; s < A; s += kWave) m = fmaxf(m, buf[s * w + sz]);
@@ -1153,7 +1108,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                             osum = wave_sum(osum);
                             if (lane == 0) put(X(sc.ATT) + par * sc.Hd + h * hd + d0 + k, osum / lsum, E(t, l, 2));
                         }
-                        STEP_STAMP(l, 12);
                     }
                 }
                 // an attention workgroup that left its K/V row stores in flight waits for them
@@ -1180,11 +1134,9 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                         gather<kGD, 1>(X(sc.QKV) + par * sc.G * HB + g * HB, HB, E(t, l, 1), qkv, nullptr, 0, 0,
                                        sc.a.ctl);
                         __syncthreads();
-                        STEP_STAMP(l, 3);
                     }, [] { __syncthreads(); }, false);
                     const int nh = sc.n_rep * sc.hd;
                     for (int i = tid; i < nh; i += kT) put(X(sc.ATT) + par * sc.Hd + g * nh + i, att_out[i], E(t, l, 2));
-                    STEP_STAMP(l, 10);
                     auto down_then_input = [&]() {
                         row_stores_done();
                         issue_down(ly);
@@ -1199,7 +1151,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     // every load issued before the attention-output polls delays them.)
                     issue_down(ly);
                     wo_phase(sc.nwg * kNW);
-                    STEP_STAMP(l, 5);
                     gemv_phase<TL, kGuR, GEMV_SILU, UL>(1, gu_groups, gu_seg, no_bias, D, wg * kNW + wave, sc.nwg * kNW, xs,
                                                     x16, gu_input, gu_epi);
                 } else {
@@ -1208,7 +1159,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                     auto wo_then_input = [&]() {
                         issue_down(ly);
                         wo_phase(attn_wg0 * kNW);
-                        STEP_STAMP(l, 5);
                         __syncthreads();  // every wave's wo rows are read out of xs before the input is staged
                         gu_input();
                     };
@@ -1216,7 +1166,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                                                     x16, wo_then_input, gu_epi);
                 }
             }
-            STEP_STAMP(l, 7);
             // ---- 5: down + residual
             {
                 const int F = sc.F;
@@ -1226,7 +1175,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 auto prep = [&]() {
                     gather<kGF, 1>(X(sc.HH) + par * F, F, E(t, l, 4), xs, nullptr, 0, 0, sc.a.ctl);
                     stage(xs, F, false, wr, 0.0f, xs, x16, kSums, red);
-                    STEP_STAMP(l, 8);
                 };
                 auto epi = [&](int, int row, float v, float, float) {
                     const float nv = xr[row] + v;
@@ -1271,13 +1219,11 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                                                          xs, x16, prep, epi);
                 }
                 __syncthreads();
-                STEP_STAMP(l, 9);
                 if (tid == 0) put(X(sc.DONE) + par * sc.nwg + wg, 0.0f, E(t, l, 5));
             }
         }
         // ---- output_norm + lm_head + greedy argmax
         if (sc.a.lm_every || last) {
-            STEP_STAMP(sc.L, 0);
             const int D = sc.D;
             float wr[NWR];
             load_norm(sc.a.out_norm, D, wr);
@@ -1288,7 +1234,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
                 gather<kGD, kGW>(X(sc.XA) + (Lm & 1) * D, D, E(t, Lm, 5), xr, X(sc.DONE) + (Lm & 1) * sc.nwg, sc.nwg,
                                  E(t, Lm, 5), sc.a.ctl);
                 stage(xr, D, true, wr, sc.a.eps, xs, x16, Fmt<TO>::kNeedSums, red);
-                STEP_STAMP(sc.L, 1);
                 if (last && sc.a.taps && wg == 0)
                     for (int j = tid; j < D; j += kT) *gptr(sc.a.taps + (size_t)sc.L * D + j) = xs[j];
             };
@@ -1303,7 +1248,6 @@ __global__ __launch_bounds__(kT, 1) void k_step(const StepArgs args) {
             best = wave_max_u64(best);
             if (lane == 0) wbest[wave] = best;
             __syncthreads();
-            STEP_STAMP(sc.L, 2);
             if (tid == 0) {
                 u64 b = wbest[0];
                 for (int i = 1; i < kNW; ++i) b = wbest[i] > b ? wbest[i] : b;

@@ -15,7 +15,6 @@
 #include <vector>
 
 #include "formats.hpp"
-#include "k_stream.hpp"
 #include "tf_internal.hpp"
 
 using namespace tfk;
@@ -83,15 +82,8 @@ struct tf_hip_ctx {
     int split_all_from = -1;                  // tf_hip_set_split_all_from (< 0: step_split_all_from)
     int split_from = kSplitFromDefault;       // tf_hip_set_split_from: spans up to this attend unsplit
     StepLayer* d_layers = nullptr;
-    // streaming step kernel (k_stream.hpp)
-    int stream_state = -1;            // -1 undecided, 0 not used, 1 ready
-    uint8_t* sbuf = nullptr;          // the weights as per-(workgroup, wave) streams
-    uint64_t* d_sbase = nullptr;
-    uint8_t* d_ssteps = nullptr;
-    uint32_t *d_sfirst = nullptr, *d_snl = nullptr, *d_snt = nullptr;
-    SLayer* d_slayers = nullptr;
-    int s_steps_max = 0, s_rs = 0;
-    int s_depth = 2, s_depth_lm = 6;  // slots in flight per wave of the streaming kernel
+    bool coop_refused = false;  // the GPU refused the step kernel's cooperative launch: graph path from then on
+    int refuse_coop = 0;        // test hook: this many more step launches report a refusal
     unsigned long long* ex = nullptr;
     size_t ex_words = 0;
     uint32_t epoch = 0;               // exchange epochs consumed (mirrors ctl->epoch)
@@ -345,10 +337,11 @@ hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof, int pos = 0, int att_start = 
                 a.x = c->x;
                 a.norm_w = V(TF_HIP_LAYER_ATTN_NORM);
                 a.eps = hp.rms_eps;
-                double bytes = 0;
+                // the first launch also reads the norm weights; each segment its bias
+                double bytes = i == 0 ? 4.0 * D : 0.0;
                 while (i < 3 && ms[i]->type == a.type) {
                     add_seg(a, *ms[i], ys[i], bs[i], nullptr, R);
-                    bytes += (double)ms[i]->gguf_bytes;
+                    bytes += (double)ms[i]->gguf_bytes + (bs[i] ? 4.0 * (double)ms[i]->N : 0.0);
                     ++i;
                 }
                 L.run(1, bytes, [&] { return launch_gemv(a, R, c->st); });
@@ -406,7 +399,7 @@ hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof, int pos = 0, int att_start = 
                 a.eps = hp.rms_eps;
                 add_seg(a, wg, c->h, nullptr, nullptr, R);
                 a.seg[0].b = wu;
-                L.run(4, (double)(wg.gguf_bytes + wu.gguf_bytes), [&] { return launch_gemv(a, R, c->st); });
+                L.run(4, (double)(wg.gguf_bytes + wu.gguf_bytes) + 4.0 * D, [&] { return launch_gemv(a, R, c->st); });
             } else {
                 L.err = hipErrorInvalidValue;  // rejected at upload; unreachable
             }
@@ -425,7 +418,7 @@ hipError_t enqueue_step(tf_hip_ctx* c, Prof* prof, int pos = 0, int att_start = 
     }
     {
         const DevMat& wout = output_mat(c);
-        L.run(6, (double)wout.gguf_bytes, [&] { return launch_lm_head(c); });
+        L.run(6, (double)wout.gguf_bytes + 4.0 * D, [&] { return launch_lm_head(c); });
     }
     return L.err;
 }
@@ -456,7 +449,7 @@ int ensure_graph(tf_hip_ctx* c) {
 // attention over workgroups (step_split, step_split_all). Returns 1 (step kernel), 0
 // (graph) or < 0.
 int ensure_step(tf_hip_ctx* c) {
-    if (c->path_opt == TF_HIP_PATH_GRAPH) return 0;
+    if (c->path_opt == TF_HIP_PATH_GRAPH || c->coop_refused) return 0;
     if (c->step_state >= 0) return c->step_state;
     int rc = check_ready(c);
     if (rc) return rc;
@@ -542,7 +535,15 @@ int epoch_guard(tf_hip_ctx* c, int n) {
     return 0;
 }
 
-// n tokens through the persistent step kernel, from position c->pos.
+// run_step's result when the GPU refused the cooperative launch (another process holds the
+// cooperative-launch resource, or the grid no longer fits): nothing ran.
+constexpr int kStepRefused = 1;
+bool coop_refusal(hipError_t e) {
+    return e == hipErrorCooperativeLaunchTooLarge || e == hipErrorLaunchOutOfResources || e == hipErrorNotSupported;
+}
+
+// n tokens through the persistent step kernel, from position c->pos. Returns 0,
+// kStepRefused (the context then takes the graph path from now on) or < 0.
 int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
     const tf_hip_hparams& p = c->hp;
     StepArgs a{};
@@ -578,261 +579,22 @@ int run_step(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
                                               : step_split_all_from(p.n_head, p.n_kv_head, p.head_dim, c->step_split);
     int rc = epoch_guard(c, n);
     if (rc) return rc;
-#ifdef TF_STEP_PROBE
-    const size_t n_dbg = (size_t)(p.n_layer + 1) * c->n_wg * 16;
-    if (n >= 8) {
-        (void)hipMalloc((void**)&a.dbg, n_dbg * 8);
-        (void)hipMemsetAsync(a.dbg, 0, n_dbg * 8, c->st);
+    hipError_t e;
+    if (c->refuse_coop > 0) {
+        --c->refuse_coop;
+        e = hipErrorCooperativeLaunchTooLarge;
+    } else {
+        e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);
     }
-#endif
-    const hipError_t e = launch_step(a, c->step_tl, c->step_to, c->n_wg, c->st);
+    if (coop_refusal(e)) {
+        (void)hipGetLastError();
+        c->coop_refused = true;
+        c->step_state = 0;
+        return kStepRefused;
+    }
     if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("step kernel launch: ") + hipGetErrorString(e));
-#ifdef TF_STEP_PROBE
-    if (a.dbg) {
-        // per stamp: median and max over workgroups of (stamp - the layer's earliest start),
-        // means over layers 1 .. L-2, in microseconds
-        std::vector<unsigned long long> h(n_dbg);
-        (void)hipMemcpyAsync(h.data(), a.dbg, n_dbg * 8, hipMemcpyDeviceToHost, c->st);
-        (void)hipStreamSynchronize(c->st);
-        (void)hipFree(a.dbg);
-        const int L = p.n_layer, W = c->n_wg;
-        double med[16] = {0}, mx[16] = {0}, cnt[16] = {0}, layer_us = 0;
-        for (int l = 1; l + 1 < L; ++l) {
-            unsigned long long t0 = ~0ull, t1 = ~0ull;
-            for (int w = 0; w < W; ++w) {
-                const unsigned long long s = h[((size_t)l * W + w) * 16];
-                const unsigned long long s1 = h[((size_t)(l + 1) * W + w) * 16];
-                if (s) t0 = std::min(t0, s);
-                if (s1) t1 = std::min(t1, s1);
-            }
-            if (t0 == ~0ull || t1 == ~0ull) continue;
-            layer_us += (double)(t1 - t0) / 100.0;
-            for (int i = 0; i < 16; ++i) {
-                std::vector<double> v;
-                for (int w = 0; w < W; ++w) {
-                    const unsigned long long s = h[((size_t)l * W + w) * 16 + i];
-                    if (s) v.push_back((double)(s - t0) / 100.0);
-                }
-                if (v.empty()) continue;
-                std::sort(v.begin(), v.end());
-                med[i] += v[v.size() / 2];
-                mx[i] += v.back();
-                cnt[i] += 1;
-            }
-        }
-        std::fprintf(stderr, "step probe n=%d pos=%d: layer %.2f us (start to next start, mean of layers 1..%d)\n", n,
-                     a.att_start, layer_us / std::max(1, L - 2), L - 2);
-        const char* nm[13] = {"start", "qkv in", "qkv done", "attn qkv in", "wo in", "wo done",
-                              "gu in", "gu done", "down in", "down done", "attn out put", "merge in", "merge put"};
-        for (int i = 0; i < 13; ++i)
-            if (cnt[i] > 0)
-                std::fprintf(stderr, "  %-16s med %6.2f max %6.2f\n", nm[i], med[i] / cnt[i], mx[i] / cnt[i]);
-        // per phase end (qkv, wo, gate/up, down): the mean stamp per eighth of the grid and the
-        // last workgroups (means over layers, relative to the layer's earliest start)
-        {
-            const int ends[4] = {2, 5, 7, 9};
-            const char* en[4] = {"qkv done", "wo done", "gu done", "down done"};
-            for (int k = 0; k < 4; ++k) {
-                std::vector<double> v(W, 0.0);
-                std::vector<int> n_l(W, 0);
-                for (int l = 1; l + 1 < L; ++l) {
-                    unsigned long long t0 = ~0ull;
-                    for (int w = 0; w < W; ++w) {
-                        const unsigned long long st = h[((size_t)l * W + w) * 16];
-                        if (st) t0 = std::min(t0, st);
-                    }
-                    if (t0 == ~0ull) continue;
-                    for (int w = 0; w < W; ++w) {
-                        const unsigned long long q = h[((size_t)l * W + w) * 16 + ends[k]];
-                        if (q) {
-                            v[w] += (double)(q - t0) / 100.0;
-                            ++n_l[w];
-                        }
-                    }
-                }
-                std::fprintf(stderr, "  %-10s by eighth:", en[k]);
-                for (int e = 0; e < 8; ++e) {
-                    double sum = 0;
-                    int cnt_w = 0;
-                    for (int w = e * W / 8; w < (e + 1) * W / 8; ++w)
-                        if (n_l[w]) {
-                            sum += v[w] / n_l[w];
-                            ++cnt_w;
-                        }
-                    std::fprintf(stderr, " %6.2f", cnt_w ? sum / cnt_w : 0.0);
-                }
-                int last = -1;
-                for (int w = 0; w < W; ++w)
-                    if (n_l[w] && (last < 0 || v[w] / n_l[w] > v[last] / n_l[last])) last = w;
-                if (last >= 0) std::fprintf(stderr, "  last wg %d %.2f", last, v[last] / n_l[last]);
-                std::fprintf(stderr, "\n");
-            }
-        }
-        unsigned long long l0 = ~0ull, l1 = 0, l2 = 0;
-        for (int w = 0; w < W; ++w) {
-            const unsigned long long* q = &h[((size_t)L * W + w) * 16];
-            if (q[0]) l0 = std::min(l0, q[0]);
-            l1 = std::max(l1, q[1]);
-            l2 = std::max(l2, q[2]);
-        }
-        if (l0 != ~0ull)
-            std::fprintf(stderr, "  lm_head: in by %.2f, done by %.2f us\n", (double)(l1 - l0) / 100.0,
-                         (double)(l2 - l0) / 100.0);
-        double acc[4] = {0, 0, 0, 0}, calls = 0;
-        for (int w = 0; w < W; ++w) {
-            const unsigned long long* q = &h[((size_t)L * W + w) * 16];
-            calls += (double)q[11];
-            for (int i = 0; i < 4; ++i) acc[i] += (double)q[12 + i];
-        }
-        if (calls > 0)
-            std::fprintf(stderr,
-                         "  attention per call (%.0f calls): rope+row %.2f, first tile staged %.2f, tiles %.2f, output %.2f us\n",
-                         calls, acc[0] / calls / 100.0, acc[1] / calls / 100.0, acc[2] / calls / 100.0,
-                         acc[3] / calls / 100.0);
-    }
-#endif
     c->epoch += (uint32_t)((uint64_t)n * (6ull * (uint64_t)p.n_layer + 8ull));
     return 0;
-}
-
-// Decides once, after the step kernel's set-up, whether the streaming kernel runs this
-// model (TF_HIP_PATH_STREAM requested, Q8_0 layers and lm_head, its LDS holds a ring of at
-// least 4 slots per wave, and split attention available where the cache needs it), and
-// repacks the weights into its streams. Returns 1 (streaming kernel), 0 or < 0.
-int ensure_stream(tf_hip_ctx* c) {
-    if (c->path_opt != TF_HIP_PATH_STREAM) return 0;
-    if (c->stream_state >= 0) return c->stream_state;
-    const int s = ensure_step(c);
-    if (s <= 0) return s;
-    c->stream_state = 0;
-    const tf_hip_hparams& p = c->hp;
-    const int V = (int)output_mat(c).N;
-    if (!stream_supported(c->step_tl, c->step_to, p.head_dim, p.n_head / p.n_kv_head, p.n_embd, p.n_ff, c->H))
-        return 0;
-    if (p.max_seq > 512 && !c->step_split_all) return 0;
-    std::vector<uint64_t> sbase;
-    std::vector<uint32_t> sfirst, snl, snt;
-    uint64_t bytes = 0;
-    uint32_t steps_total = 0;
-    int steps_max = 0;
-    stream_plan(p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, V, c->n_wg, sbase, sfirst, snl, snt,
-                &bytes, &steps_total, &steps_max);
-    const int rs = stream_ring_slots(p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, V, c->n_wg,
-                                     steps_max);
-    if (rs < 4) return 0;
-    std::vector<SLayer> tab((size_t)p.n_layer);
-    for (int l = 0; l < p.n_layer; ++l) {
-        auto Vv = [&](int k) { return vec(c, TF_HIP_SLOT_LAYER(l, k)); };
-        SLayer& t = tab[(size_t)l];
-        t.attn_norm = Vv(TF_HIP_LAYER_ATTN_NORM);
-        t.ffn_norm = Vv(TF_HIP_LAYER_FFN_NORM);
-        t.bq = Vv(TF_HIP_LAYER_BQ);
-        t.bk = Vv(TF_HIP_LAYER_BK);
-        t.bv = Vv(TF_HIP_LAYER_BV);
-        t.kc = c->kc + (size_t)l * c->kv_layer;
-        t.vc = c->vc + (size_t)l * c->kv_layer;
-    }
-    const size_t n = sbase.size();
-    int rc = 0;
-    if ((rc = dalloc(c, &c->sbuf, bytes)) || (rc = dalloc(c, &c->d_sbase, n * 8)) ||
-        (rc = dalloc(c, &c->d_ssteps, steps_total)) || (rc = dalloc(c, &c->d_sfirst, n * 4)) ||
-        (rc = dalloc(c, &c->d_snl, n * 4)) || (rc = dalloc(c, &c->d_snt, n * 4)) ||
-        (rc = dalloc(c, &c->d_slayers, tab.size() * sizeof(SLayer))))
-        return rc;
-    HIPCHK(c, hipMemcpy(c->d_sbase, sbase.data(), n * 8, hipMemcpyHostToDevice));
-    HIPCHK(c, hipMemcpy(c->d_sfirst, sfirst.data(), n * 4, hipMemcpyHostToDevice));
-    HIPCHK(c, hipMemcpy(c->d_snl, snl.data(), n * 4, hipMemcpyHostToDevice));
-    HIPCHK(c, hipMemcpy(c->d_snt, snt.data(), n * 4, hipMemcpyHostToDevice));
-    HIPCHK(c, hipMemcpy(c->d_slayers, tab.data(), tab.size() * sizeof(SLayer), hipMemcpyHostToDevice));
-    HIPCHK(c, launch_stream_pack(c->d_layers, output_mat(c), p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head,
-                                 p.head_dim, V, c->n_wg, c->sbuf, c->d_sbase, c->d_ssteps, c->d_sfirst, c->st));
-    HIPCHK(c, hipStreamSynchronize(c->st));
-    c->s_steps_max = steps_max;
-    c->s_rs = rs;
-    if (const char* e = std::getenv("TF_HIP_STREAM_DEPTH")) c->s_depth = std::max(1, std::min(8, std::atoi(e)));
-    if (const char* e = std::getenv("TF_HIP_STREAM_DEPTH_LM")) c->s_depth_lm = std::max(1, std::min(8, std::atoi(e)));
-    c->stream_state = 1;
-    return 1;
-}
-
-// n tokens through the streaming kernel, from position c->pos.
-int run_stream(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
-    const tf_hip_hparams& p = c->hp;
-    StreamArgs a{};
-    a.layers = c->d_slayers;
-    a.stream = c->sbuf;
-    a.sbase = c->d_sbase;
-    a.ssteps = c->d_ssteps;
-    a.sfirst = c->d_sfirst;
-    a.snl = c->d_snl;
-    a.snt = c->d_snt;
-    a.embd = mat(c, TF_HIP_SLOT_TOKEN_EMBD);
-    a.out_norm = vec(c, TF_HIP_SLOT_OUTPUT_NORM);
-    a.rope_cos = c->rope_cos;
-    a.rope_sin = c->rope_sin;
-    a.ex = c->ex;
-    a.ctl = c->ctl;
-    a.hist = c->hist;
-    a.logits = c->logits;
-    a.taps = c->taps;
-    a.n_layer = p.n_layer;
-    a.D = p.n_embd;
-    a.F = p.n_ff;
-    a.H = p.n_head;
-    a.G = p.n_kv_head;
-    a.hd = p.head_dim;
-    a.V = (int)output_mat(c).N;
-    a.max_seq = p.max_seq;
-    a.layout = p.kv_layout;
-    a.eps = p.rms_eps;
-    a.n_tokens = n;
-    a.greedy = greedy;
-    a.lm_every = lm_every;
-    a.att_start = att_start;
-    a.split_all = c->step_split_all;
-    a.split_from = c->split_from;
-    a.ring_slots = c->s_rs;
-    a.steps_max = c->s_steps_max;
-    a.depth = c->s_depth;
-    a.depth_lm = c->s_depth_lm;
-    int rc = epoch_guard(c, n);
-    if (rc) return rc;
-#ifdef TF_STREAM_PROBE
-    static unsigned long long* dbg = nullptr;
-    if (!dbg) (void)hipMalloc(&dbg, (size_t)c->n_wg * 64 * 8);
-    (void)hipMemsetAsync(dbg, 0, (size_t)c->n_wg * 64 * 8, c->st);
-    a.dbg = dbg;
-#endif
-    const hipError_t e = launch_stream(a, c->n_wg, c->st);
-    if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("stream kernel launch: ") + hipGetErrorString(e));
-#ifdef TF_STREAM_PROBE
-    {
-        std::vector<unsigned long long> h((size_t)c->n_wg * 64);
-        (void)hipMemcpyAsync(h.data(), dbg, h.size() * 8, hipMemcpyDeviceToHost, c->st);
-        (void)hipStreamSynchronize(c->st);
-        for (int wv = 0; wv < 8; ++wv) {
-            double q[8] = {0};
-            for (int w = 0; w < c->n_wg; ++w)
-                for (int i = 0; i < 8; ++i) q[i] += (double)h[(size_t)w * 64 + wv * 8 + i] / c->n_wg / 100.0 / n;
-            std::fprintf(stderr, "probe n=%d wave %d us/token: total %.1f feed-wait %.1f gather %.1f units %.1f attn %.1f lm %.1f slots %.0f\n",
-                         n, wv, q[5], q[0], q[1], q[2], q[3], q[4], q[6] * 100.0);
-        }
-    }
-#endif
-    c->epoch += (uint32_t)((uint64_t)n * (6ull * (uint64_t)p.n_layer + 8ull));
-    return 0;
-}
-
-// The persistent kernel of this context: 2 streaming, 1 step kernel, 0 none (graph path), < 0 error.
-int ensure_persistent(tf_hip_ctx* c) {
-    const int s = ensure_stream(c);
-    if (s < 0) return s;
-    if (s == 1) return 2;
-    return ensure_step(c);
-}
-
-int run_persistent(tf_hip_ctx* c, int kind, int n, int greedy, int lm_every, int att_start) {
-    return kind == 2 ? run_stream(c, n, greedy, lm_every, att_start) : run_step(c, n, greedy, lm_every, att_start);
 }
 
 // Writes att_start and mode of the device control block.
@@ -841,6 +603,21 @@ int set_ctl(tf_hip_ctx* c, int att_start, int mode) {
     c->ctl_host->mode = mode;
     HIPCHK(c, hipMemcpyAsync((char*)c->ctl + offsetof(Ctl, att_start), (char*)c->ctl_host + offsetof(Ctl, att_start),
                              2 * sizeof(int32_t), hipMemcpyHostToDevice, c->st));
+    return 0;
+}
+
+// n tokens on the context's decode path, from position c->pos: the step kernel when
+// *use_step, else n replays of the captured graph. A refused cooperative launch switches
+// the context to the graph path and runs the tokens there (*use_step then reads 0).
+int run_tokens(tf_hip_ctx* c, int* use_step, int n, int greedy, int lm_every, int att_start) {
+    if (*use_step) {
+        const int rc = run_step(c, n, greedy, lm_every, att_start);
+        if (rc != kStepRefused) return rc;
+        *use_step = 0;
+        const int g = ensure_graph(c);
+        if (g) return g;
+    }
+    for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
     return 0;
 }
 
@@ -1059,13 +836,12 @@ int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out) {
         const long v = std::strtol(sf, &end, 10);
         if (end != sf && *end == 0 && v >= 0 && v <= kSplitFromMax) c->split_from = (int)v;
     }
-    // TF_HIP_DECODE_PATH=step|graph|stream: the initial decode path, for callers that do not
+    // TF_HIP_DECODE_PATH=step|graph: the initial decode path, for callers that do not
     // call tf_hip_set_decode_path (other values are ignored)
     if (const char* dp = std::getenv("TF_HIP_DECODE_PATH")) {
         const std::string v(dp);
         if (v == "step") c->path_opt = TF_HIP_PATH_STEP;
         if (v == "graph") c->path_opt = TF_HIP_PATH_GRAPH;
-        if (v == "stream") c->path_opt = TF_HIP_PATH_STREAM;
     }
     c->hp = p;
     c->H = p.n_head * p.head_dim;
@@ -1107,6 +883,10 @@ int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out) {
         hipMemset(c->taps, 0, (size_t)(p.n_layer + 1) * D * 4) != hipSuccess)
         return bail(TF_HIP_EDEVICE);
     if (hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess) return bail(TF_HIP_EDEVICE);
+    if (const char* lg = std::getenv("TF_HIP_LOG"); lg && *lg && std::strcmp(lg, "0") != 0)
+        std::fprintf(stderr, "tf_hip: device %d kv=%s max_seq=%d layers=%d dim=%d heads=%d/%d\n", device,
+                     p.kv_layout == TF_HIP_KV_HEAD_MAJOR ? "head" : "seq", p.max_seq, p.n_layer, p.n_embd,
+                     p.n_head, p.n_kv_head);
     *out = c;
     return 0;
 }
@@ -1161,7 +941,6 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
             if (rc) return rc;
             c->vecs[(size_t)slot] = d;
             c->step_state = -1;
-            c->stream_state = -1;
             c->pf_state = -1;
         }
         c->vec_len[(size_t)slot] = want;
@@ -1210,7 +989,6 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
     c->allocs.insert(c->allocs.end(), owned.begin(), owned.end());
     c->mats[(size_t)slot] = m;  // a re-upload leaves the old streams allocated until destroy
     c->step_state = -1;         // the step kernel's layer table is rebuilt
-    c->stream_state = -1;       // and the streams repacked
     c->pf_state = -1;
     return 0;
 }
@@ -1250,18 +1028,14 @@ int tf_hip_decode(tf_hip_ctx* c, int32_t token, float* logits, int32_t* argmax) 
     if (c->pos >= c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
     if (token < 0 || token >= mat(c, TF_HIP_SLOT_TOKEN_EMBD).N)
         return fail(c, TF_HIP_ERANGE, "token " + std::to_string(token) + " out of range");
-    const int use_step = ensure_persistent(c);
+    int use_step = ensure_step(c);
     if (use_step < 0) return use_step;
     int rc = use_step ? 0 : ensure_graph(c);
     if (rc) return rc;
     c->tok_host[0] = token;
     HIPCHK(c, hipMemcpyAsync(c->hist + c->pos, c->tok_host, 4, hipMemcpyHostToDevice, c->st));
     if ((rc = set_ctl(c, 0, 0))) return rc;
-    if (use_step) {
-        if ((rc = run_persistent(c, use_step, 1, 0, 1, 0))) return rc;
-    } else {
-        HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
-    }
+    if ((rc = run_tokens(c, &use_step, 1, 0, 1, 0))) return rc;
     c->pos += 1;
     rc = finish_step_outputs(c, logits, argmax);
     if (rc) return rc;
@@ -1280,7 +1054,7 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
             return fail(c, TF_HIP_ERANGE, "token " + std::to_string(tokens[i]) + " out of range");
     const int use_pf = n >= 2 ? ensure_pf(c) : 0;
     if (use_pf < 0) return use_pf;
-    const int use_step = use_pf ? 0 : ensure_persistent(c);
+    int use_step = use_pf ? 0 : ensure_step(c);
     if (use_step < 0) return use_step;
     int rc = (use_pf || use_step) ? 0 : ensure_graph(c);
     if (rc) return rc;
@@ -1290,10 +1064,8 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
     HIPCHK(c, hipEventRecord(c->ev0, c->st));
     if (use_pf) {
         if ((rc = prefill_mfma(c, n))) return rc;
-    } else if (use_step) {
-        if ((rc = run_persistent(c, use_step, n, 0, 0, c->pos))) return rc;
-    } else {
-        for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    } else if ((rc = run_tokens(c, &use_step, n, 0, 0, c->pos))) {
+        return rc;
     }
     HIPCHK(c, hipEventRecord(c->ev1, c->st));
     c->pos += n;
@@ -1301,7 +1073,7 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
     if (rc) return rc;
     HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
     c->last_steps = use_pf ? 1 : (use_step ? 1 : n);
-    c->last_name = use_pf ? "prefill_mfma" : (use_step == 2 ? "k_stream" : (use_step ? "k_step" : "decode_graph"));
+    c->last_name = use_pf ? "prefill_mfma" : (use_step ? "k_step" : "decode_graph");
     c->have_logits = true;
     return 0;
 }
@@ -1312,18 +1084,14 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     HIPCHK(c, hipSetDevice(c->device));
     if (!c->have_logits) return fail(c, TF_HIP_ESTATE, "generate needs a prior prefill or decode");
     if (n > c->hp.max_seq - c->pos) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
-    const int use_step = ensure_persistent(c);
+    int use_step = ensure_step(c);
     if (use_step < 0) return use_step;
     int rc = use_step ? 0 : ensure_graph(c);
     if (rc) return rc;
     const int pos0 = c->pos;
     if ((rc = set_ctl(c, 0, 1))) return rc;
     HIPCHK(c, hipEventRecord(c->ev0, c->st));
-    if (use_step) {
-        if ((rc = run_persistent(c, use_step, n, 1, 1, 0))) return rc;
-    } else {
-        for (int i = 0; i < n; ++i) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
-    }
+    if ((rc = run_tokens(c, &use_step, n, 1, 1, 0))) return rc;
     HIPCHK(c, hipEventRecord(c->ev1, c->st));
     HIPCHK(c, hipMemcpyAsync(c->tok_host, c->hist + pos0, (size_t)n * 4, hipMemcpyDeviceToHost, c->st));
     c->pos += n;
@@ -1332,16 +1100,27 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     std::memcpy(out, c->tok_host, (size_t)n * 4);
     HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
     c->last_steps = use_step ? 1 : n;
-    c->last_name = use_step == 2 ? "k_stream" : (use_step == 1 ? "k_step" : "decode_graph");
+    c->last_name = use_step ? "k_step" : "decode_graph";
     return 0;
 }
 
 int tf_hip_set_decode_path(tf_hip_ctx* c, int32_t path) {
-    if (!c || (path != TF_HIP_PATH_GRAPH && path != TF_HIP_PATH_STEP && path != TF_HIP_PATH_STREAM))
+    if (!c || (path != TF_HIP_PATH_GRAPH && path != TF_HIP_PATH_STEP))
         return TF_HIP_EINVAL;
     c->path_opt = path;
     if (path != TF_HIP_PATH_GRAPH && c->step_state == 0) c->step_state = -1;  // decide again
-    if (path == TF_HIP_PATH_STREAM && c->stream_state == 0) c->stream_state = -1;
+    return 0;
+}
+
+int tf_hip_get_hparams(const tf_hip_ctx* c, tf_hip_hparams* out) {
+    if (!c || !out) return TF_HIP_EINVAL;
+    *out = c->hp;
+    return 0;
+}
+
+int tf_hip_test_refuse_cooperative(tf_hip_ctx* c, int32_t n) {
+    if (!c || n < 0) return TF_HIP_EINVAL;
+    c->refuse_coop = n;
     return 0;
 }
 
@@ -1407,8 +1186,8 @@ int tf_hip_get_prefill_path(tf_hip_ctx* c) {
 int tf_hip_get_decode_path(tf_hip_ctx* c) {
     if (!c) return TF_HIP_EINVAL;
     HIPCHK(c, hipSetDevice(c->device));
-    const int s = ensure_persistent(c);
-    return s < 0 ? s : (s == 2 ? TF_HIP_PATH_STREAM : (s ? TF_HIP_PATH_STEP : TF_HIP_PATH_GRAPH));
+    const int s = ensure_step(c);
+    return s < 0 ? s : (s ? TF_HIP_PATH_STEP : TF_HIP_PATH_GRAPH);
 }
 
 int tf_hip_get_layer_act(tf_hip_ctx* c, int32_t layer, float* out) {
@@ -1420,7 +1199,8 @@ int tf_hip_get_layer_act(tf_hip_ctx* c, int32_t layer, float* out) {
 }
 
 int tf_hip_read_kv(tf_hip_ctx* c, int32_t layer, int32_t which, int32_t pos0, int32_t n, float* out) {
-    if (!c || !out || layer < 0 || layer >= c->hp.n_layer || pos0 < 0 || n < 0 || pos0 + n > c->hp.max_seq)
+    if (!c || !out || layer < 0 || layer >= c->hp.n_layer || pos0 < 0 || n < 0 || pos0 > c->hp.max_seq ||
+        n > c->hp.max_seq - pos0)
         return TF_HIP_EINVAL;
     HIPCHK(c, hipSetDevice(c->device));
     HIPCHK(c, hipStreamSynchronize(c->st));
@@ -1758,11 +1538,17 @@ std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxDevices] = {};
 
 // The device address of `scratch` on `device` (the current device), looked up once per
-// device. In host code the array's name is only a stand-in; kernels get this address.
-int scratch_on(int device, float** out) {
+// device. In host code the array's name is only a stand-in; kernels get this address. The
+// lookup may load the library's code objects, which a stream under graph capture must not
+// see: while `st` is capturing, a device whose address is not known yet gets TF_HIP_ESTATE
+// before anything is enqueued (its first call has to be made outside capture).
+int scratch_on(int device, hipStream_t st, float** out) {
     if (device < 0 || device >= kMaxDevices) return TF_HIP_EINVAL;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[device]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess) return TF_HIP_EDEVICE;
+        if (cs != hipStreamCaptureStatusNone) return TF_HIP_ESTATE;
         void* p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return TF_HIP_EDEVICE;
         g_scratch_ptr[device] = (float*)p;
@@ -1787,7 +1573,7 @@ int tf_hip_attn_decode_noalloc(int device, const float* q, const float* k_cache,
     if (S > 1 && need > kScratchFloats) return TF_HIP_ESCRATCH;
     if (hipSetDevice(device) != hipSuccess) return TF_HIP_EDEVICE;
     float* ptr = nullptr;
-    int rc = scratch_on(device, &ptr);
+    int rc = scratch_on(device, (hipStream_t)stream, &ptr);
     if (rc) return rc;
     AttnArgs a{};
     a.q = q;
@@ -1893,18 +1679,29 @@ int tf_hip_argmax(int device, const float* x, int32_t n, int32_t* out) {
     return 0;
 }
 
-int tf_hip_read_stream(int device, size_t nbytes, int32_t iters, double* best, double* median) {
+// The sum (mod 2^32) of the wave partials k_read_stream wrote to sink.
+static uint32_t sink_total(const uint32_t* d_sink, size_t n, hipStream_t st, hipError_t* err) {
+    std::vector<uint32_t> h(n);
+    *err = hipMemcpyAsync(h.data(), d_sink, n * 4, hipMemcpyDeviceToHost, st);
+    if (*err == hipSuccess) *err = hipStreamSynchronize(st);
+    uint32_t t = 0;
+    for (uint32_t v : h) t += v;
+    return t;
+}
+
+int tf_hip_read_stream(int device, size_t nbytes, int32_t iters, double* best, double* median, uint32_t* checksum) {
     if (nbytes < 16 || iters <= 0 || !best || !median) return TF_HIP_EINVAL;
     OpScope s;
     int rc = op_begin(device, s);
     if (rc) return rc;
     const size_t n4 = nbytes / 16;
-    float4* p;
-    double* sink;
+    uint4* p;
+    uint32_t* sink;
     const int blocks = 8 * device_cu_count();
+    const size_t n_sink = (size_t)blocks * kWavesPerBlock;
     OPCHK(s.alloc(&p, n4 * 16));
-    OPCHK(s.alloc(&sink, (size_t)blocks * kWavesPerBlock * sizeof(double)));
-    OPCHK(hipMemset(p, 0, n4 * 16));
+    OPCHK(s.alloc(&sink, n_sink * sizeof(uint32_t)));
+    OPCHK(launch_fill_stream(p, n4, blocks, s.st));
     hipEvent_t e0, e1;
     OPCHK(hipEventCreate(&e0));
     OPCHK(hipEventCreate(&e1));
@@ -1921,23 +1718,31 @@ int tf_hip_read_stream(int device, size_t nbytes, int32_t iters, double* best, d
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    hipError_t e = hipSuccess;
+    const uint32_t sum = sink_total(sink, n_sink, s.st, &e);
+    OPCHK(e);
+    if (checksum) *checksum = sum;
     std::sort(gbs.begin(), gbs.end());
     *best = gbs.back();
     *median = gbs[gbs.size() / 2];
     return 0;
 }
 
-int tf_hip_copy_stream(int device, size_t nbytes, int32_t iters, double* best, double* median) {
+int tf_hip_copy_stream(int device, size_t nbytes, int32_t iters, double* best, double* median, uint32_t* checksum) {
     if (nbytes < 16 || iters <= 0 || !best || !median) return TF_HIP_EINVAL;
     OpScope s;
     int rc = op_begin(device, s);
     if (rc) return rc;
     const size_t n4 = nbytes / 16;
-    float4 *src, *dst;
+    uint4 *src, *dst;
+    uint32_t* sink;
     const int blocks = 8 * device_cu_count();
+    const size_t n_sink = (size_t)blocks * kWavesPerBlock;
     OPCHK(s.alloc(&src, n4 * 16));
     OPCHK(s.alloc(&dst, n4 * 16));
-    OPCHK(hipMemset(src, 0, n4 * 16));
+    OPCHK(s.alloc(&sink, n_sink * sizeof(uint32_t)));
+    OPCHK(launch_fill_stream(src, n4, blocks, s.st));
+    OPCHK(hipMemsetAsync(dst, 0, n4 * 16, s.st));
     hipEvent_t e0, e1;
     OPCHK(hipEventCreate(&e0));
     OPCHK(hipEventCreate(&e1));
@@ -1954,6 +1759,12 @@ int tf_hip_copy_stream(int device, size_t nbytes, int32_t iters, double* best, d
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    // the copy's destination summed by the read stream's kernel
+    OPCHK(launch_read_stream(dst, n4, sink, blocks, s.st));
+    hipError_t e = hipSuccess;
+    const uint32_t sum = sink_total(sink, n_sink, s.st, &e);
+    OPCHK(e);
+    if (checksum) *checksum = sum;
     std::sort(gbs.begin(), gbs.end());
     *best = gbs.back();
     *median = gbs[gbs.size() / 2];

@@ -148,7 +148,6 @@ struct StepArgs {
     int split_all;             // > 0: splits per kv head when every workgroup splits (step_split_all)
     int split_all_from;        // spans longer than this use split_all (step_split_all_from)
     int split_from;            // spans (positions attended) up to this attend on one workgroup per kv head
-    unsigned long long* dbg;   // builds with TF_STEP_PROBE: [n_layer + 1][n_wg][16] time stamps, or nullptr
 };
 
 // ---------------------------------------------------------------- prefill on the matrix cores
@@ -255,23 +254,6 @@ hipError_t launch_step(const StepArgs& a, int type_layers, int type_out, int n_w
 // the Q8_0 builds with ffn_down split over K (stage_lds 2)
 hipError_t launch_step_split(const StepArgs& a, int n_wg, hipStream_t st);
 
-// ---------------------------------------------------------------- streaming step kernel (k_stream.hpp)
-struct StepLayer;
-struct StreamArgs;
-// true when the streaming kernel runs this model: Q8_0 layer matrices and lm_head, head
-// size <= 128, row lengths divisible by 64.
-bool stream_supported(int type_layers, int type_out, int hd, int n_rep, int D, int F, int H);
-// Per-(workgroup, compute wave) streams of one token: byte offsets, first slot in the
-// steps table, slots of the layers and of the whole token; totals and the largest stream.
-int stream_plan(int n_layer, int D, int F, int H, int G, int hd, int V, int nwg, std::vector<uint64_t>& sbase,
-                std::vector<uint32_t>& sfirst, std::vector<uint32_t>& snl, std::vector<uint32_t>& snt,
-                uint64_t* stream_bytes, uint32_t* steps_total, int* steps_max);
-int stream_ring_slots(int n_layer, int D, int F, int H, int G, int hd, int V, int nwg, int steps_max);
-hipError_t launch_stream_pack(const StepLayer* d_layers, const DevMat& out, int n_layer, int D, int F, int H, int G,
-                              int hd, int V, int nwg, uint8_t* stream, const uint64_t* sbase, uint8_t* ssteps,
-                              const uint32_t* sfirst, hipStream_t st);
-hipError_t launch_stream(const StreamArgs& a, int nwg, hipStream_t st);
-
 // Launchers (k_*.hip).
 hipError_t launch_gemv(const GemvArgs& a, int rows_per_wave, hipStream_t st);
 int64_t gemv_groups(int64_t n_rows, int rows_per_wave);
@@ -291,8 +273,12 @@ hipError_t launch_sample(const float* logits, int n, float temperature, float to
 hipError_t launch_rope_rows(float* x, int seq, int n_heads, int hd, int pos0, const float* cos_tab,
                             const float* sin_tab, hipStream_t st);
 hipError_t launch_argmax(const float* x, int n, Ctl* ctl, hipStream_t st);
-hipError_t launch_copy_stream(float4* dst, const float4* src, size_t n4, int blocks, hipStream_t st);
-hipError_t launch_read_stream(const float4* p, size_t n4, double* out, int blocks, hipStream_t st);
+// The read and copy streams (k_misc.hip): buffers filled by launch_fill_stream hold 32-bit
+// word i = i * kStreamMul, and k_read_stream writes one integer partial sum per wave.
+constexpr uint32_t kStreamMul = 0x9E3779B1u;
+hipError_t launch_copy_stream(uint4* dst, const uint4* src, size_t n4, int blocks, hipStream_t st);
+hipError_t launch_read_stream(const uint4* p, size_t n4, uint32_t* out, int blocks, hipStream_t st);
+hipError_t launch_fill_stream(uint4* p, size_t n4, int blocks, hipStream_t st);
 int device_cu_count();
 
 }  // namespace tfk

@@ -89,6 +89,23 @@ int tfh_generate(void* hp, int32_t n, int32_t* out) {
     return guard(h, [&] { h->m->generate(n, out); });
 }
 
+// The greedy loop of a caller of the reference's Model with the backend switch patched in
+// (bench_e2e.cpp:49-54 over model.cpp:197-208 as forwarded to tf_hip_decode): every step
+// copies the logits to the host and takes their first maximum there (sample_greedy,
+// sampler.cpp:8-13). out[i] is the token fed to step i, starting with `first`.
+int tfh_greedy_host(void* hp, int32_t first, int32_t n, int32_t* out) {
+    Handle* h = (Handle*)hp;
+    return guard(h, [&] {
+        std::vector<float> logits((size_t)h->m->n_vocab());
+        int tok = first;
+        for (int i = 0; i < n; ++i) {
+            out[i] = tok;
+            h->m->decode(tok, logits.data());
+            tok = (int)(std::max_element(logits.begin(), logits.end()) - logits.begin());
+        }
+    });
+}
+
 int tfh_reset(void* hp) {
     Handle* h = (Handle*)hp;
     return guard(h, [&] { h->m->reset(); });

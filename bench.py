@@ -62,6 +62,7 @@ TRAFFIC_SUMMARIES = {
     "cfg1": ROOT / "profiles" / "decode_llama1b_q8_0_step_kernel_traffic.txt",
     "cfg2": ROOT / "profiles" / "decode_qwen05b_q8_0_step_kernel_traffic.txt",
     "cfg3": ROOT / "profiles" / "decode_llama1b_mixq4_step_kernel_traffic.txt",
+    "cfg4": ROOT / "profiles" / "decode_llama1b_q8_0_512_step_kernel_traffic.txt",
     "cfg5": ROOT / "profiles" / "decode_qwen15b_q8_4096_step_kernel_traffic.txt",
 }
 # context sweep: decode after prompts of these lengths, cache of CTX_MAX_SEQ positions
@@ -135,18 +136,42 @@ def ensure_model(pkg, preset: str, threads: int):
     return path, info
 
 
-def measured_traffic(key: str, tokens: int):
-    """HBM bytes of `tokens` decoded tokens of the step kernel from the config's committed
-    counter summary (None when there is none)."""
+def kernel_source_digest() -> str:
+    """sha256 (first 16 hex digits) of the kernel sources (agent-serve_amd/csrc/*) and the
+    ABI header: the counter summaries record the digest of the build they measured."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted((ROOT / "agent-serve_amd" / "csrc").glob("*")) + [ROOT / "include" / "tf_hip.h"]
+    for f in files:
+        if f.is_file():
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(key: str, tokens: int, kernel: str):
+    """HBM bytes of `tokens` decoded tokens of `kernel` from the config's committed counter
+    summary, and where they come from: the summary, the commit and kernel-source digest it
+    measured, and whether that digest is the one of the sources being benched (a summary of
+    other sources is reported with current false and traffic null)."""
     path = TRAFFIC_SUMMARIES.get(key)
+    per_token, meta = None, {}
     try:
         for line in path.read_text().splitlines():
             f = line.split()
-            if len(f) == 3 and f[0] == "traffic_bytes_per_token" and f[1] == "k_step":
-                return int(float(f[2]) * tokens), str(path.relative_to(ROOT))
+            if len(f) == 3 and f[0] == "traffic_bytes_per_token" and f[1] == kernel:
+                per_token = float(f[2])
+            elif len(f) == 2 and f[0] in ("commit", "csrc_sha256"):
+                meta[f[0]] = f[1]
     except (OSError, AttributeError):
-        pass
-    return None, None
+        return None, None
+    src = {"summary": str(path.relative_to(ROOT)), "commit": meta.get("commit"),
+           "csrc_sha256": meta.get("csrc_sha256"),
+           "current": meta.get("csrc_sha256") == kernel_source_digest()}
+    if per_token is None or not src["current"]:
+        return None, src
+    return int(per_token * tokens), src
 
 
 def prefill_flops(info, n):
@@ -183,7 +208,10 @@ def e2e_once(m, prompt, n_predict):
 def gpu_config(pkg, key, desc, preset, n_prompt, n_dec, max_seq, layout, runs, warmup, threads):
     path, info = ensure_model(pkg, preset, threads)
     prompt = pkg.synth_prompt(info["seed"], n_prompt, info["n_vocab"])
+    # load + upload: GGUF read, every tensor copied to the device and repacked (model.cpp:9-78)
+    t0 = time.perf_counter()
     m = pkg.HipModel(path, max_seq=max_seq, kv_layout=layout)
+    upload_s = time.perf_counter() - t0
     wall_first = None
     for w in range(max(1, warmup)):
         t0 = time.perf_counter()
@@ -207,9 +235,19 @@ def gpu_config(pkg, key, desc, preset, n_prompt, n_dec, max_seq, layout, runs, w
     gen = m.generate(n_dec)
     loop_wall = time.perf_counter() - t0
     k_ms, _, launches, k_name = m.last_timing()
+    # the drop-in path: the reference's loop over the patched Model::decode, logits copied to
+    # the host every step and sample_greedy there (bench_e2e.cpp:49-54)
+    dropin_tps, dropin_ids = [], None
+    for _ in range(max(1, runs // 2)):
+        m.reset()
+        logits, _ = m.prefill(prompt, want_logits=True)
+        first = int(logits.argmax())
+        t0 = time.perf_counter()
+        dropin_ids = m.greedy_host(first, n_dec)
+        dropin_tps.append(n_dec / (time.perf_counter() - t0))
     step_bytes = [m.decode_bytes(n_prompt + i) for i in range(n_dec)]
     achieved = sum(step_bytes) / (k_ms * 1e-3) / 1e9
-    traffic, traffic_src = measured_traffic(key, n_dec)
+    traffic, traffic_src = measured_traffic(key, n_dec, k_name)
     path_name = "persistent step kernel" if m.decode_path() == m.PATH_STEP else "graph"
     m.close()
     return {
@@ -224,6 +262,12 @@ def gpu_config(pkg, key, desc, preset, n_prompt, n_dec, max_seq, layout, runs, w
             "decode_tok_ms_p99": round(statistics.median(p99), 4),
             "note": "one synchronous call per token (device argmax returned, no logits copy), host wall clock",
         },
+        "dropin_loop": {"decode_tok_s": med_iqr(dropin_tps, 1),
+                        "logits_bytes_per_token": 4 * info["n_vocab"],
+                        "tokens_match_e2e": bool(list(dropin_ids) == list(ids)),
+                        "note": "Model::decode as the backend patch forwards it: logits to the host every "
+                                "token, first-max argmax on the host (C++ loop, tfh_greedy_host)"},
+        "upload_s": round(upload_s, 3),
         "device_loop": {"decode_tok_s": round(n_dec / loop_wall, 1), "kernel_ms": round(k_ms, 4),
                         "launches": launches, "prefill_device_ms": round(pf_dev_ms, 4),
                         "prefill_tok_s": round(n_prompt / (pf_dev_ms * 1e-3), 1),
@@ -400,8 +444,8 @@ def main() -> int:
     m.prefill(prompt, want_logits=False)
     ids_prof, prof = m.profile_generate(K)
     m.close()
-    traffic, traffic_src = measured_traffic(HEADLINE, K)
-    read_best, read_med = pkg.read_stream(4 << 30, iters=10)
+    traffic, traffic_src = measured_traffic(HEADLINE, K, kname)
+    read_best, read_med, read_cs = pkg.read_stream(4 << 30, iters=10, with_checksum=True)
     copy_best, _ = pkg.copy_stream(COPY_CALIB_BYTES, iters=3)
     value = K / wall_s
 
@@ -474,6 +518,7 @@ def main() -> int:
         "step_hbm_gb_s": round(sum(step_bytes) / wall_s / 1e9, 1),
         "read_stream_gb_s": round(read_best, 1),
         "read_stream_median_gb_s": round(read_med, 1),
+        "read_stream_checksum_ok": read_cs == pkg.stream_checksum(4 << 30),
         "copy_stream_gb_s": round(copy_best, 1),
         "frac_of_read_stream": round(achieved / read_best, 4),
         "bytes_per_step": round(statistics.mean(step_bytes)),

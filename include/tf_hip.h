@@ -29,7 +29,7 @@ extern "C" {
 #define TF_HIP_ERANGE -2   /* max_seq exceeded or token out of range (model.cpp:185, 198) */
 #define TF_HIP_ENOMEM -3   /* device allocation failed */
 #define TF_HIP_EDEVICE -4  /* HIP runtime error */
-#define TF_HIP_ESTATE -5   /* required tensors not uploaded */
+#define TF_HIP_ESTATE -5   /* call not allowed in this state (tensors not uploaded, first no-alloc call under capture) */
 #define TF_HIP_ESCRATCH -6 /* request larger than a static scratch (tf_hip_attn_decode_noalloc) */
 
 /* ggml tensor types accepted by the token loop (tensor.cpp:18-28) */
@@ -120,16 +120,13 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
  * per-layer kernels replayed per token. Both compute the same function; neither has a
  * counterpart in the reference (a backend choice below Model::decode, model.cpp:197-208).
  * tf_hip_get_decode_path returns the path the next call will take (needs every tensor
- * uploaded). The environment variable TF_HIP_DECODE_PATH (step, graph or stream), read by
+ * uploaded). The environment variable TF_HIP_DECODE_PATH (step or graph), read by
  * tf_hip_create, sets the initial path for callers that never call the setter. The step
- * and stream paths launch cooperatively: one process at a time can hold the GPU's
- * cooperative-launch resource, so a second process on the same GPU needs the graph path. */
+ * path launches cooperatively; when the GPU refuses the cooperative launch (another
+ * process holds that resource, or the grid does not fit), the context switches itself to
+ * the graph path for the rest of its life and tf_hip_get_decode_path reports that. */
 #define TF_HIP_PATH_GRAPH 0
 #define TF_HIP_PATH_STEP 1
-/* TF_HIP_PATH_STREAM: the persistent kernel with every wave streaming its weight tiles
- * through an LDS ring of its own at a bounded depth (Q8_0 models with head size <= 128);
- * models it does not cover take TF_HIP_PATH_STEP's choice. */
-#define TF_HIP_PATH_STREAM 2
 int tf_hip_set_decode_path(tf_hip_ctx* ctx, int32_t path);
 int tf_hip_get_decode_path(tf_hip_ctx* ctx);
 
@@ -161,6 +158,16 @@ int tf_hip_get_step_config(tf_hip_ctx* ctx, int32_t* out, int32_t n);
  * counter, so that a test can run a launch across the counter's wrap at 2^32 (the kernel
  * then clears its exchange words and starts the count again). */
 int tf_hip_set_exchange_epoch(tf_hip_ctx* ctx, uint32_t epoch);
+
+/* The hyperparameters the context was created with (Model's accessors, model.hpp; the
+ * device KV cache's layout is out->kv_layout). With the environment variable TF_HIP_LOG
+ * set (and not "0"), tf_hip_create also prints them as one line on stderr. */
+int tf_hip_get_hparams(const tf_hip_ctx* ctx, tf_hip_hparams* out);
+
+/* Test hook (no counterpart in the reference): the next n launches of the step kernel on
+ * this context report the refusal a GPU gives when another process holds its
+ * cooperative-launch resource, so a test can check the switch to the graph path. */
+int tf_hip_test_refuse_cooperative(tf_hip_ctx* ctx, int32_t n);
 
 /* Prefill path (no counterpart in the reference, whose layer_prefill is the one
  * path, model.cpp:144-195): TF_HIP_PREFILL_MFMA runs a prompt of two or more tokens
@@ -195,8 +202,10 @@ int tf_hip_last_timing(const tf_hip_ctx* ctx, float* total_ms, float* kernel_ms,
 
 /* The loop of tf_hip_generate with each kernel launched on its own (no graph) and bracketed
  * by HIP events on the context stream. Per kernel class k < TF_HIP_KERNEL_CLASSES it
- * reports the summed device milliseconds, the launch count and the algorithmic bytes
- * (weights read; attention reports 0). Classes: 0 embedding, 1 QKV GEMV, 2 attention,
+ * reports the summed device milliseconds, the launch count and the algorithmic bytes (the
+ * weights, norm weights and biases each kernel reads; attention the K and V rows it reads
+ * and the new row it writes), so that over a step they add up to the decode byte formula
+ * (every tensor once + one embedding row + K/V rows). Classes: 0 embedding, 1 QKV GEMV, 2 attention,
  * 3 attn_output GEMV, 4 gate/up GEMV, 5 down GEMV, 6 lm_head GEMV (tf_hip_kernel_class_name). */
 #define TF_HIP_KERNEL_CLASSES 7
 int tf_hip_profile_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens, float* ms_by_class,
@@ -251,7 +260,10 @@ int tf_hip_attn_decode(int device, const float* q, const float* k_rows, const fl
  * process ends): n_heads * S * (hd + 2) * 4 bytes must fit, else TF_HIP_ESCRATCH before
  * any launch. Every call on a GPU shares that GPU's scratch, so calls that overlap on
  * one GPU (other streams, other host threads) race; each call rewrites every partial it
- * reads, so nothing needs clearing between calls. */
+ * reads, so nothing needs clearing between calls. The first call on each device looks up
+ * the scratch's address and must be made outside graph capture (a warm-up call); made on a
+ * capturing stream it returns TF_HIP_ESTATE and enqueues nothing. Later calls may be
+ * captured: the graph then replays the same kernels on the same scratch. */
 #define TF_HIP_ATTN_SCRATCH_BYTES (4u << 20)
 int tf_hip_attn_decode_noalloc(int device, const float* q, const float* k_cache, const float* v_cache,
                                int32_t n_heads, int32_t n_kv, int32_t hd, int32_t n_pos, int32_t max_seq,
@@ -284,13 +296,20 @@ int tf_hip_sample_logits(int device, const float* logits, int32_t n, float tempe
 int tf_hip_argmax(int device, const float* x, int32_t n, int32_t* out);
 
 /* Read-only HBM stream (the GPU analogue of bench/stream.c:128-141): sums nbytes of device
- * memory `iters` times; reports the best and median GB/s over the iterations. */
-int tf_hip_read_stream(int device, size_t nbytes, int32_t iters, double* best_gbs, double* median_gbs);
+ * memory `iters` times; reports the best and median GB/s over the iterations. The buffer
+ * holds 32-bit word i = i * 0x9E3779B1 (mod 2^32), summed as integers, so *checksum (may be
+ * NULL) is 0x9E3779B1 * n (n - 1) / 2 mod 2^32 for n = nbytes / 16 * 4 words exactly when
+ * every word was read. */
+int tf_hip_read_stream(int device, size_t nbytes, int32_t iters, double* best_gbs, double* median_gbs,
+                       uint32_t* checksum);
 
 /* Copy stream (the GPU analogue of kernel_copy, bench/stream.c:106-115): copies nbytes
  * between two device buffers `iters` times; GB/s counts the bytes read plus the bytes
- * written. Its kernel (k_copy_stream) is also the known-size reference for HBM counters. */
-int tf_hip_copy_stream(int device, size_t nbytes, int32_t iters, double* best_gbs, double* median_gbs);
+ * written. Its kernel (k_copy_stream) is also the known-size reference for HBM counters.
+ * The source holds the read stream's pattern and *checksum (may be NULL) is the read
+ * stream's sum over the destination after the copies. */
+int tf_hip_copy_stream(int device, size_t nbytes, int32_t iters, double* best_gbs, double* median_gbs,
+                       uint32_t* checksum);
 
 #ifdef __cplusplus
 }

@@ -40,15 +40,13 @@ def model_parity(pkg, path, prompt, n, max_seq, layout, tol=1e-3, taps=True, dec
     """Decode the oracle's greedy stream on both sides, comparing logits, argmax and
     per-layer activations at every step; then the device greedy loop from a reset.
     Errors must also stay under REGRESS.
-    decode_path: HipModel.PATH_GRAPH / PATH_STEP / PATH_STREAM; prefill_path: HipModel.PREFILL_TOKENS /
+    decode_path: HipModel.PATH_GRAPH / PATH_STEP; prefill_path: HipModel.PREFILL_TOKENS /
     PREFILL_MFMA; None for the defaults. setup(hip): called once on the model before use.
     Returns (oracle ids, max logits rel err, max tap rel err, min top-2 margin)."""
     orc = OracleModel(path, max_seq=max_seq, kv_layout=layout, n_threads=n_threads())
     hip = pkg.HipModel(path, max_seq=max_seq, kv_layout=layout)
     if decode_path is not None:
         hip.set_decode_path(decode_path)
-        if decode_path == pkg.HipModel.PATH_STREAM:
-            assert hip.decode_path() == decode_path, "the streaming kernel was not chosen"
     if prefill_path is not None:
         hip.set_prefill_path(prefill_path)
     if setup is not None:

@@ -13,16 +13,13 @@ from gpu_util import REGRESS, model_parity
 pytestmark = pytest.mark.gpu
 
 SMALL = ["tiny_f32", "tiny_q8", "tiny_mixq4", "tiny_qwen", "tiny_hd128", "small_q8"]
-GRAPH, STEP, STREAM = 0, 1, 2  # HipModel.PATH_GRAPH, PATH_STEP, PATH_STREAM
-Q8 = ["tiny_q8", "tiny_qwen", "tiny_hd128", "small_q8"]  # presets the streaming kernel runs
+GRAPH, STEP = 0, 1  # HipModel.PATH_GRAPH, PATH_STEP
 
 
-@pytest.mark.parametrize("path", [GRAPH, STEP, STREAM], ids=["graph", "step", "stream"])
+@pytest.mark.parametrize("path", [GRAPH, STEP], ids=["graph", "step"])
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("preset", SMALL)
 def test_small_models(pkg, gguf, preset, layout, path):
-    if path == STREAM and preset not in Q8:
-        pytest.skip("the streaming kernel runs Q8_0 models; others take the step kernel")
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"], 6, info["n_vocab"])
     ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 16, 64, layout, decode_path=path)
@@ -47,16 +44,14 @@ def test_decode_path_selection(pkg, gguf, preset, want):
     big.close()
 
 
-@pytest.mark.parametrize("path", [GRAPH, STEP, STREAM], ids=["graph", "step", "stream"])
+@pytest.mark.parametrize("path", [GRAPH, STEP], ids=["graph", "step"])
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("preset", ["tiny_q8", "tiny_f32", "tiny_qwen", "small_q8", "tiny_mixq4", "tiny_hd128"])
 def test_long_cache_split_attention(pkg, gguf, preset, layout, path):
     """A 600-token prompt in a 1024-position cache: the step kernel's attention splits the
     positions over its trailing workgroups and merges the splits there, the graph path's
-    over split workgroups and a combine launch, the stream kernel's over every workgroup;
-    each against the oracle while decoding past it."""
-    if path == STREAM and preset not in Q8:
-        pytest.skip("the streaming kernel runs Q8_0 models; others take the step kernel")
+    over split workgroups and a combine launch; each against the oracle while decoding
+    past it."""
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"] + 7, 600, info["n_vocab"])
     ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, 1024, layout, decode_path=path)
@@ -149,6 +144,42 @@ def test_exchange_epoch_wrap(pkg, gguf):
         hip.close()
     assert np.array_equal(out[0][0], out[1][0])
     assert np.array_equal(out[0][1], out[1][1])
+
+
+@pytest.mark.parametrize("call", ["generate", "decode", "prefill"])
+def test_cooperative_refusal_falls_back_to_graph(pkg, gguf, call):
+    """A refused cooperative launch (another process holding the GPU's cooperative-launch
+    resource, forced here through the test hook) runs the same tokens on the graph path,
+    and the context stays there; the greedy stream equals the oracle's."""
+    from oracle.bind import OracleModel, greedy_stream
+
+    path = gguf("tiny_q8")
+    info = pkg.synth_preset_info("tiny_q8")
+    prompt = pkg.synth_prompt(info["seed"], 6, info["n_vocab"])
+    ref_ids, _ = greedy_stream(OracleModel(path, max_seq=64, n_threads=4), prompt, 12)
+    hip = pkg.HipModel(path, max_seq=64)
+    try:
+        assert hip.decode_path() == STEP
+        if call == "prefill":
+            hip.set_prefill_path(pkg.HipModel.PREFILL_TOKENS)  # the prompt runs on the decode path
+            hip.test_refuse_cooperative(1)
+        _, am = hip.prefill(prompt)
+        assert am == ref_ids[0]
+        if call == "decode":
+            hip.test_refuse_cooperative(1)
+            _, am2 = hip.decode(int(ref_ids[0]))
+            assert am2 == ref_ids[1]
+            assert np.array_equal(hip.generate(10), ref_ids[1:11])
+        else:
+            if call == "generate":
+                hip.test_refuse_cooperative(1)
+            ids = hip.generate(11)
+            assert np.array_equal(ids, ref_ids[:11])
+        assert hip.decode_path() == GRAPH
+        hip.set_decode_path(STEP)  # the switch holds for the context's life
+        assert hip.decode_path() == GRAPH
+    finally:
+        hip.close()
 
 
 TOKENS, MFMA = 0, 1  # HipModel.PREFILL_TOKENS, HipModel.PREFILL_MFMA
@@ -288,20 +319,6 @@ def test_full_size(pkg, gguf, preset, n_prompt, n_gen, max_seq, layout):
     prompt = pkg.synth_prompt(info["seed"], n_prompt, info["n_vocab"])
     ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, n_gen, max_seq, layout)
     print(f"{preset}: {len(ids)} tokens identical; logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
-
-
-@pytest.mark.parametrize("preset,n_prompt,n_gen,max_seq,layout", [
-    ("llama1b_q8", 6, 32, 512, 0),
-    ("qwen05b_q8", 16, 32, 512, 0),
-    ("qwen15b_q8", 64, 16, 8192, 1),
-])
-def test_full_size_stream(pkg, gguf, preset, n_prompt, n_gen, max_seq, layout):
-    """The Q8_0 workloads at full size through the streaming kernel, against the oracle."""
-    info = pkg.synth_preset_info(preset)
-    prompt = pkg.synth_prompt(info["seed"], n_prompt, info["n_vocab"])
-    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, n_gen, max_seq, layout,
-                                                 decode_path=STREAM)
-    print(f"{preset} stream: {len(ids)} tokens identical; logits {worst:.2e} taps {worst_tap:.2e}")
 
 
 GOLDEN =__import__("pathlib").Path(__file__).resolve().parent / "golden"

@@ -126,3 +126,12 @@ def test_model_rope_tables_from_file(pkg, gguf, preset):
     rc, rs = _ref_tables(_ref_freqs(theta, hd), 256)
     assert np.array_equal(c.view(np.uint32), rc.view(np.uint32))
     assert np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+
+
+def test_stream_checksum_closed_form(pkg):
+    """The streams' expected checksum (word i = i * 0x9E3779B1, summed mod 2^32) against a
+    brute-force sum, including sizes that are not a multiple of 16 bytes."""
+    for nbytes in (16, 48, 4096, 1 << 20, (1 << 20) + 40):
+        n = nbytes // 16 * 4
+        words = (np.arange(n, dtype=np.uint64) * np.uint64(0x9E3779B1)) % np.uint64(1 << 32)
+        assert pkg.stream_checksum(nbytes) == int(words.sum() % np.uint64(1 << 32)), nbytes

@@ -31,6 +31,12 @@ class Hip:
         self.L.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
         self.L.hipStreamSynchronize.argtypes = [C.c_void_p]
         self.L.hipStreamDestroy.argtypes = [C.c_void_p]
+        self.L.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        self.L.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        self.L.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+        self.L.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        self.L.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        self.L.hipGraphDestroy.argtypes = [C.c_void_p]
         assert self.L.hipSetDevice(0) == 0
         self.mem = []
 
@@ -121,4 +127,63 @@ def test_noalloc_attention_rejects_requests_past_its_scratch(pkg):
                                                       None)
         assert rc == E_SCRATCH
     finally:
+        hip.close()
+
+
+CAPTURE_GLOBAL = 0  # hipStreamCaptureModeGlobal
+
+
+def test_noalloc_attention_under_graph_capture(pkg):
+    """After a warm-up call outside capture (the first call on a device looks up the
+    scratch's address), the entry point is captured into a graph on a caller's stream; each
+    replay, with the output cleared and other calls rewriting the shared scratch in between,
+    gives tf_hip_attn_decode's result bit for bit."""
+    n_heads, n_kv, hd, n_pos, max_seq, layout = CASES[0]
+    hip = Hip(pkg)
+    stream = C.c_void_p()
+    assert hip.L.hipStreamCreate(C.byref(stream)) == 0
+    graph, gexec = C.c_void_p(), C.c_void_p()
+    rng = np.random.default_rng(131)
+    lib = pkg.hip_lib()
+    try:
+        q = rng.standard_normal((n_heads, hd)).astype(np.float32)
+        k = rng.standard_normal((n_pos, n_kv, hd)).astype(np.float32)
+        v = rng.standard_normal((n_pos, n_kv, hd)).astype(np.float32)
+        want = pkg.attn_decode(q, k, v, max_seq, layout)
+        dq = hip.upload(q)
+        dk = hip.upload(cache_of(k, max_seq, layout))
+        dv = hip.upload(cache_of(v, max_seq, layout))
+        out = hip.upload(np.full(q.shape, np.nan, np.float32))
+        q2 = hip.upload(rng.standard_normal((n_heads, hd)).astype(np.float32))
+        out2 = hip.upload(np.zeros(q.shape, np.float32))
+
+        def call(qp, op):
+            return lib.tf_hip_attn_decode_noalloc(0, qp, dk, dv, n_heads, n_kv, hd, n_pos, max_seq, layout, op,
+                                                 stream)
+
+        assert call(dq, out) == 0  # warm-up, outside capture
+        assert hip.L.hipStreamSynchronize(stream) == 0
+        assert np.array_equal(hip.download(out, q.shape).view(np.uint32), want.view(np.uint32))
+
+        assert hip.L.hipStreamBeginCapture(stream, CAPTURE_GLOBAL) == 0
+        rc = call(dq, out)
+        assert hip.L.hipStreamEndCapture(stream, C.byref(graph)) == 0
+        assert rc == 0
+        assert hip.L.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0) == 0
+        nan = np.full(q.shape, np.nan, np.float32)
+        for replay in range(3):
+            assert hip.L.hipMemcpy(out, nan.ctypes.data, nan.nbytes, H2D) == 0
+            assert hip.L.hipGraphLaunch(gexec, stream) == 0
+            assert hip.L.hipStreamSynchronize(stream) == 0
+            got = hip.download(out, q.shape)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), replay
+            assert call(q2, out2) == 0  # eager work between replays rewrites the scratch
+            assert hip.L.hipStreamSynchronize(stream) == 0
+    finally:
+        hip.L.hipStreamSynchronize(stream)
+        if gexec.value:
+            hip.L.hipGraphExecDestroy(gexec)
+        if graph.value:
+            hip.L.hipGraphDestroy(graph)
+        hip.L.hipStreamDestroy(stream)
         hip.close()
