@@ -535,11 +535,13 @@ int epoch_guard(tf_hip_ctx* c, int n) {
     return 0;
 }
 
-// run_step's result when the GPU refused the cooperative launch (another process holds the
-// cooperative-launch resource, or the grid no longer fits): nothing ran.
+// run_step's result when the GPU refused the cooperative launch: nothing ran. A second
+// process on a GPU whose cooperative-launch resource another process holds gets
+// hipErrorIllegalState (measured on MI355X); a grid that no longer fits, the others.
 constexpr int kStepRefused = 1;
 bool coop_refusal(hipError_t e) {
-    return e == hipErrorCooperativeLaunchTooLarge || e == hipErrorLaunchOutOfResources || e == hipErrorNotSupported;
+    return e == hipErrorIllegalState || e == hipErrorCooperativeLaunchTooLarge || e == hipErrorLaunchOutOfResources ||
+           e == hipErrorNotSupported;
 }
 
 // n tokens through the persistent step kernel, from position c->pos. Returns 0,

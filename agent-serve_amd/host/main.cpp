@@ -52,7 +52,8 @@ void usage() {
                  "  --kv-layout seq|head override KV layout\n"
                  "  --no-bos             do not prepend BOS\n"
                  "  --device N           HIP device (default 0)\n"
-                 "  --decode-path P      step (persistent kernel, the default) | graph\n"
+                 "  --decode-path P      step (persistent kernel, the default) | graph; a step kernel the\n"
+                 "                       GPU refuses (another process holds it) runs as graph\n"
                  "  --profile            print the per-kernel-class breakdown of one greedy pass\n");
 }
 
@@ -68,7 +69,7 @@ std::vector<int> parse_tokens(const std::string& s) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    std::string model_path, prompt, token_str, stage = "v2", kv_layout, decode_path = "step";
+    std::string model_path, prompt, token_str, stage = "v2", kv_layout, decode_path;
     int n_predict = 64, seed = 42, max_seq = 4096, device = 0;
     float temp = 0, topp = 0.9f;
     bool profile = false, add_bos = true;
@@ -119,10 +120,11 @@ int main(int argc, char** argv) {
         if (kv_layout == "seq") cfg.kv_layout = KVLayout::SeqMajor;
         Model model(model_path, cfg);
         const Tokenizer tok(model.gguf());
+        // without the flag the library's choice stands (step, or TF_HIP_DECODE_PATH)
         if (decode_path == "graph" || decode_path == "step") {
             if (tf_hip_set_decode_path(model.ctx(), decode_path == "graph" ? TF_HIP_PATH_GRAPH : TF_HIP_PATH_STEP))
                 die("tf_hip_set_decode_path failed");
-        } else {
+        } else if (!decode_path.empty()) {
             die("--decode-path takes step or graph");
         }
         std::fprintf(stderr, "%s\n", model.describe().c_str());

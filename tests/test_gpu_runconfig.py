@@ -53,9 +53,10 @@ def _run(args, env):
 def _cli_case(pkg, gguf):
     info = pkg.synth_preset_info("tiny_qwen")
     toks = ",".join(str(t) for t in pkg.synth_prompt(info["seed"], 6, info["n_vocab"]))
-    # graph path: a test process that launched the step kernel holds the GPU's
-    # cooperative-launch resource, which a child process cannot take at the same time
-    env = dict(os.environ, TF_HIP_LOG="1", TF_HIP_DECODE_PATH="graph")
+    # no decode path is forced: a test process that launched the step kernel holds the
+    # GPU's cooperative-launch resource, and the child's refused step launch then runs its
+    # tokens on the graph path (the library's fallback)
+    env = dict(os.environ, TF_HIP_LOG="1")
     return gguf("tiny_qwen"), toks, env
 
 
