@@ -38,6 +38,28 @@ __device__ __forceinline__ float4 gload_f4(const void* p) {
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// Direct global -> LDS loads (global_load_lds), issued from inline assembly: lane i of a
+// 16-byte load writes LDS at m0 + 16 i (4 i for a dword load), m0 saved and restored around
+// it, with the one wait state gfx9 parts need between an SALU write of m0 and an LDS-DMA
+// instruction (s_nop 0; the compiler's hazard recognizer does not look inside inline asm).
+// Written as assembly so that the compiler does not count these loads: it would wait for
+// all of them before every LDS read (it cannot tell the buffer a load targets); the kernel
+// waits for them itself (s_waitcnt vmcnt with the count of its later loads).
+__device__ __forceinline__ void lds_dma16(const TF_GLOBAL void* g, uint32_t m0) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(m0), "v"(g)
+                 : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const TF_GLOBAL void* g, uint32_t m0) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"(m0), "v"(g)
+                 : "memory");
+}
+
 // IEEE half bits -> float (v_cvt_f32_f16: exact for every half value).
 __device__ __forceinline__ float h2f(uint32_t bits16) {
     _Float16 v;

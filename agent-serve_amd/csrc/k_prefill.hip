@@ -352,26 +352,6 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
     }
 }
 
-// Direct global -> LDS loads (global_load_lds), issued from inline assembly: lane i of a
-// 16-byte load writes LDS at m0 + 16 i (4 i for a dword load), m0 saved and restored around
-// it. Written as assembly so that the compiler does not count these loads: it would wait
-// for all of them before every LDS read (it cannot tell the buffer a load targets); the
-// kernel waits for them itself (s_waitcnt vmcnt with the count of its later loads).
-__device__ __forceinline__ void lds_dma16(const TF_GLOBAL void* g, uint32_t m0) {
-    uint32_t save;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(save)
-                 : "s"(m0), "v"(g)
-                 : "memory");
-}
-__device__ __forceinline__ void lds_dma4(const TF_GLOBAL void* g, uint32_t m0) {
-    uint32_t save;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(save)
-                 : "s"(m0), "v"(g)
-                 : "memory");
-}
-
 // Large tiles for GEMMs with enough of them to fill the CUs: a workgroup of 8 waves
 // (2 rows x 4 columns of waves) owns 128 rows x 16 weight-column subtiles (256 weight rows;
 // GEMV_SILU: 8 gate and the 8 matching up subtiles, 128 output columns). A stage (one

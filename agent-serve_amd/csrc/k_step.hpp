@@ -76,7 +76,7 @@ __device__ __forceinline__ void set_err(Ctl* c, int v) {
 // words tid + i*kT. Every load of the first pass is issued before any is checked; a word
 // that does not carry its epoch yet is read again (bit i of `pend`) until it does.
 // Needs na <= NA * kT, nb <= NB * kT, NA + NB <= 32.
-template <int NA, int NB>
+template <int NA, int NB, int SLEEP = 1>
 __device__ __forceinline__ void gather(u64* pa, int na, uint32_t ea, float* da, u64* pb, int nb, uint32_t eb,
                                        Ctl* ctl) {
     const int tid = threadIdx.x;
@@ -103,10 +103,10 @@ __device__ __forceinline__ void gather(u64* pa, int na, uint32_t ea, float* da, 
         if (tid + i * kT < nb && (uint32_t)(wb[i] >> 32) != eb) pend |= 1u << (NA + i);
     for (int spin = 0; pend; ++spin) {
         if (spin >= kSpinLimit || ((spin & 1023) == 1023 && get_err(ctl))) {
-            set_err(ctl, kErrTimeout);
+            if (!get_err(ctl)) set_err(ctl, kErrTimeout);  // the first failure's code stays
             break;
         }
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(SLEEP);
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             if (pend & (1u << i)) {
@@ -129,7 +129,7 @@ __device__ __forceinline__ void gather(u64* pa, int na, uint32_t ea, float* da, 
 }
 
 // gather() of words base[idx(j)], j < n, of epoch e into d[j] (LDS).
-template <int NA, class Idx>
+template <int NA, class Idx, int SLEEP = 1>
 __device__ __forceinline__ void gather_idx(u64* base, Idx&& idx, int n, uint32_t e, float* d, Ctl* ctl) {
     const int tid = threadIdx.x;
     u64 w[NA];
@@ -149,10 +149,10 @@ __device__ __forceinline__ void gather_idx(u64* base, Idx&& idx, int n, uint32_t
     }
     for (int spin = 0; pend; ++spin) {
         if (spin >= kSpinLimit || ((spin & 1023) == 1023 && get_err(ctl))) {
-            set_err(ctl, kErrTimeout);
+            if (!get_err(ctl)) set_err(ctl, kErrTimeout);  // the first failure's code stays
             break;
         }
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(SLEEP);
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             if (pend & (1u << i)) {
@@ -430,8 +430,6 @@ __device__ __forceinline__ void attn_span(const A& a, const Ly& ly, int g, int p
         rc[k] = cs[j];
         rs[k] = sn[j];
     }
-#ifdef TF_STEP_PROBE
-#endif
     fetch();
     // RoPE (rope_one, with the reference build's contractions)
 #pragma unroll
