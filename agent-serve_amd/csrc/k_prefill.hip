@@ -1,12 +1,12 @@
 // Prefill of prompt tokens on the matrix cores: Model::prefill and layer_prefill
 // (model.cpp:144-195) for a chunk of M tokens at once.
 //
-// k_pf_pack_q8   a Q8_0 matrix's integers as fp16 in MFMA fragment order, once per matrix
 // k_pf_split     rmsnorm (layers.cpp:7-12) of each row, or the row as it is, scaled by
 //                a power of two and written as fp16 hi + lo in fragment order (the A operand)
-// k_pf_gemm_q8   matmul (matmul.cpp:64-73) of Q8_0 weights on v_mfma_f32_16x16x32_f16,
-//                epilogues: store (+ F32 bias, model.cpp:85-89), residual add
-//                (add_inplace, layers.cpp:21-23), silu(gate) * up (layers.cpp:14-19)
+// k_pf_gemm_tile / k_pf_gemm_big   matmul (matmul.cpp:64-73) of Q8_0, Q4_0, Q4_1 or F16
+//                weights, read in their HBM layout, on v_mfma_f32_16x16x32_f16; epilogues:
+//                store (+ F32 bias, model.cpp:85-89), residual add (add_inplace,
+//                layers.cpp:21-23), silu(gate) * up (layers.cpp:14-19)
 // k_pf_rope_store apply_rope_many of q and k (attention.cpp:48-53) and KVCache::store
 //                (kvcache.cpp:31-36) of every row
 // k_pf_reduce    the slices of a GEMM with K split, added in slice order, + its epilogue;
@@ -17,13 +17,14 @@
 // k_pf_attn      causal GQA attention of the chunk (attn_prefill, attention.cpp:82-111)
 //                on v_mfma_f32_16x16x32_f16 with fp16 operand pairs and an online softmax
 //
-// Numerics. A Q8_0 weight q is an integer in [-128, 127] and exact in fp16; a
-// 32-element block's products with the fp16 pair (hi, lo) of an activation are exact
-// in the fp32 accumulator, and hi + lo carries 22 significant bits of the fp32
-// activation (24). Each block's two MFMAs start from zero and the block sum is scaled
-// by its fp16 d in fp32 (quant.cpp:266-321 scales block sums the same way), so the
-// result differs from the fp32 reference by summation order and the 2^-22 split, both
-// far inside the 1e-3 parity bound. Scaling rows by 2^e (max |x| in [2^14, 2^15))
+// Numerics. A Q8_0 weight q is an integer in [-128, 127], a Q4_0 one in [-8, 7], a Q4_1
+// code in [0, 15], all exact in fp16, as is an F16 weight; a 32-element block's products
+// with the fp16 pair (hi, lo) of an activation are exact in the fp32 accumulator, and
+// hi + lo carries 22 significant bits of the fp32 activation (24). Each block's two MFMAs
+// start from zero and the block sum is scaled by its fp16 d in fp32 (quant.cpp:266-321
+// scales block sums the same way; Q4_1 adds m times the block sum of the activations),
+// so the result differs from the fp32 reference by summation order and the 2^-22 split,
+// both far inside the 1e-3 parity bound. Scaling rows by 2^e (max |x| in [2^14, 2^15))
 // keeps hi and lo in fp16 range and off its subnormals; the epilogue multiplies the
 // exact inverse back.
 #include "dev_common.hpp"
@@ -40,10 +41,14 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 // ---------------------------------------------------------------- operands in MFMA fragment order
 //
 // v_mfma_f32_16x16x32_f16 takes from lane l the 8 halves (row l % 16, k = 8 (l / 16) + j)
-// of a 16 x 32 operand tile. Both operands are stored so that one tile is 64 lanes x 16
+// of a 16 x 32 operand tile. The activations are stored so that one tile is 64 lanes x 16
 // bytes, contiguous: a wave fills a fragment with one coalesced 1 KiB load.
 //   activations: xa[row tile][block][hi, lo][lane][8]   (k_pf_split)
-//   weights:     wf[row tile][block][lane][8]            (k_pf_pack_q8, once per matrix)
+// The weights stay where they lie (DevMat streams, no copy): the GEMMs turn the 8 values a
+// lane needs (row l % 16 of a 16-row subtile, elements 8 c .. 8 c + 7 of a 32-element block,
+// c = l / 16) into fp16 as they go. Each format gives the integers of its blocks, exact in
+// fp16, and the block's scale multiplies the block sum afterwards in fp32 (Q4_1's d n + m as
+// d sum x n + m sum x); F16 weights are their own fp16 values with scale 1.
 
 // Eight int8 bytes q -> their fp16 values: with u = q + 128 (the byte with its top bit
 // flipped), 0x64UU is the half 1024 + u, and 1024 + u - 1152 = q exactly.
@@ -59,16 +64,97 @@ __device__ __forceinline__ h8_t q8_to_h8(uint2 w) {
     return __builtin_bit_cast(h8_t, p) - off;
 }
 
-// Q8_0 matrix (DevMat q stream, N x K) -> its integers q as fp16 in fragment order.
-__global__ __launch_bounds__(kBlock) void k_pf_pack_q8(const uint8_t* q, int K, int64_t N, h8_t* wf) {
-    const int nblk = K / 32;
-    const int64_t total = N / 16 * nblk * 64;
-    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
-        const int l = (int)(i & 63);
-        const int64_t tb = i >> 6;
-        const int b = (int)(tb % nblk);
-        const int64_t t = tb / nblk;
-        wf[i] = q8_to_h8(*(const uint2*)(q + (16 * t + (l & 15)) * (int64_t)K + 32 * b + 8 * (l >> 4)));
+// The 4-bit codes n in the low (hi = 0) or high (hi = 1) nibbles of 8 bytes -> fp16 n - OFF
+// (0x640n is the half 1024 + n).
+template <int OFF>
+__device__ __forceinline__ h8_t q4_to_h8(uint2 w, int hi) {
+    const int sh = 4 * hi;
+    const uint32_t a = (w.x >> sh) & 0x0F0F0F0Fu, b = (w.y >> sh) & 0x0F0F0F0Fu;
+    const uint32_t p0 = (a & 0xFFu) | ((a & 0xFF00u) << 8) | 0x64006400u;
+    const uint32_t p1 = ((a >> 16) & 0xFFu) | ((a >> 8) & 0xFF0000u) | 0x64006400u;
+    const uint32_t p2 = (b & 0xFFu) | ((b & 0xFF00u) << 8) | 0x64006400u;
+    const uint32_t p3 = ((b >> 16) & 0xFFu) | ((b >> 8) & 0xFF0000u) | 0x64006400u;
+    const tf_u32x4 p = {p0, p1, p2, p3};
+    constexpr _Float16 o = (_Float16)(1024 + OFF);
+    const h8_t off = {o, o, o, o, o, o, o, o};
+    return __builtin_bit_cast(h8_t, p) - off;
+}
+
+// A layer-matrix format as the GEMMs read it.
+//   kBytes  bytes of one row's 32-element block in the q stream
+//   kSub    LDS bytes of a 16-row subtile's block (k_pf_gemm_big)
+//   kScale  bytes of one row's block in the s stream (0: no scales)
+//   kMin    Q4_1's min term
+//   off(c)  byte offset in a row's block of the piece lane c = l / 16 reads
+//   lds(p, r, c)  that piece of subtile row r from the subtile's LDS block at p
+//   cvt(raw, c)   its 8 values as fp16
+template <int T>
+struct PfW;
+
+// Q8_0 (quant.cpp:66-72): 32 int8 per block. LDS: the 16-byte half h of row r at 16 (16 h + r).
+template <>
+struct PfW<TF_HIP_TYPE_Q8_0> {
+    static constexpr int kBytes = 32, kSub = 512, kScale = 2;
+    static constexpr bool kMin = false;
+    typedef uint2 Raw;
+    __device__ static int off(int c) { return 8 * c; }
+    __device__ static Raw load(const TF_GLOBAL uint8_t* p) { return gload_u2((const void*)p); }
+    __device__ static Raw lds(const unsigned char* p, int r, int c) {
+        return *(const uint2*)(p + 256 * (c >> 1) + 16 * r + 8 * (c & 1));
+    }
+    __device__ static h8_t cvt(Raw w, int) { return q8_to_h8(w); }
+};
+
+// Q4_0 (quant.cpp:74-86): 16 bytes per block, element j in the low nibble of byte j and
+// element j + 16 in its high nibble, value n - 8. LDS: row r's 16 bytes at 16 r.
+template <>
+struct PfW<TF_HIP_TYPE_Q4_0> {
+    static constexpr int kBytes = 16, kSub = 256, kScale = 2;
+    static constexpr bool kMin = false;
+    typedef uint2 Raw;
+    __device__ static int off(int c) { return 8 * (c & 1); }
+    __device__ static Raw load(const TF_GLOBAL uint8_t* p) { return gload_u2((const void*)p); }
+    __device__ static Raw lds(const unsigned char* p, int r, int c) { return *(const uint2*)(p + 16 * r + 8 * (c & 1)); }
+    __device__ static h8_t cvt(Raw w, int c) { return q4_to_h8<8>(w, c >> 1); }
+};
+
+// Q4_1 (quant.cpp:87-99): the Q4_0 layout with value n d + m; the s stream holds d and m.
+template <>
+struct PfW<TF_HIP_TYPE_Q4_1> {
+    static constexpr int kBytes = 16, kSub = 256, kScale = 4;
+    static constexpr bool kMin = true;
+    typedef uint2 Raw;
+    __device__ static int off(int c) { return 8 * (c & 1); }
+    __device__ static Raw load(const TF_GLOBAL uint8_t* p) { return gload_u2((const void*)p); }
+    __device__ static Raw lds(const unsigned char* p, int r, int c) { return *(const uint2*)(p + 16 * r + 8 * (c & 1)); }
+    __device__ static h8_t cvt(Raw w, int c) { return q4_to_h8<0>(w, c >> 1); }
+};
+
+// F16 (quant.cpp:129-131): 64 bytes per block. LDS: the 16-byte piece c of row r at 16 (16 c + r).
+template <>
+struct PfW<TF_HIP_TYPE_F16> {
+    static constexpr int kBytes = 64, kSub = 1024, kScale = 0;
+    static constexpr bool kMin = false;
+    typedef uint4 Raw;
+    __device__ static int off(int c) { return 16 * c; }
+    __device__ static Raw load(const TF_GLOBAL uint8_t* p) { return gload_u4((const void*)p); }
+    __device__ static Raw lds(const unsigned char* p, int r, int c) { return *(const uint4*)(p + 256 * c + 16 * r); }
+    __device__ static h8_t cvt(Raw w, int) { return __builtin_bit_cast(h8_t, w); }
+};
+
+// Block blk's scale d and min m from a scale word: a pair of fp16 d (blocks 2 p, 2 p + 1)
+// for kScale 2, d | m << 16 of block blk for kScale 4, none for kScale 0.
+template <int KS>
+__device__ __forceinline__ void pf_scale(uint32_t word, int blk, float& d, float& m) {
+    if (KS == 2) {
+        d = h2f(word >> (16 * (blk & 1)));
+        m = 0.0f;
+    } else if (KS == 4) {
+        d = h2f(word & 0xFFFFu);
+        m = h2f(word >> 16);
+    } else {
+        d = 1.0f;
+        m = 0.0f;
     }
 }
 
@@ -192,7 +278,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
     split_emit<NG, WPR>(v, tid, m, K, w, eps, xa, rs, red_d, red_f);
 }
 
-// ---------------------------------------------------------------- Q8_0 GEMM
+// ---------------------------------------------------------------- GEMM
 
 // Field of the segment holding output subtile u (uniform per wave: scalar selects).
 #define PF_SEL(s, f) ((s) == 0 ? a.seg[0].f : ((s) == 1 ? a.seg[1].f : a.seg[2].f))
@@ -201,11 +287,13 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
 // of 16 (GEMV_SILU: NI / 2 output subtiles, each a gate and an up subtile). Per 32-element
 // block: for each (row subtile, column subtile) an MFMA of the hi part from zero, then
 // one of the lo part on top (issued after all eight hi MFMAs, so no MFMA waits on the
-// one before it), then acc += d * block sum. Fragments stream from L2 into registers,
-// one stage of two blocks ahead; every load is unconditional (indices clamped) so the
-// compiler waits only for the stage it consumes.
-template <int MODE, int NI>
-__global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
+// one before it), then acc += d * block sum (Q4_1: + m * the rows' block sums, from the
+// same two MFMAs against a fragment of ones). Weight bytes and activation fragments stream
+// from L2 into registers, one stage of two blocks ahead; every load is unconditional
+// (indices clamped) so the compiler waits only for the stage it consumes.
+template <int MODE, int NI, int T>
+__global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
+    using W = PfW<T>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous range
     // of tiles, rows fastest, so the row tiles that share a weight tile share an L2.
@@ -219,11 +307,12 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
     const int m0 = mt * kPfTileM + (wave & 1) * 32;
     const int wid = nt * 2 + (wave >> 1);
     const int K = a.K, nblk = K / 32;
-    const int l16 = lane & 15;
+    const int l16 = lane & 15, lc = lane >> 4;
 
     constexpr int NO = MODE == GEMV_SILU ? NI / 2 : NI;  // output subtiles per wave
-    const TF_GLOBAL h8_t* bp[NI];
-    const uint16_t* sp[NI];
+    constexpr int SW = W::kScale == 4 ? 2 : 1;           // scale words per stage and column
+    const TF_GLOBAL uint8_t* bp[NI];
+    const TF_GLOBAL uint32_t* sp[NI];
     float* yp[NI];
     const float* bsp[NI];
     int64_t ldy[NI];
@@ -238,10 +327,10 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
         const int tile = u - PF_SEL(s, sub0);
         const int c = tile * 16 + l16;
         const bool up = MODE == GEMV_SILU && ni >= NO;
-        const uint16_t* wf = up ? PF_SEL(s, wf2) : PF_SEL(s, wf);
+        const uint8_t* wq = up ? PF_SEL(s, w2.q) : PF_SEL(s, w.q);
         const uint8_t* ws = up ? PF_SEL(s, w2.s) : PF_SEL(s, w.s);
-        bp[ni] = (const TF_GLOBAL h8_t*)wf + (int64_t)tile * nblk * 64 + lane;
-        sp[ni] = (const uint16_t*)ws + (int64_t)c * nblk;
+        bp[ni] = (const TF_GLOBAL uint8_t*)wq + (int64_t)c * nblk * W::kBytes + W::off(lc);
+        sp[ni] = (const TF_GLOBAL uint32_t*)(ws + (int64_t)c * nblk * W::kScale);
         yp[ni] = PF_SEL(s, y);
         bsp[ni] = PF_SEL(s, bias);
         ldy[ni] = PF_SEL(s, ldy);
@@ -258,9 +347,9 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
         for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
 
     struct Stage {
-        h8_t ah[2][2], al[2][2];  // [row subtile][block]
-        h8_t bh[NI][2];           // [column subtile][block]
-        uint32_t d[NI];           // the two blocks' fp16 scales
+        h8_t ah[2][2], al[2][2];         // [row subtile][block]
+        typename W::Raw bw[NI][2];       // [column subtile][block]: the lane's weight bytes
+        uint32_t d[NI][SW];              // the scale words of the stage's two blocks
     };
     const int S = K / 64;
     auto load = [&](int s, Stage& g) {
@@ -274,33 +363,49 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
                 g.al[mi][j] = ap[mi][blk * 128 + 64];
             }
 #pragma unroll
-            for (int ni = 0; ni < NI; ++ni) g.bh[ni][j] = bp[ni][blk * 64];
+            for (int ni = 0; ni < NI; ++ni) g.bw[ni][j] = W::load(bp[ni] + (int64_t)blk * W::kBytes);
         }
+        if (W::kScale)
 #pragma unroll
-        for (int ni = 0; ni < NI; ++ni) g.d[ni] = *(const TF_GLOBAL uint32_t*)(sp[ni] + 2 * s);
+            for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+                for (int w = 0; w < SW; ++w) g.d[ni][w] = sp[ni][SW * s + w];
     };
+    const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
     auto compute = [&](const Stage& g) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            f4_t t[2][NI];
+            h8_t bh[NI];
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+            for (int ni = 0; ni < NI; ++ni) bh[ni] = W::cvt(g.bw[ni][j], lc);
+            f4_t t[2][NI], ts[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni)
-                    t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], g.bh[ni][j],
+                    t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], bh[ni],
                                                                       (f4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                if (W::kMin)
+                    ts[mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], ones, (f4_t){0.0f, 0.0f, 0.0f, 0.0f},
+                                                                    0, 0, 0);
+            }
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+            for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni)
-                    t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], g.bh[ni][j], t[mi][ni], 0, 0, 0);
+                    t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], bh[ni], t[mi][ni], 0, 0, 0);
+                if (W::kMin) ts[mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], ones, ts[mi], 0, 0, 0);
+            }
 #pragma unroll
             for (int ni = 0; ni < NI; ++ni) {
-                const float dv = h2f(g.d[ni] >> (16 * j));
+                float dv, mv;
+                pf_scale<W::kScale>(g.d[ni][SW == 2 ? j : 0], j, dv, mv);
 #pragma unroll
                 for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[mi][ni][r] = fmaf(dv, t[mi][ni][r], acc[mi][ni][r]);
+                    for (int r = 0; r < 4; ++r)
+                        acc[mi][ni][r] = W::kMin ? fmaf(dv, t[mi][ni][r], fmaf(mv, ts[mi][r], acc[mi][ni][r]))
+                                                 : fmaf(dv, t[mi][ni][r], acc[mi][ni][r]);
             }
         }
     };
@@ -356,23 +461,28 @@ __global__ __launch_bounds__(256) void k_pf_gemm_q8(const PfGemmArgs a) {
 // (2 rows x 4 columns of waves) owns 128 rows x 16 weight-column subtiles (256 weight rows;
 // GEMV_SILU: 8 gate and the 8 matching up subtiles, 128 output columns). A stage (one
 // 32-element block) of both operands and the scales goes straight from global memory into
-// one of four LDS buffers, five loads per wave, three stages ahead of its use; each wave
-// then runs 4 x 4 tiles of 16 x 16, reading its fragments from LDS (4 waves of 4 x 8 tiles,
-// a third fewer LDS reads per MFMA, measured 12% slower: one wave per SIMD leaves the
-// MFMA-to-scale dependencies exposed). The per-block arithmetic and its order are those of
-// k_pf_gemm_q8, so the two give the same bits.
+// one of four LDS buffers, four loads per wave, three stages ahead of its use: the 16
+// activation fragments (1 KiB each), the 256 weight rows' bytes of the block in the
+// format's subtile layout, and their scale words. Each wave then runs 4 x 4 tiles of
+// 16 x 16, reading activation fragments and weight bytes from LDS and turning the bytes
+// into fp16 in registers (4 waves of 4 x 8 tiles, a third fewer LDS reads per MFMA,
+// measured 12% slower: one wave per SIMD leaves the MFMA-to-scale dependencies exposed).
+// The per-block arithmetic and its order are those of k_pf_gemm_tile, so the two give the
+// same bits.
 constexpr int kBigThreads = 512;
 constexpr int kBigWaves = kBigThreads / 64;
 constexpr int kBigRows = 128;
-constexpr int kBigFragBytes = 32 * 1024;                 // 16 A fragments (8 row tiles, hi and lo) + 16 B fragments
-constexpr int kBigStageBytes = kBigFragBytes + 256 * 4;  // + the fp16 scale pairs of the 256 weight columns
-constexpr int kBigStages = 4;                            // LDS buffers: one in use, three loading
+constexpr int kBigABytes = 16 * 1024;                           // 16 activation fragments (8 row tiles, hi and lo)
+constexpr int kBigBBytes = 16 * 1024;                           // 256 weight rows x 64 bytes at most (F16)
+constexpr int kBigStageBytes = kBigABytes + kBigBBytes + 1024;  // + a scale word per weight row
+constexpr int kBigStages = 4;                                   // LDS buffers: one in use, three loading
 constexpr size_t kBigLdsBytes = kBigStages * (size_t)kBigStageBytes;
 
 // SPLIT: the grid also splits K into a.ks slices; slice ks writes its row-scaled partial
 // sums to a.part[ks][row][output column] and k_pf_reduce applies the epilogue.
-template <int MODE, bool SPLIT>
+template <int MODE, bool SPLIT, int T>
 __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a) {
+    using W = PfW<T>;
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int b = blockIdx.x;
@@ -387,7 +497,7 @@ __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a)
     const int K = a.K, nblk = K / 32;
     const int S = SPLIT ? nblk / a.ks : nblk;  // stages (blocks) of this slice
     const int s0 = kslice * S;                 // its first block
-    const int l16 = lane & 15;
+    const int l16 = lane & 15, lc = lane >> 4;
     constexpr bool SILU = MODE == GEMV_SILU;
 
     // weight-column subtile q (0..15) of this workgroup: output subtile, matrix, tile row
@@ -397,49 +507,73 @@ __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a)
         u = u < a.n_sub ? u : a.n_sub - 1;
         seg = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
     };
-    // this wave's 4 fragments per stage, f = wave + 8 i: f < 16 the A fragment (row tile f / 2,
-    // hi or lo), else the B fragment of weight-column subtile f - 16; one block per stage
-    const TF_GLOBAL h8_t* src[4];
-    int step[4];  // h8 per block
+    // row r of weight-column subtile q, at byte off of each block
+    auto wrow = [&](int q, int r, int off) {
+        int u, seg;
+        bool up;
+        resolve(q, u, seg, up);
+        const uint8_t* wq = up ? PF_SEL(seg, w2.q) : PF_SEL(seg, w.q);
+        return (const TF_GLOBAL uint8_t*)wq + ((int64_t)(u - PF_SEL(seg, sub0)) * 16 + r) * nblk * W::kBytes + off;
+    };
+    // this wave's loads per stage: activation fragments f = wave + 8 i (row tile f / 2, hi
+    // or lo); weight bytes of subtiles 2 wave, 2 wave + 1 (lane i writes LDS byte 16 i of
+    // the wave's part): Q8_0 one 1 KiB load (lane i: half i / 16 % 2 of row i % 16 of
+    // subtile 2 wave + i / 32), Q4 one 512-byte load of lanes 0..31 (row i % 16 of subtile
+    // 2 wave + i / 16), F16 a 1 KiB load per subtile (piece i / 16 of row i % 16)
+    const TF_GLOBAL h8_t* asrc[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
         const int f = wave + kBigWaves * i;
-        if (i < 2) {
-            src[i] = (const TF_GLOBAL h8_t*)a.xa + (int64_t)(mt * 8 + f / 2) * nblk * 128 + (f % 2) * 64 + lane;
-            step[i] = 128;
-        } else {
-            int u, seg;
-            bool up;
-            resolve(f - 16, u, seg, up);
-            const int tile = u - PF_SEL(seg, sub0);
-            const uint16_t* wf = up ? PF_SEL(seg, wf2) : PF_SEL(seg, wf);
-            src[i] = (const TF_GLOBAL h8_t*)wf + (int64_t)tile * nblk * 64 + lane;
-            step[i] = 64;
-        }
+        asrc[i] = (const TF_GLOBAL h8_t*)a.xa + (int64_t)(mt * 8 + f / 2) * nblk * 128 + (f % 2) * 64 + lane;
     }
-    // the scales: lane i < 32 of wave w loads the fp16 pair (blocks 2p, 2p + 1) of weight
-    // column 32 w + i
-    const TF_GLOBAL uint32_t* dsrc;
-    {
+    constexpr int NB = W::kSub == 1024 ? 2 : 1;  // weight loads per wave and stage
+    const TF_GLOBAL uint8_t* bsrc[NB];
+    if (W::kSub == 512) {
+        bsrc[0] = wrow(2 * wave + (lane >> 5), l16, 16 * (lc & 1));
+    } else if (W::kSub == 256) {
+        bsrc[0] = wrow(2 * wave + (lc & 1), l16, 0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) bsrc[j] = wrow(2 * wave + j, l16, 16 * lc);
+    }
+    // the scales: lane i < 32 of wave w loads the scale word of weight column 32 w + i
+    // (Q8_0 / Q4_0: the fp16 pair of blocks 2 p, 2 p + 1; Q4_1: d and m of the block)
+    const TF_GLOBAL uint32_t* dsrc = nullptr;
+    if (W::kScale) {
         const int j = 32 * wave + (lane & 31), q = j / 16;
         int u, seg;
         bool up;
         resolve(q, u, seg, up);
         const int c = (u - PF_SEL(seg, sub0)) * 16 + (j & 15);
         const uint8_t* ws = up ? PF_SEL(seg, w2.s) : PF_SEL(seg, w.s);
-        dsrc = (const TF_GLOBAL uint32_t*)((const uint16_t*)ws + (int64_t)c * nblk);
+        dsrc = (const TF_GLOBAL uint32_t*)(ws + (int64_t)c * nblk * W::kScale);
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
-    auto issue = [&](int s) {  // stage s into buffer s % 4: 5 loads per wave
+    auto issue = [&](int s) {  // stage s into buffer s % 4: 4 loads per wave
         const int blk = s0 + s;
         const uint32_t base = lds0 + (uint32_t)((s % kBigStages) * kBigStageBytes);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            lds_dma16(src[i] + (int64_t)blk * step[i],
+        for (int i = 0; i < 2; ++i)
+            lds_dma16(asrc[i] + (int64_t)blk * 128,
                       __builtin_amdgcn_readfirstlane(base + (uint32_t)((wave + kBigWaves * i) * 1024)));
-        const uint32_t m0 = __builtin_amdgcn_readfirstlane(base + (uint32_t)(kBigFragBytes + 128 * wave));
-        if (lane < 32) lds_dma4(dsrc + blk / 2, m0);
+        const uint32_t bb = base + kBigABytes;
+        if (W::kSub == 512) {
+            lds_dma16(bsrc[0] + (int64_t)blk * W::kBytes, __builtin_amdgcn_readfirstlane(bb + 1024u * wave));
+        } else if (W::kSub == 256) {
+            const uint32_t m0 = __builtin_amdgcn_readfirstlane(bb + 512u * wave);
+            if (lane < 32) lds_dma16(bsrc[0] + (int64_t)blk * W::kBytes, m0);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                lds_dma16(bsrc[j] + (int64_t)blk * W::kBytes, __builtin_amdgcn_readfirstlane(bb + 1024u * (2 * wave + j)));
+        }
+        if (W::kScale) {
+            const uint32_t m0 = __builtin_amdgcn_readfirstlane(base + (uint32_t)(kBigABytes + kBigBBytes + 128 * wave));
+            if (lane < 32) lds_dma4(dsrc + (W::kScale == 2 ? blk / 2 : blk), m0);
+        }
     };
+    constexpr int kLoads = 2 + NB + (W::kScale ? 1 : 0);
+    static_assert(kLoads == 4, "the waits below count 4 loads per stage");
 
     const int wm = wave & 1, wn = wave >> 1;
     int qb[4];  // this wave's weight-column subtiles
@@ -456,53 +590,68 @@ __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a)
     // MFMAs are issued (the last half of a block after the first of the next block), so the
     // scaling never waits on MFMAs just issued. Same operations, same order per acc.
     f4_t tp[2][4];  // pending block sums: rows half 1 of the previous block
-    float dvp[4];
-    auto scale_in = [&](int half, const f4_t (&t)[2][4], const float (&dv)[4]) {
+    f4_t tsp[2];    // Q4_1: their rows' block sums
+    float dvp[4], mvp[4];
+    auto scale_in = [&](int half, const f4_t (&t)[2][4], const f4_t (&ts)[2], const float (&dv)[4],
+                        const float (&mv)[4]) {
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
             for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    acc[half * 2 + mm][ni][r] = fmaf(dv[ni], t[mm][ni][r], acc[half * 2 + mm][ni][r]);
+                for (int r = 0; r < 4; ++r) {
+                    const float o = acc[half * 2 + mm][ni][r];
+                    acc[half * 2 + mm][ni][r] =
+                        W::kMin ? fmaf(dv[ni], t[mm][ni][r], fmaf(mv[ni], ts[mm][r], o)) : fmaf(dv[ni], t[mm][ni][r], o);
+                }
     };
+    const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
     auto compute = [&](int buf, int blk, bool pending) {
         const h8_t* st = (const h8_t*)(lds + buf * kBigStageBytes);
-        const uint32_t* sd = (const uint32_t*)(lds + buf * kBigStageBytes + kBigFragBytes);
-        float dv[4];
+        const unsigned char* sb = lds + buf * kBigStageBytes + kBigABytes;
+        const uint32_t* sd = (const uint32_t*)(lds + buf * kBigStageBytes + kBigABytes + kBigBBytes);
+        float dv[4], mv[4];
         h8_t bh[4];
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
-            dv[ni] = h2f(sd[qb[ni] * 16 + l16] >> (16 * (blk & 1)));
-            bh[ni] = st[(16 + qb[ni]) * 64 + lane];
+            pf_scale<W::kScale>(W::kScale ? sd[qb[ni] * 16 + l16] : 0u, blk, dv[ni], mv[ni]);
+            bh[ni] = W::cvt(W::lds(sb + qb[ni] * W::kSub, l16, lc), lc);
         }
-        auto mfmas = [&](int half, f4_t (&t)[2][4]) {
+        auto mfmas = [&](int half, f4_t (&t)[2][4], f4_t (&ts)[2]) {
             h8_t ah[2], al[2];
 #pragma unroll
             for (int mm = 0; mm < 2; ++mm) {
-                const int T = wm * 4 + half * 2 + mm;
-                ah[mm] = st[(T * 2 + 0) * 64 + lane];
-                al[mm] = st[(T * 2 + 1) * 64 + lane];
+                const int T2 = wm * 4 + half * 2 + mm;
+                ah[mm] = st[(T2 * 2 + 0) * 64 + lane];
+                al[mm] = st[(T2 * 2 + 1) * 64 + lane];
             }
 #pragma unroll
-            for (int mm = 0; mm < 2; ++mm)
+            for (int mm = 0; mm < 2; ++mm) {
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni)
                     t[mm][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mm], bh[ni], (f4_t){0.0f, 0.0f, 0.0f, 0.0f},
                                                                       0, 0, 0);
+                if (W::kMin)
+                    ts[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mm], ones, (f4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            }
 #pragma unroll
-            for (int mm = 0; mm < 2; ++mm)
+            for (int mm = 0; mm < 2; ++mm) {
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni)
                     t[mm][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mm], bh[ni], t[mm][ni], 0, 0, 0);
+                if (W::kMin) ts[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mm], ones, ts[mm], 0, 0, 0);
+            }
         };
-        f4_t t0[2][4];
-        mfmas(0, t0);
-        if (pending) scale_in(1, tp, dvp);
-        mfmas(1, tp);
-        scale_in(0, t0, dv);
+        f4_t t0[2][4], ts0[2];
+        mfmas(0, t0, ts0);
+        if (pending) scale_in(1, tp, tsp, dvp, mvp);
+        mfmas(1, tp, tsp);
+        scale_in(0, t0, ts0, dv, mv);
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) dvp[ni] = dv[ni];
+        for (int ni = 0; ni < 4; ++ni) {
+            dvp[ni] = dv[ni];
+            mvp[ni] = mv[ni];
+        }
     };
 
     const int pre = S < kBigStages - 1 ? S : kBigStages - 1;
@@ -513,15 +662,15 @@ __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a)
         // wave has left compute(s - 1), whose buffer stage s + 3 takes
         const int after = S - 1 - s;
         if (after >= 2)
-            asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         else if (after == 1)
-            asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         else
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (s + kBigStages - 1 < S) issue(s + kBigStages - 1);
         compute(s % kBigStages, s0 + s, s > 0);
     }
-    if (S > 0) scale_in(1, tp, dvp);
+    if (S > 0) scale_in(1, tp, tsp, dvp, mvp);
 
     // epilogue: lane holds rows 16 T + 4 (lane / 16) + r of weight column 16 q + l16
 #pragma unroll
@@ -1099,7 +1248,9 @@ __global__ __launch_bounds__(kBlock) void k_pf_tail(Ctl* ctl, int pos_last, cons
 }  // namespace
 
 bool pf_gemm_supported(int type, int64_t K, int64_t N) {
-    return type == TF_HIP_TYPE_Q8_0 && K % 64 == 0 && N % 16 == 0 && K <= kBlock * 8 * kSplitGroups;
+    const bool fmt = type == TF_HIP_TYPE_Q8_0 || type == TF_HIP_TYPE_Q4_0 || type == TF_HIP_TYPE_Q4_1 ||
+                     type == TF_HIP_TYPE_F16;
+    return fmt && K % 64 == 0 && N % 16 == 0 && K <= kBlock * 8 * kSplitGroups;
 }
 
 hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,
@@ -1125,30 +1276,11 @@ hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, flo
     return hipGetLastError();
 }
 
-hipError_t launch_pf_pack_q8(const DevMat& m, uint16_t* wf, hipStream_t st) {
-    if (m.type != TF_HIP_TYPE_Q8_0 || m.K % 32 != 0 || m.N % 16 != 0) return hipErrorInvalidValue;
-    const int64_t total = m.N / 16 * (m.K / 32) * 64;
-    int64_t blocks = (total + kBlock - 1) / kBlock;
-    blocks = blocks < 4096 ? blocks : 4096;
-    hipLaunchKernelGGL(k_pf_pack_q8, dim3((unsigned)blocks), dim3(kBlock), 0, st, m.q, (int)m.K, m.N, (h8_t*)wf);
-    return hipGetLastError();
-}
+namespace {
 
-hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused) {
-    if (fused) *fused = false;
-    if (a.K % 64 != 0 || a.Mpad % kPfTileM != 0 || a.M > a.Mpad || a.M <= 0 || a.n_sub <= 0 || a.n_seg < 1 ||
-        a.n_seg > 3)
-        return hipErrorInvalidValue;
-    for (int s = 0; s < a.n_seg; ++s) {
-        const PfSeg& g = a.seg[s];
-        if (g.w.type != TF_HIP_TYPE_Q8_0 || g.w.K != a.K || g.w.N % 16 != 0 || !g.y || !g.wf)
-            return hipErrorInvalidValue;
-        const int next = s + 1 < a.n_seg ? a.seg[s + 1].sub0 : a.n_sub;
-        if (next - g.sub0 != g.w.N / 16) return hipErrorInvalidValue;
-        if (a.mode == GEMV_SILU && (g.w2.type != TF_HIP_TYPE_Q8_0 || g.w2.K != a.K || g.w2.N != g.w.N || !g.wf2))
-            return hipErrorInvalidValue;
-    }
-    if (a.seg[0].sub0 != 0 || (a.mode == GEMV_SILU && a.n_seg != 1)) return hipErrorInvalidValue;
+// The launch of launch_pf_gemm for weights of format T (arguments checked).
+template <int T>
+hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
     // large tiles when they give every CU a workgroup, directly or with K split in slices
     if (a.Mpad % kBigRows == 0) {
         const int per_big = a.mode == GEMV_SILU ? 8 : 16;  // output subtiles per large tile
@@ -1173,12 +1305,12 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused) {
         }
         if (n_big >= cus || ks > 1) {
             static bool attr_set[6] = {false, false, false, false, false, false};
-            const void* fns[6] = {(const void*)k_pf_gemm_big<GEMV_STORE, false>,
-                                  (const void*)k_pf_gemm_big<GEMV_RESID, false>,
-                                  (const void*)k_pf_gemm_big<GEMV_SILU, false>,
-                                  (const void*)k_pf_gemm_big<GEMV_STORE, true>,
-                                  (const void*)k_pf_gemm_big<GEMV_RESID, true>,
-                                  (const void*)k_pf_gemm_big<GEMV_SILU, true>};
+            const void* fns[6] = {(const void*)k_pf_gemm_big<GEMV_STORE, false, T>,
+                                  (const void*)k_pf_gemm_big<GEMV_RESID, false, T>,
+                                  (const void*)k_pf_gemm_big<GEMV_SILU, false, T>,
+                                  (const void*)k_pf_gemm_big<GEMV_STORE, true, T>,
+                                  (const void*)k_pf_gemm_big<GEMV_RESID, true, T>,
+                                  (const void*)k_pf_gemm_big<GEMV_SILU, true, T>};
             const int fi = a.mode + (ks > 1 ? 3 : 0);
             if (!attr_set[fi]) {
                 const hipError_t e =
@@ -1190,11 +1322,11 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused) {
             b.ks = ks;
             const dim3 grid((unsigned)(n_big * ks));
             switch (fi) {
-                case 0: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_STORE, false>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
-                case 1: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_RESID, false>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
-                case 2: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_SILU, false>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
-                case 3: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_STORE, true>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
-                default: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_RESID, true>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                case 0: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_STORE, false, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                case 1: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_RESID, false, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                case 2: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_SILU, false, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                case 3: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_STORE, true, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                default: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_RESID, true, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
             }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess || ks == 1) return e;
@@ -1265,7 +1397,7 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused) {
     const int ni = wg4 >= 2 * device_cu_count() ? 4 : 2;
     const int per_wg = 2 * (a.mode == GEMV_SILU ? ni / 2 : ni);  // output subtiles per workgroup column
     const dim3 grid((unsigned)((a.n_sub + per_wg - 1) / per_wg * mt));
-#define PF_LAUNCH(MODE, NI) hipLaunchKernelGGL((k_pf_gemm_q8<MODE, NI>), grid, dim3(256), 0, st, a)
+#define PF_LAUNCH(MODE, NI) hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T>), grid, dim3(256), 0, st, a)
     switch (a.mode * 8 + ni) {
         case GEMV_STORE * 8 + 4: PF_LAUNCH(GEMV_STORE, 4); break;
         case GEMV_STORE * 8 + 2: PF_LAUNCH(GEMV_STORE, 2); break;
@@ -1277,6 +1409,33 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused) {
     }
 #undef PF_LAUNCH
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused) {
+    if (fused) *fused = false;
+    if (a.K % 64 != 0 || a.Mpad % kPfTileM != 0 || a.M > a.Mpad || a.M <= 0 || a.n_sub <= 0 || a.n_seg < 1 ||
+        a.n_seg > 3)
+        return hipErrorInvalidValue;
+    // one format for every matrix of the launch
+    const int t = a.seg[0].w.type;
+    for (int s = 0; s < a.n_seg; ++s) {
+        const PfSeg& g = a.seg[s];
+        if (!pf_gemm_supported(g.w.type, g.w.K, g.w.N) || g.w.type != t || g.w.K != a.K || !g.y)
+            return hipErrorInvalidValue;
+        const int next = s + 1 < a.n_seg ? a.seg[s + 1].sub0 : a.n_sub;
+        if (next - g.sub0 != g.w.N / 16) return hipErrorInvalidValue;
+        if (a.mode == GEMV_SILU && (g.w2.type != t || g.w2.K != a.K || g.w2.N != g.w.N)) return hipErrorInvalidValue;
+    }
+    if (a.seg[0].sub0 != 0 || (a.mode == GEMV_SILU && a.n_seg != 1)) return hipErrorInvalidValue;
+    switch (t) {
+        case TF_HIP_TYPE_Q8_0: return launch_gemm_t<TF_HIP_TYPE_Q8_0>(a, st, fused);
+        case TF_HIP_TYPE_Q4_0: return launch_gemm_t<TF_HIP_TYPE_Q4_0>(a, st, fused);
+        case TF_HIP_TYPE_Q4_1: return launch_gemm_t<TF_HIP_TYPE_Q4_1>(a, st, fused);
+        case TF_HIP_TYPE_F16: return launch_gemm_t<TF_HIP_TYPE_F16>(a, st, fused);
+    }
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_pf_rope_store(float* qkv, int64_t ld, int n, int H, int G, int hd, const float* rope_cos,

@@ -101,7 +101,6 @@ struct tf_hip_ctx {
     size_t ppart_floats = 0;
     void* pattn_ws = nullptr;           // packed key/value tiles of prefill attention
     size_t pattn_ws_bytes = 0;
-    std::vector<uint16_t*> pf_wf;       // per slot: the matrix's integers as fp16 fragments
     std::string err;
 };
 
@@ -762,6 +761,8 @@ int ensure_pf(tf_hip_ctx* c) {
                               TF_HIP_LAYER_GATE, TF_HIP_LAYER_UP, TF_HIP_LAYER_DOWN};
         for (int k : kinds)
             if (!pf_gemm_supported(M(k).type, M(k).K, M(k).N)) return 0;
+        // gate and up run in one launch, which takes one format
+        if (M(TF_HIP_LAYER_GATE).type != M(TF_HIP_LAYER_UP).type) return 0;
     }
     if (!pf_attn_supported(p.head_dim, p.n_head / p.n_kv_head)) return 0;
     if (!c->px) {
@@ -780,19 +781,6 @@ int ensure_pf(tf_hip_ctx* c) {
         if ((rc = dalloc(c, &c->pattn_ws, c->pattn_ws_bytes))) return rc;
         c->pf_cap = cap;
     }
-    // every layer matrix's integers as fp16 fragments (2 bytes per weight, kept for the
-    // context's life; a re-uploaded matrix is packed again)
-    c->pf_wf.assign(c->mats.size(), nullptr);
-    for (int l = 0; l < p.n_layer; ++l)
-        for (int k : {TF_HIP_LAYER_Q, TF_HIP_LAYER_K, TF_HIP_LAYER_V, TF_HIP_LAYER_O, TF_HIP_LAYER_GATE, TF_HIP_LAYER_UP,
-                      TF_HIP_LAYER_DOWN}) {
-            const int slot = TF_HIP_SLOT_LAYER(l, k);
-            const DevMat& m = mat(c, slot);
-            uint16_t* wf = nullptr;
-            if ((rc = dalloc(c, &wf, (size_t)m.N * m.K * 2))) return rc;
-            HIPCHK(c, launch_pf_pack_q8(m, wf, c->st));
-            c->pf_wf[(size_t)slot] = wf;
-        }
     HIPCHK(c, hipStreamSynchronize(c->st));
     c->pf_state = 1;
     return 1;
@@ -832,7 +820,6 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
             PfSeg& s = a.seg[a.n_seg++];
             const DevMat& w = mat(c, slot);
             s.w = w;
-            s.wf = c->pf_wf[(size_t)slot];
             s.y = y;
             s.ldy = ldy;
             s.bias = bias;
@@ -857,7 +844,21 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                 chk(launch_pf_split(c->px, D, V(TF_HIP_LAYER_ATTN_NORM), p.rms_eps, D, nc, Mpad, c->pxa, c->prs,
                                     c->st));
             x_split = false;
-            {
+            const int tq = mat(c, M(TF_HIP_LAYER_Q)).type;
+            if (mat(c, M(TF_HIP_LAYER_K)).type != tq || mat(c, M(TF_HIP_LAYER_V)).type != tq) {
+                // q, k and v in different formats: a launch each, then rope and the cache
+                const int kinds[3] = {TF_HIP_LAYER_Q, TF_HIP_LAYER_K, TF_HIP_LAYER_V};
+                const int bias[3] = {TF_HIP_LAYER_BQ, TF_HIP_LAYER_BK, TF_HIP_LAYER_BV};
+                const int off[3] = {0, Hd, Hd + KVd};
+                for (int i = 0; i < 3; ++i) {
+                    PfGemmArgs a = base(D);
+                    a.mode = GEMV_STORE;
+                    seg(a, M(kinds[i]), c->pqkv + off[i], NQ, V(bias[i]));
+                    chk(launch_pf_gemm(a, c->st));
+                }
+                chk(launch_pf_rope_store(c->pqkv, NQ, nc, p.n_head, p.n_kv_head, p.head_dim, c->rope_cos, c->rope_sin,
+                                         pos0, kc, vc, p.kv_layout, p.max_seq, c->st));
+            } else {
                 PfGemmArgs a = base(D);
                 a.mode = GEMV_STORE;
                 seg(a, M(TF_HIP_LAYER_Q), c->pqkv, NQ, V(TF_HIP_LAYER_BQ));
@@ -898,7 +899,6 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                 a.mode = GEMV_SILU;
                 seg(a, M(TF_HIP_LAYER_GATE), c->ph, F, nullptr);
                 a.seg[0].w2 = mat(c, M(TF_HIP_LAYER_UP));
-                a.seg[0].wf2 = c->pf_wf[(size_t)M(TF_HIP_LAYER_UP)];
                 chk(launch_pf_gemm(a, c->st));
             }
             chk(launch_pf_split(c->ph, F, nullptr, 0.0f, F, nc, Mpad, c->pxa, c->prs, c->st));
@@ -1482,12 +1482,10 @@ int tf_hip_matmul(int device, int t, const void* w, int64_t ne0, int64_t ne1, co
     if (n_rows_x >= 2 && pf_gemm_supported(t, ne0, ne1)) {
         // several rows: the prefill GEMM on the matrix cores
         const int Mpad = (n_rows_x + kPfTileM - 1) / kPfTileM * kPfTileM;
-        uint16_t *xa, *wf;
+        uint16_t* xa;
         float* rs;
         OPCHK(s.alloc(&xa, (size_t)Mpad * ne0 * 2 * 2));
-        OPCHK(s.alloc(&wf, (size_t)ne1 * ne0 * 2));
         OPCHK(s.alloc(&rs, (size_t)Mpad * 4));
-        OPCHK(launch_pf_pack_q8(m, wf, s.st));
         OPCHK(launch_pf_split(dx, ne0, nullptr, 0.0f, (int)ne0, n_rows_x, Mpad, xa, rs, s.st));
         PfGemmArgs a;
         a.xa = xa;
@@ -1502,7 +1500,6 @@ int tf_hip_matmul(int device, int t, const void* w, int64_t ne0, int64_t ne1, co
         a.mode = GEMV_STORE;
         a.n_seg = 1;
         a.seg[0].w = m;
-        a.seg[0].wf = wf;
         a.seg[0].y = dy;
         a.seg[0].ldy = ne1;
         a.n_sub = (int)(ne1 / 16);

@@ -224,10 +224,8 @@ __host__ __device__ inline int64_t kv_offset(int layout, int G, int max_seq, int
 
 // One weight matrix of a prefill GEMM and where its output columns go.
 struct PfSeg {
-    DevMat w;                     // weight (gate for GEMV_SILU): shape and fp16 d stream
-    DevMat w2;                    // up matrix for GEMV_SILU
-    const uint16_t* wf = nullptr;   // w's integers as fp16 in fragment order (launch_pf_pack_q8)
-    const uint16_t* wf2 = nullptr;  // the same for w2
+    DevMat w;                     // weight (gate for GEMV_SILU), read in its HBM layout
+    DevMat w2;                    // up matrix for GEMV_SILU, w's format
     float* y = nullptr;           // output rows of ldy floats
     int64_t ldy = 0;
     const float* bias = nullptr;  // F32 bias added to the output (GEMV_STORE)
@@ -266,12 +264,12 @@ struct PfGemmArgs {
     int pos0 = 0, n_head = 0, n_kv = 0, hd = 0, kv_layout = 0, max_seq = 0;
 };
 
+// Q8_0, Q4_0, Q4_1 or F16 with K % 64 == 0 and N % 16 == 0; the matrices of one
+// launch_pf_gemm share one format.
 bool pf_gemm_supported(int type, int64_t K, int64_t N);
 // xa needs Mpad * K * 2 halves, rs Mpad floats.
 hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,
                            uint16_t* xa, float* rs, hipStream_t st);
-// wf needs m.N * m.K halves.
-hipError_t launch_pf_pack_q8(const DevMat& m, uint16_t* wf, hipStream_t st);
 hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused = nullptr);
 hipError_t launch_embed_rows(const DevMat& emb, const int32_t* tok, int n, float* x, int D, hipStream_t st);
 hipError_t launch_pf_rope_store(float* qkv, int64_t ld, int n, int H, int G, int hd, const float* rope_cos,

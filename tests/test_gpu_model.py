@@ -204,10 +204,11 @@ def test_small_models_token_prefill(pkg, gguf, preset, layout):
 
 
 @pytest.mark.parametrize("preset,want", [("tiny_q8", MFMA), ("tiny_qwen", MFMA), ("small_q8", MFMA),
-                                         ("tiny_f32", TOKENS), ("tiny_mixq4", TOKENS)])
+                                         ("tiny_f32", TOKENS), ("tiny_mixq4", MFMA), ("tiny_mixfmt", MFMA)])
 def test_prefill_path_selection(pkg, gguf, preset, want):
-    """Prompts run on the matrix cores when every layer matrix is Q8_0 with tileable
-    shapes; F32 and Q4 models keep the per-token path; PREFILL_TOKENS forces it."""
+    """Prompts run on the matrix cores when every layer matrix is Q8_0, Q4_0, Q4_1 or F16
+    with tileable shapes (gate and up in one format); F32 models keep the per-token path;
+    PREFILL_TOKENS forces it."""
     hip = pkg.HipModel(gguf(preset), max_seq=64)
     assert hip.prefill_path() == want
     hip.set_prefill_path(TOKENS)
@@ -236,6 +237,33 @@ def test_prefill_paths_agree(pkg, gguf):
     assert rel_err(l1, l0) <= 1e-4
     for a, b in zip(t1, t0):
         assert rel_err(a, b) <= 1e-4
+    for a, b in zip(k1, k0):
+        assert rel_err(a, b) <= 1e-4
+
+
+@pytest.mark.parametrize("n_prompt", [6, 150])
+@pytest.mark.parametrize("preset", ["tiny_mixq4", "tiny_mixfmt"])
+def test_mixed_format_prefill(pkg, gguf, preset, n_prompt):
+    """Q4_0 / Q4_1 / F16 / Q8_0 layer matrices on the matrix cores against the oracle
+    (tiny_mixfmt: q, k and v in three formats, one launch each; Q4_1 and F16 gate / up),
+    and against the per-token prefill of the same prompt."""
+    info = pkg.synth_preset_info(preset)
+    prompt = pkg.synth_prompt(info["seed"] + 3, n_prompt, info["n_vocab"])
+    hip = pkg.HipModel(gguf(preset), max_seq=256)
+    assert hip.prefill_path() == MFMA
+    hip.close()
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 8, 256, 0)
+    print(f"{preset} {n_prompt}-token prompt: ids {ids} logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
+    res = []
+    for pf in (TOKENS, MFMA):
+        hip = pkg.HipModel(gguf(preset), max_seq=256)
+        hip.set_prefill_path(pf)
+        lg, am = hip.prefill(prompt)
+        kv = [hip.read_kv(layer, w, 0, n_prompt) for layer in range(hip.n_layer) for w in (0, 1)]
+        res.append((lg, am, kv))
+        hip.close()
+    (l0, a0, k0), (l1, a1, k1) = res
+    assert a0 == a1 and rel_err(l1, l0) <= 1e-4
     for a, b in zip(k1, k0):
         assert rel_err(a, b) <= 1e-4
 
@@ -321,6 +349,7 @@ def test_errors_and_reset(pkg, gguf):
     ("llama1b_mixq4", 6, 64, 512, 0),   # Q4_0 / Q4_1 / Q6_K mix
     ("qwen15b_q8", 64, 16, 8192, 1),    # Qwen2.5-1.5B shape, head-major cache (short prompt)
     ("llama1b_q8", 512, 16, 1024, 0),   # 512-token prompt on the matrix cores, then 16 decode tokens
+    ("llama1b_mixq4", 512, 16, 1024, 0),  # the same on Q4_0 / Q4_1 layer matrices
 ])
 def test_full_size(pkg, gguf, preset, n_prompt, n_gen, max_seq, layout):
     info = pkg.synth_preset_info(preset)

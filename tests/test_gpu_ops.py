@@ -121,19 +121,51 @@ PF_GEMM_SHAPES = [(2, 64, 16), (37, 2048, 256), (64, 896, 1152), (100, 8192, 128
                   (512, 2048, 2048)]  # 32 such tiles, K split in 8 slices and reduced
 
 
-@pytest.mark.parametrize("m,k,n", PF_GEMM_SHAPES)
-def test_prefill_gemm_matches_oracle(pkg, m, k, n):
-    """Q8_0 rows x M activation rows on the matrix cores: |y - y_oracle| <= 2e-5 * sum_k
-    |x_k w_nk| per output. The fp16 pair of an activation keeps it to 2^-22 of its row's
-    largest element; the rest is fp32 reassociation, as for the GEMV."""
-    rng = np.random.default_rng(2000 + m + k + n)
-    rows = random_rows(rng, 8, k, n)
+# the other formats the matrix cores take, read in their own layout: the register-streamed
+# tiles, the LDS-staged tiles (500 x 256 x 16384) and K split in slices (512 x 2048 x 2048)
+PF_GEMM_FMT_SHAPES = [(t, m, k, n) for t in (2, 3, 1)
+                      for (m, k, n) in [(2, 64, 16), (37, 2048, 256), (130, 1536, 48), (7, 192, 320),
+                                        (500, 256, 16384), (512, 2048, 2048)]]
+
+
+@pytest.mark.parametrize("t,m,k,n", [(8, m, k, n) for (m, k, n) in PF_GEMM_SHAPES] + PF_GEMM_FMT_SHAPES)
+def test_prefill_gemm_matches_oracle(pkg, t, m, k, n):
+    """Q8_0, Q4_0, Q4_1 or F16 rows x M activation rows on the matrix cores: |y - y_oracle|
+    <= 2e-5 * sum_k |x_k w_nk| per output. The fp16 pair of an activation keeps it to 2^-22
+    of its row's largest element; the rest is fp32 reassociation, as for the GEMV."""
+    rng = np.random.default_rng(2000 + m + k + n + t)
+    rows = random_rows(rng, t, k, n)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    got = pkg.matmul(8, rows, k, n, x)
-    want = oracle_matmul(8, rows, k, x)
-    budget = np.abs(x).astype(np.float64) @ np.abs(oracle_dequant(8, rows, k)).astype(np.float64).T
+    got = pkg.matmul(t, rows, k, n, x)
+    want = oracle_matmul(t, rows, k, x)
+    budget = np.abs(x).astype(np.float64) @ np.abs(oracle_dequant(t, rows, k)).astype(np.float64).T
     err = np.abs(got.astype(np.float64) - want)
     assert np.all(err <= 2e-5 * budget + 1e-30), f"max err/budget {np.max(err / (budget + 1e-30)):.3e}"
+
+
+@pytest.mark.parametrize("t", [8, 2, 3, 1])
+def test_prefill_gemm_single_element_rows(pkg, t):
+    """A row with one non-zero x_j gives x_j * w[:, j] (one product per output; Q4_1's
+    d n + m as d (x n) + m x, which the oracle's fp32 dequant rounds once: within 2 ulp)."""
+    rng = np.random.default_rng(90 + t)
+    k, n = 256, 4096  # 500 rows below: the LDS-staged kernel
+    rows = random_rows(rng, t, k, n)
+    deq = oracle_dequant(t, rows, k)
+    x = np.zeros((500, k), np.float32)
+    js = rng.integers(0, k, 500)
+    x[np.arange(500), js] = rng.choice([-3.0, 0.5, 2.0, 7.0], 500).astype(np.float32)
+    got = pkg.matmul(t, rows, k, n, x)
+    want = (x[np.arange(500), js][:, None] * deq[:, js].T).astype(np.float32)
+    if t == 3:
+        # Q4_1 blocks are (d, m, 16 bytes): the two roundings of x (d n) + x m, against the
+        # magnitudes of their terms
+        m = rows.reshape(n, k // 32, 20)[:, :, 2:4].copy().view(np.float16).astype(np.float64)[:, :, 0]
+        mj = m[:, js // 32].T
+        xa = np.abs(x[np.arange(500), js].astype(np.float64))[:, None]
+        bound = 2.0**-22 * xa * (np.abs(deq[:, js].T - mj) + np.abs(mj))
+        assert np.all(np.abs(got.astype(np.float64) - want) <= bound + 1e-30)
+    else:
+        assert np.array_equal(got, want)
 
 
 def test_prefill_gemm_row_scales(pkg):

@@ -300,7 +300,8 @@ def test_attention_matches_reference(layout, H, G, hd, n_pos, S):
 
 @needs_ref
 @pytest.mark.parametrize("layout", [0, 1])
-@pytest.mark.parametrize("preset", ["tiny_f32", "tiny_q8", "tiny_mixq4", "tiny_qwen", "tiny_hd128", "small_q8"])
+@pytest.mark.parametrize("preset", ["tiny_f32", "tiny_q8", "tiny_mixq4", "tiny_qwen", "tiny_hd128", "small_q8",
+                                    "tiny_mixfmt"])
 def test_model_matches_reference_bit_for_bit(pkg, gguf, preset, layout):
     path = gguf(preset)
     info = pkg.synth_preset_info(preset)
