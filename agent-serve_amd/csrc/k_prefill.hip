@@ -50,31 +50,28 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 // fp16, and the block's scale multiplies the block sum afterwards in fp32 (Q4_1's d n + m as
 // d sum x n + m sum x); F16 weights are their own fp16 values with scale 1.
 
+// Bytes of a dword, two at a time, as the low bytes of two halves whose high byte is 0x64
+// (v_perm_b32: selector byte n < 4 takes byte n of the second operand, 4 byte 0 of the
+// first): bytes 0, 1 (hi = 0) or 2, 3 (hi = 1) of w -> the halves 1024 + byte.
+__device__ __forceinline__ uint32_t bytes_to_h2(uint32_t w, int hi) {
+    return __builtin_amdgcn_perm(0x64646464u, w, hi ? 0x04030402u : 0x04010400u);
+}
+
 // Eight int8 bytes q -> their fp16 values: with u = q + 128 (the byte with its top bit
 // flipped), 0x64UU is the half 1024 + u, and 1024 + u - 1152 = q exactly.
 __device__ __forceinline__ h8_t q8_to_h8(uint2 w) {
-    w.x ^= 0x80808080u;
-    w.y ^= 0x80808080u;
-    const uint32_t p0 = (w.x & 0xFFu) | ((w.x & 0xFF00u) << 8) | 0x64006400u;
-    const uint32_t p1 = ((w.x >> 16) & 0xFFu) | ((w.x >> 8) & 0xFF0000u) | 0x64006400u;
-    const uint32_t p2 = (w.y & 0xFFu) | ((w.y & 0xFF00u) << 8) | 0x64006400u;
-    const uint32_t p3 = ((w.y >> 16) & 0xFFu) | ((w.y >> 8) & 0xFF0000u) | 0x64006400u;
-    const tf_u32x4 p = {p0, p1, p2, p3};
+    const uint32_t x = w.x ^ 0x80808080u, y = w.y ^ 0x80808080u;
+    const tf_u32x4 p = {bytes_to_h2(x, 0), bytes_to_h2(x, 1), bytes_to_h2(y, 0), bytes_to_h2(y, 1)};
     const h8_t off = {1152, 1152, 1152, 1152, 1152, 1152, 1152, 1152};
     return __builtin_bit_cast(h8_t, p) - off;
 }
 
-// The 4-bit codes n in the low (hi = 0) or high (hi = 1) nibbles of 8 bytes -> fp16 n - OFF
-// (0x640n is the half 1024 + n).
+// The 4-bit codes n in the low (hi = 0) or high (hi = 1) nibbles of 8 bytes -> fp16 n - OFF.
 template <int OFF>
 __device__ __forceinline__ h8_t q4_to_h8(uint2 w, int hi) {
     const int sh = 4 * hi;
     const uint32_t a = (w.x >> sh) & 0x0F0F0F0Fu, b = (w.y >> sh) & 0x0F0F0F0Fu;
-    const uint32_t p0 = (a & 0xFFu) | ((a & 0xFF00u) << 8) | 0x64006400u;
-    const uint32_t p1 = ((a >> 16) & 0xFFu) | ((a >> 8) & 0xFF0000u) | 0x64006400u;
-    const uint32_t p2 = (b & 0xFFu) | ((b & 0xFF00u) << 8) | 0x64006400u;
-    const uint32_t p3 = ((b >> 16) & 0xFFu) | ((b >> 8) & 0xFF0000u) | 0x64006400u;
-    const tf_u32x4 p = {p0, p1, p2, p3};
+    const tf_u32x4 p = {bytes_to_h2(a, 0), bytes_to_h2(a, 1), bytes_to_h2(b, 0), bytes_to_h2(b, 1)};
     constexpr _Float16 o = (_Float16)(1024 + OFF);
     const h8_t off = {o, o, o, o, o, o, o, o};
     return __builtin_bit_cast(h8_t, p) - off;
