@@ -4,7 +4,8 @@
 // k_pf_split     rmsnorm (layers.cpp:7-12) of each row, or the row as it is, scaled by
 //                a power of two and written as fp16 hi + lo in fragment order (the A operand)
 // k_pf_gemm_tile / k_pf_gemm_big   matmul (matmul.cpp:64-73) of Q8_0, Q4_0, Q4_1 or F16
-//                weights, read in their HBM layout, on v_mfma_f32_16x16x32_f16; epilogues:
+//                weights, read in their HBM layout, on v_mfma_f32_16x16x32_f16 (k_pf_gemm_q6k:
+//                Q6_K; k_pf_gemm_f32: F32 weights on v_mfma_f32_16x16x4_f32); epilogues:
 //                store (+ F32 bias, model.cpp:85-89), residual add (add_inplace,
 //                layers.cpp:21-23), silu(gate) * up (layers.cpp:14-19)
 // k_pf_rope_store apply_rope_many of q and k (attention.cpp:48-53) and KVCache::store
@@ -280,62 +281,118 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
 // Field of the segment holding output subtile u (uniform per wave: scalar selects).
 #define PF_SEL(s, f) ((s) == 0 ? a.seg[0].f : ((s) == 1 ? a.seg[1].f : a.seg[2].f))
 
-// Workgroup: 4 waves as 2 (rows) x 2 (columns); a wave owns 32 rows x NI column subtiles
-// of 16 (GEMV_SILU: NI / 2 output subtiles, each a gate and an up subtile). Per 32-element
-// block: for each (row subtile, column subtile) an MFMA of the hi part from zero, then
-// one of the lo part on top (issued after all eight hi MFMAs, so no MFMA waits on the
-// one before it), then acc += d * block sum (Q4_1: + m * the rows' block sums, from the
+// A register-streamed tile (k_pf_gemm_tile, k_pf_gemm_f32, k_pf_gemm_q6k): a workgroup of 4
+// waves as 2 (rows) x 2 (columns); a wave owns 32 rows from m0 and NI weight-column subtiles
+// of 16 (GEMV_SILU: NI / 2 output subtiles, each a gate and an up subtile). Per subtile: its
+// segment, the weight row c this lane reads (the output column), whether it is past the
+// last subtile (computed on a clamped one, not written).
+template <int MODE, int NI>
+struct TileCtx {
+    static constexpr int NO = MODE == GEMV_SILU ? NI / 2 : NI;  // output subtiles per wave
+    int lane, l16, lc, m0;
+    int seg[NI], c[NI];
+    bool ok[NI];
+    float* y[NI];
+    const float* bias[NI];
+    int64_t ldy[NI];
+    const uint8_t *wq[NI], *wq2[NI], *ws[NI], *ws2[NI];  // the subtile's matrix streams
+    __device__ __forceinline__ TileCtx(const PfGemmArgs& a) {
+        lane = threadIdx.x & 63;
+        l16 = lane & 15;
+        lc = lane >> 4;
+        const int wave = threadIdx.x >> 6;
+        // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous range
+        // of tiles, rows fastest, so the row tiles that share a weight tile share an L2.
+        int b = blockIdx.x;
+        {
+            const int q = (int)gridDim.x / 8;
+            if (b < 8 * q) b = (b % 8) * q + b / 8;
+        }
+        const int MT = a.Mpad / kPfTileM;
+        const int mt = b % MT, nt = b / MT;
+        m0 = mt * kPfTileM + (wave & 1) * 32;
+        const int wid = nt * 2 + (wave >> 1);
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+            int u = wid * NO + ni % NO;
+            ok[ni] = u < a.n_sub;
+            u = u < a.n_sub ? u : a.n_sub - 1;
+            seg[ni] = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
+            c[ni] = (u - PF_SEL(seg[ni], sub0)) * 16 + l16;
+            const bool u2 = up(ni);
+            const int sg = seg[ni];
+            wq[ni] = u2 ? PF_SEL(sg, w2.q) : PF_SEL(sg, w.q);
+            wq2[ni] = u2 ? PF_SEL(sg, w2.q2) : PF_SEL(sg, w.q2);
+            ws[ni] = u2 ? PF_SEL(sg, w2.s) : PF_SEL(sg, w.s);
+            ws2[ni] = u2 ? PF_SEL(sg, w2.s2) : PF_SEL(sg, w.s2);
+            y[ni] = PF_SEL(seg[ni], y);
+            bias[ni] = PF_SEL(seg[ni], bias);
+            ldy[ni] = PF_SEL(seg[ni], ldy);
+        }
+    }
+    __device__ __forceinline__ static bool up(int ni) { return MODE == GEMV_SILU && ni >= NO; }
+    // fragment pointers of the wave's two 16-row activation subtiles (lane's 8 halves)
+    __device__ __forceinline__ void act(const PfGemmArgs& a, const TF_GLOBAL h8_t* (&ap)[2]) const {
+        const int nblk = a.K / 32;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+            ap[mi] = (const TF_GLOBAL h8_t*)a.xa + (int64_t)(m0 / 16 + mi) * nblk * 128 + lane;
+    }
+    // lane holds rows m0 + 16 mi + 4 (lane / 16) + r of output column c[ni], scaled back by
+    // the row scales: store (+ bias), residual add (+ the tap row) or silu(gate) * up
+    __device__ __forceinline__ void epilogue(const PfGemmArgs& a, const f4_t (&acc)[2][NI]) const {
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+            const int r0 = m0 + 16 * mi + 4 * (lane >> 4);
+            const float4 rsv = *(const float4*)(a.rs + r0);
+            const float rsa[4] = {rsv.x, rsv.y, rsv.z, rsv.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = r0 + r;
+                if (row >= a.M) continue;
+#pragma unroll
+                for (int ni = 0; ni < NO; ++ni) {
+                    if (!ok[ni]) continue;
+                    float* p = y[ni] + (int64_t)row * ldy[ni] + c[ni];
+                    if (MODE == GEMV_SILU) {
+                        const float gv = acc[mi][ni][r] * rsa[r];
+                        const float uv = acc[mi][ni + NO][r] * rsa[r];
+                        *p = (gv / (1.0f + expf(-gv))) * uv;
+                    } else if (MODE == GEMV_STORE) {
+                        const float v = acc[mi][ni][r] * rsa[r];
+                        *p = bias[ni] ? v + bias[ni][c[ni]] : v;
+                    } else {
+                        const float nv = *p + acc[mi][ni][r] * rsa[r];
+                        *p = nv;
+                        if (row == a.tap_row && a.tap) a.tap[c[ni]] = nv;
+                    }
+                }
+            }
+        }
+    }
+};
+
+// Per 32-element block: for each (row subtile, column subtile) an MFMA of the hi part from
+// zero, then one of the lo part on top (issued after all eight hi MFMAs, so no MFMA waits on
+// the one before it), then acc += d * block sum (Q4_1: + m * the rows' block sums, from the
 // same two MFMAs against a fragment of ones). Weight bytes and activation fragments stream
 // from L2 into registers, one stage of two blocks ahead; every load is unconditional
 // (indices clamped) so the compiler waits only for the stage it consumes.
 template <int MODE, int NI, int T>
 __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
     using W = PfW<T>;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous range
-    // of tiles, rows fastest, so the row tiles that share a weight tile share an L2.
-    int b = blockIdx.x;
-    {
-        const int q = (int)gridDim.x / 8;
-        if (b < 8 * q) b = (b % 8) * q + b / 8;
-    }
-    const int MT = a.Mpad / kPfTileM;
-    const int mt = b % MT, nt = b / MT;
-    const int m0 = mt * kPfTileM + (wave & 1) * 32;
-    const int wid = nt * 2 + (wave >> 1);
+    const TileCtx<MODE, NI> t(a);
     const int K = a.K, nblk = K / 32;
-    const int l16 = lane & 15, lc = lane >> 4;
-
-    constexpr int NO = MODE == GEMV_SILU ? NI / 2 : NI;  // output subtiles per wave
-    constexpr int SW = W::kScale == 4 ? 2 : 1;           // scale words per stage and column
+    constexpr int SW = W::kScale == 4 ? 2 : 1;  // scale words per stage and column
     const TF_GLOBAL uint8_t* bp[NI];
     const TF_GLOBAL uint32_t* sp[NI];
-    float* yp[NI];
-    const float* bsp[NI];
-    int64_t ldy[NI];
-    int col[NI];
-    bool ok[NI];
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
-        int u = wid * NO + ni % NO;
-        ok[ni] = u < a.n_sub;
-        u = u < a.n_sub ? u : a.n_sub - 1;
-        const int s = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
-        const int tile = u - PF_SEL(s, sub0);
-        const int c = tile * 16 + l16;
-        const bool up = MODE == GEMV_SILU && ni >= NO;
-        const uint8_t* wq = up ? PF_SEL(s, w2.q) : PF_SEL(s, w.q);
-        const uint8_t* ws = up ? PF_SEL(s, w2.s) : PF_SEL(s, w.s);
-        bp[ni] = (const TF_GLOBAL uint8_t*)wq + (int64_t)c * nblk * W::kBytes + W::off(lc);
-        sp[ni] = (const TF_GLOBAL uint32_t*)(ws + (int64_t)c * nblk * W::kScale);
-        yp[ni] = PF_SEL(s, y);
-        bsp[ni] = PF_SEL(s, bias);
-        ldy[ni] = PF_SEL(s, ldy);
-        col[ni] = c;
+        bp[ni] = (const TF_GLOBAL uint8_t*)t.wq[ni] + (int64_t)t.c[ni] * nblk * W::kBytes + W::off(t.lc);
+        sp[ni] = (const TF_GLOBAL uint32_t*)(t.ws[ni] + (int64_t)t.c[ni] * nblk * W::kScale);
     }
     const TF_GLOBAL h8_t* ap[2];
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi) ap[mi] = (const TF_GLOBAL h8_t*)a.xa + (int64_t)(m0 / 16 + mi) * nblk * 128 + lane;
+    t.act(a, ap);
 
     f4_t acc[2][NI];
 #pragma unroll
@@ -344,9 +401,9 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
         for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
 
     struct Stage {
-        h8_t ah[2][2], al[2][2];         // [row subtile][block]
-        typename W::Raw bw[NI][2];       // [column subtile][block]: the lane's weight bytes
-        uint32_t d[NI][SW];              // the scale words of the stage's two blocks
+        h8_t ah[2][2], al[2][2];    // [row subtile][block]
+        typename W::Raw bw[NI][2];  // [column subtile][block]: the lane's weight bytes
+        uint32_t d[NI][SW];         // the scale words of the stage's two blocks
     };
     const int S = K / 64;
     auto load = [&](int s, Stage& g) {
@@ -374,14 +431,14 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
         for (int j = 0; j < 2; ++j) {
             h8_t bh[NI];
 #pragma unroll
-            for (int ni = 0; ni < NI; ++ni) bh[ni] = W::cvt(g.bw[ni][j], lc);
-            f4_t t[2][NI], ts[2];
+            for (int ni = 0; ni < NI; ++ni) bh[ni] = W::cvt(g.bw[ni][j], t.lc);
+            f4_t tb[2][NI], ts[2];
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni)
-                    t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], bh[ni],
-                                                                      (f4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    tb[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], bh[ni],
+                                                                       (f4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
                 if (W::kMin)
                     ts[mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], ones, (f4_t){0.0f, 0.0f, 0.0f, 0.0f},
                                                                     0, 0, 0);
@@ -390,7 +447,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
             for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni)
-                    t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], bh[ni], t[mi][ni], 0, 0, 0);
+                    tb[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], bh[ni], tb[mi][ni], 0, 0, 0);
                 if (W::kMin) ts[mi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], ones, ts[mi], 0, 0, 0);
             }
 #pragma unroll
@@ -401,8 +458,8 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
                 for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[mi][ni][r] = W::kMin ? fmaf(dv, t[mi][ni][r], fmaf(mv, ts[mi][r], acc[mi][ni][r]))
-                                                 : fmaf(dv, t[mi][ni][r], acc[mi][ni][r]);
+                        acc[mi][ni][r] = W::kMin ? fmaf(dv, tb[mi][ni][r], fmaf(mv, ts[mi][r], acc[mi][ni][r]))
+                                                 : fmaf(dv, tb[mi][ni][r], acc[mi][ni][r]);
             }
         }
     };
@@ -416,42 +473,122 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
         compute(s1);
     }
     if (s < S) compute(s0);
+    t.epilogue(a, acc);
+}
 
-    // epilogue: lane holds rows m0 + 16 mi + 4 (lane / 16) + r of column col[ni]
+// F32 weights on v_mfma_f32_16x16x4_f32. The activations come from the same hi + lo
+// fragments (their sum, exact in fp32, is the row's 22-bit value); the weights are loaded as
+// they lie. Within a 32-element block, MFMA j (0..7) takes from lane l the element
+// k = 8 (l / 16) + j: the 8 consecutive values each lane holds of both operands, a
+// reordering of the block's terms. No block scales: every MFMA accumulates into acc.
+template <int MODE, int NI>
+__global__ __launch_bounds__(256) void k_pf_gemm_f32(const PfGemmArgs a) {
+    const TileCtx<MODE, NI> t(a);
+    const int K = a.K, nblk = K / 32;
+    const float* bp[NI];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi) {
-        const int r0 = m0 + 16 * mi + 4 * (lane >> 4);
-        const float4 rsv = *(const float4*)(a.rs + r0);
-        const float rsa[4] = {rsv.x, rsv.y, rsv.z, rsv.w};
+    for (int ni = 0; ni < NI; ++ni) bp[ni] = (const float*)t.wq[ni] + (int64_t)t.c[ni] * K + 8 * t.lc;
+    const TF_GLOBAL h8_t* ap[2];
+    t.act(a, ap);
+    f4_t acc[2][NI];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = r0 + r;
-            if (row >= a.M) continue;
-            if (MODE == GEMV_SILU) {
+    for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-                for (int j = 0; j < NO; ++j) {
-                    if (!ok[j]) continue;
-                    const float gv = acc[mi][j][r] * rsa[r];
-                    const float uv = acc[mi][j + NO][r] * rsa[r];
-                    yp[j][(int64_t)row * ldy[j] + col[j]] = (gv / (1.0f + expf(-gv))) * uv;
-                }
-            } else {
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int blk = 0; blk < nblk; ++blk) {
+        float x[2][8];
 #pragma unroll
-                for (int ni = 0; ni < NI; ++ni) {
-                    if (!ok[ni]) continue;
-                    const float v = acc[mi][ni][r] * rsa[r];
-                    float* p = yp[ni] + (int64_t)row * ldy[ni] + col[ni];
-                    if (MODE == GEMV_STORE) {
-                        *p = bsp[ni] ? v + bsp[ni][col[ni]] : v;
-                    } else {
-                        const float nv = *p + v;
-                        *p = nv;
-                        if (row == a.tap_row && a.tap) a.tap[col[ni]] = nv;
-                    }
-                }
-            }
+        for (int mi = 0; mi < 2; ++mi) {
+            const h8_t hi = ap[mi][blk * 128], lo = ap[mi][blk * 128 + 64];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[mi][j] = (float)hi[j] + (float)lo[j];
         }
+        float w[NI][8];
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+            const float4 u = gload_f4(bp[ni] + 32 * blk), v = gload_f4(bp[ni] + 32 * blk + 4);
+            w[ni][0] = u.x; w[ni][1] = u.y; w[ni][2] = u.z; w[ni][3] = u.w;
+            w[ni][4] = v.x; w[ni][5] = v.y; w[ni][6] = v.z; w[ni][7] = v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[mi][j], w[ni][j], acc[mi][ni], 0, 0, 0);
     }
+    t.epilogue(a, acc);
+}
+
+// Q6_K weights (quant.cpp:101-127). A 32-element group of a row: lo[16] (element e < 16 in
+// the low nibble of byte e, e + 16 in its high nibble), hi[8] (element e's top two bits at
+// bits 2 (e / 8) of byte e % 8), an int8 scale per 16 elements and an fp16 d per 256: the
+// value d sc (u - 32) for the 6-bit code u. Lane l's 8 elements 8 c .. 8 c + 7 (c = l / 16)
+// share the scale sc of sub-block c / 2, folded into the B operand: sc (u - 32), an integer
+// of at most 4096 in magnitude, is the fp16 pair hi (its rounding, v_pk_mul_f16) + lo (the
+// exact remainder, at most 1, from v_pk_fma_f16). Per block: the activation hi and lo against
+// B hi and the activation hi against B lo (the lo x lo term is below 2^-22 of the product)
+// from zero, then acc += d * block sum.
+template <int MODE, int NI>
+__global__ __launch_bounds__(256) void k_pf_gemm_q6k(const PfGemmArgs a) {
+    const TileCtx<MODE, NI> t(a);
+    const int K = a.K, nblk = K / 32;
+    const TF_GLOBAL uint8_t *lp[NI], *hp[NI], *scp[NI];
+    const TF_GLOBAL uint16_t* dp[NI];
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+        const int64_t c = t.c[ni];
+        lp[ni] = (const TF_GLOBAL uint8_t*)t.wq[ni] + c * (K / 2) + 8 * (t.lc & 1);
+        hp[ni] = (const TF_GLOBAL uint8_t*)t.wq2[ni] + c * (K / 4);
+        scp[ni] = (const TF_GLOBAL uint8_t*)t.ws[ni] + c * (K / 16) + (t.lc >> 1);
+        dp[ni] = (const TF_GLOBAL uint16_t*)(t.ws2[ni] + c * (K / 256) * 2);
+    }
+    const TF_GLOBAL h8_t* ap[2];
+    t.act(a, ap);
+    f4_t acc[2][NI];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    const f4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int blk = 0; blk < nblk; ++blk) {
+        h8_t ah[2], al[2];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+            ah[mi] = ap[mi][blk * 128];
+            al[mi] = ap[mi][blk * 128 + 64];
+        }
+        h8_t bh[NI], bl[NI];
+        float dv[NI];
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+            const uint2 lo = gload_u2((const void*)(lp[ni] + 16 * blk));
+            const uint2 hi = gload_u2((const void*)(hp[ni] + 8 * blk));
+            const int sh = 4 * (t.lc >> 1), hs = 2 * t.lc;
+            const uint32_t u0 = ((lo.x >> sh) & 0x0F0F0F0Fu) | (((hi.x >> hs) & 0x03030303u) << 4);
+            const uint32_t u1 = ((lo.y >> sh) & 0x0F0F0F0Fu) | (((hi.y >> hs) & 0x03030303u) << 4);
+            const tf_u32x4 p = {bytes_to_h2(u0, 0), bytes_to_h2(u0, 1), bytes_to_h2(u1, 0), bytes_to_h2(u1, 1)};
+            const h8_t off = {1056, 1056, 1056, 1056, 1056, 1056, 1056, 1056};
+            const h8_t q = __builtin_bit_cast(h8_t, p) - off;  // u - 32, exact
+            const _Float16 sc = (_Float16)(int8_t)scp[ni][2 * blk];
+            const h8_t scv = {sc, sc, sc, sc, sc, sc, sc, sc};
+            bh[ni] = q * scv;
+            bl[ni] = __builtin_elementwise_fma(q, scv, -bh[ni]);
+            dv[ni] = h2f(dp[ni][blk >> 3]);
+        }
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni) {
+                f4_t tb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mi], bh[ni], zero, 0, 0, 0);
+                tb = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mi], bh[ni], tb, 0, 0, 0);
+                tb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mi], bl[ni], tb, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[mi][ni][r] = fmaf(dv[ni], tb[r], acc[mi][ni][r]);
+            }
+    }
+    t.epilogue(a, acc);
 }
 
 // Large tiles for GEMMs with enough of them to fill the CUs: a workgroup of 8 waves
@@ -1246,8 +1383,9 @@ __global__ __launch_bounds__(kBlock) void k_pf_tail(Ctl* ctl, int pos_last, cons
 
 bool pf_gemm_supported(int type, int64_t K, int64_t N) {
     const bool fmt = type == TF_HIP_TYPE_Q8_0 || type == TF_HIP_TYPE_Q4_0 || type == TF_HIP_TYPE_Q4_1 ||
-                     type == TF_HIP_TYPE_F16;
-    return fmt && K % 64 == 0 && N % 16 == 0 && K <= kBlock * 8 * kSplitGroups;
+                     type == TF_HIP_TYPE_F16 || type == TF_HIP_TYPE_F32 || type == TF_HIP_TYPE_Q6_K;
+    return fmt && K % 64 == 0 && N % 16 == 0 && K <= kBlock * 8 * kSplitGroups &&
+           (type != TF_HIP_TYPE_Q6_K || K % 256 == 0);
 }
 
 hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,
@@ -1426,6 +1564,35 @@ hipError_t launch_pf_gemm(const PfGemmArgs& a, hipStream_t st, bool* fused) {
         if (a.mode == GEMV_SILU && (g.w2.type != t || g.w2.K != a.K || g.w2.N != g.w.N)) return hipErrorInvalidValue;
     }
     if (a.seg[0].sub0 != 0 || (a.mode == GEMV_SILU && a.n_seg != 1)) return hipErrorInvalidValue;
+    if (t == TF_HIP_TYPE_F32 || t == TF_HIP_TYPE_Q6_K) {
+        // register-streamed tiles only: 4 column subtiles per wave, 2 when that leaves
+        // fewer than two workgroups per CU
+        const int mt = a.Mpad / kPfTileM;
+        const int out4 = a.mode == GEMV_SILU ? 2 : 4;
+        const int wg4 = (a.n_sub + 2 * out4 - 1) / (2 * out4) * mt;
+        const int ni = wg4 >= 2 * device_cu_count() ? 4 : 2;
+        const int per_wg = 2 * (a.mode == GEMV_SILU ? ni / 2 : ni);
+        const dim3 grid((unsigned)((a.n_sub + per_wg - 1) / per_wg * mt));
+#define PF_OWN(KERNEL, MODE, NI) hipLaunchKernelGGL((KERNEL<MODE, NI>), grid, dim3(256), 0, st, a)
+#define PF_OWN_ALL(KERNEL)                                             \
+    switch (a.mode * 8 + ni) {                                         \
+        case GEMV_STORE * 8 + 4: PF_OWN(KERNEL, GEMV_STORE, 4); break; \
+        case GEMV_STORE * 8 + 2: PF_OWN(KERNEL, GEMV_STORE, 2); break; \
+        case GEMV_RESID * 8 + 4: PF_OWN(KERNEL, GEMV_RESID, 4); break; \
+        case GEMV_RESID * 8 + 2: PF_OWN(KERNEL, GEMV_RESID, 2); break; \
+        case GEMV_SILU * 8 + 4: PF_OWN(KERNEL, GEMV_SILU, 4); break;   \
+        case GEMV_SILU * 8 + 2: PF_OWN(KERNEL, GEMV_SILU, 2); break;   \
+        default: return hipErrorInvalidValue;                          \
+    }
+        if (t == TF_HIP_TYPE_F32) {
+            PF_OWN_ALL(k_pf_gemm_f32)
+        } else {
+            PF_OWN_ALL(k_pf_gemm_q6k)
+        }
+#undef PF_OWN_ALL
+#undef PF_OWN
+        return hipGetLastError();
+    }
     switch (t) {
         case TF_HIP_TYPE_Q8_0: return launch_gemm_t<TF_HIP_TYPE_Q8_0>(a, st, fused);
         case TF_HIP_TYPE_Q4_0: return launch_gemm_t<TF_HIP_TYPE_Q4_0>(a, st, fused);

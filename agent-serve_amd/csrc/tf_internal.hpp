@@ -264,8 +264,8 @@ struct PfGemmArgs {
     int pos0 = 0, n_head = 0, n_kv = 0, hd = 0, kv_layout = 0, max_seq = 0;
 };
 
-// Q8_0, Q4_0, Q4_1 or F16 with K % 64 == 0 and N % 16 == 0; the matrices of one
-// launch_pf_gemm share one format.
+// Q8_0, Q4_0, Q4_1, F16, F32 or Q6_K (K % 256 == 0) with K % 64 == 0 and N % 16 == 0; the
+// matrices of one launch_pf_gemm share one format.
 bool pf_gemm_supported(int type, int64_t K, int64_t N);
 // xa needs Mpad * K * 2 halves, rs Mpad floats.
 hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, float eps, int K, int M, int Mpad,

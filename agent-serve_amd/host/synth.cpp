@@ -268,13 +268,14 @@ bool synth_preset(const std::string& name, SynthSpec* s) {
         p.type_embd = GGML_Q6_K;
         p.overrides = {{0, "ffn_down", GGML_Q4_1}, {2, "ffn_down", GGML_Q4_1}};
     } else if (name == "tiny_mixfmt") {
-        // a format per matrix: q, k and v each in another one, Q4_1 and F16 gate / up pairs
+        // a format per matrix: q, k and v in different ones, Q4_1 and F16 gate / up pairs, F32 q
+        // and ffn_down, a Q6_K attention output
         p.n_vocab = 512; p.n_embd = 256; p.n_ff = 512; p.n_layer = 2; p.n_head = 4; p.n_kv_head = 2;
         p.rope_theta = 500000.0f;
         p.overrides = {{0, "attn_q", GGML_F16},      {0, "attn_k", GGML_Q4_0},   {0, "attn_v", GGML_Q4_1},
-                       {0, "attn_output", GGML_Q4_0}, {0, "ffn_gate", GGML_Q4_1}, {0, "ffn_up", GGML_Q4_1},
-                       {0, "ffn_down", GGML_F16},     {1, "attn_output", GGML_Q4_1}, {1, "ffn_gate", GGML_F16},
-                       {1, "ffn_up", GGML_F16},       {1, "ffn_down", GGML_Q4_0}};
+                       {0, "attn_output", GGML_Q6_K}, {0, "ffn_gate", GGML_Q4_1}, {0, "ffn_up", GGML_Q4_1},
+                       {0, "ffn_down", GGML_F16},     {1, "attn_q", GGML_F32},    {1, "attn_output", GGML_Q4_1},
+                       {1, "ffn_gate", GGML_F16},     {1, "ffn_up", GGML_F16},    {1, "ffn_down", GGML_F32}};
     } else if (name == "tiny_qwen") {
         p.arch = "qwen2";
         p.n_vocab = 640; p.n_embd = 192; p.n_ff = 320; p.n_layer = 2; p.n_head = 6; p.n_kv_head = 1;

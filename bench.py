@@ -283,14 +283,11 @@ def gpu_config(pkg, key, desc, preset, n_prompt, n_dec, max_seq, layout, runs, w
     }
 
 
-def prefill_leg(pkg, threads, reps=5):
-    """The 512-token prompt of the Llama-3.2-1B shape on the matrix cores: device ms from HIP
-    events around the call's kernels, median of `reps` prefills from a reset. The first prompt
-    of a context also packs every layer matrix's integers as fp16 fragments once (kept for
-    the context's life): its time is the first call's wall time minus the later calls'
-    median, its memory 2 bytes per weight."""
-    path, info = ensure_model(pkg, "llama1b_q8", threads)
-    n = 512
+def prefill_run(pkg, preset, threads, n, reps):
+    """Median device ms (HIP events around the call's kernels) and wall ms of `reps` prefills
+    of the n-token prompt from a reset, after a first prompt that allocates the chunk buffers
+    (its extra wall time is returned too)."""
+    path, info = ensure_model(pkg, preset, threads)
     prompt = pkg.synth_prompt(info["seed"], n, info["n_vocab"])
     m = pkg.HipModel(path, max_seq=1024, kv_layout=0)
     t0 = time.perf_counter()
@@ -305,25 +302,30 @@ def prefill_leg(pkg, threads, reps=5):
         dev.append(m.last_timing()[0])
     name = m.last_timing()[3]
     m.close()
+    return info, name, statistics.median(dev), statistics.median(wall), first_wall * 1e3 - statistics.median(wall)
+
+
+def prefill_leg(pkg, threads, reps=5):
+    """The 512-token prompt of the Llama-3.2-1B shape on the matrix cores (Q8_0, and the
+    Q4_0 / Q4_1 mix of the same shape), the layer matrices read in their HBM layout."""
+    n = 512
+    info, name, d_ms, w_ms, first_extra = prefill_run(pkg, "llama1b_q8", threads, n, reps)
+    _, name4, d4_ms, w4_ms, _ = prefill_run(pkg, "llama1b_mixq4", threads, n, reps)
     flops, dense = prefill_flops(info, n)
-    d_ms = statistics.median(dev)
     tflops = flops / (d_ms * 1e-3) / 1e12
-    D, F, L, H, G = info["n_embd"], info["n_ff"], info["n_layer"], info["n_head"], info["n_kv_head"]
-    hd = D // H
-    weights = L * (D * (H * hd + 2 * G * hd) + H * hd * D + 3 * D * F)
     return {
         "workload": f"{n}-token prompt (uniform ids, seed {info['seed']}) of the Llama-3.2-1B shape, max-seq 1024",
-        "path": name, "tokens": n, "device_ms": round(d_ms, 3), "wall_ms": round(statistics.median(wall), 3),
+        "path": name, "tokens": n, "device_ms": round(d_ms, 3), "wall_ms": round(w_ms, 3),
         "tok_s": round(n / (d_ms * 1e-3), 1), "tflop": round(flops / 1e12, 4), "dense_tflop": round(dense / 1e12, 4),
         "achieved_tflop_s": round(tflops, 2), "mfma_peak_tflop_s": MFMA_F16_PEAK_TFLOPS,
         "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
         "mfma_note": "algorithmic FLOP/s over the dense fp16 MFMA peak; the GEMMs issue two fp16 MFMAs "
                      "(activation hi and lo) per algorithmic product, attention three fp16 MFMAs per "
                      "product (fp16 operand pairs)",
-        "weight_pack": {"ms": round(first_wall * 1e3 - statistics.median(wall), 1),
-                        "bytes": 2 * weights,
-                        "note": "one-time per context, excluded from device_ms: layer matrices' integers as fp16 "
-                                "fragments (first prompt's wall time minus the later prompts' median)"},
+        "first_prompt_extra_ms": round(first_extra, 1),
+        "mixq4": {"path": name4, "device_ms": round(d4_ms, 3), "wall_ms": round(w4_ms, 3),
+                  "tok_s": round(n / (d4_ms * 1e-3), 1),
+                  "note": "the same prompt on the Q4_0 layer matrices (Q4_1 ffn_down in layers 0 and 15)"},
     }
 
 

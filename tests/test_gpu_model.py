@@ -206,9 +206,9 @@ def test_small_models_token_prefill(pkg, gguf, preset, layout):
 @pytest.mark.parametrize("preset,want", [("tiny_q8", MFMA), ("tiny_qwen", MFMA), ("small_q8", MFMA),
                                          ("tiny_f32", TOKENS), ("tiny_mixq4", MFMA), ("tiny_mixfmt", MFMA)])
 def test_prefill_path_selection(pkg, gguf, preset, want):
-    """Prompts run on the matrix cores when every layer matrix is Q8_0, Q4_0, Q4_1 or F16
-    with tileable shapes (gate and up in one format); F32 models keep the per-token path;
-    PREFILL_TOKENS forces it."""
+    """Prompts run on the matrix cores when every layer matrix is Q8_0, Q4_0, Q4_1, F16,
+    F32 or Q6_K with rows of a multiple of 64 (256 for Q6_K; gate and up in one format);
+    tiny_f32's rows of 32 keep the per-token path; PREFILL_TOKENS forces it."""
     hip = pkg.HipModel(gguf(preset), max_seq=64)
     assert hip.prefill_path() == want
     hip.set_prefill_path(TOKENS)
@@ -244,9 +244,10 @@ def test_prefill_paths_agree(pkg, gguf):
 @pytest.mark.parametrize("n_prompt", [6, 150])
 @pytest.mark.parametrize("preset", ["tiny_mixq4", "tiny_mixfmt"])
 def test_mixed_format_prefill(pkg, gguf, preset, n_prompt):
-    """Q4_0 / Q4_1 / F16 / Q8_0 layer matrices on the matrix cores against the oracle
-    (tiny_mixfmt: q, k and v in three formats, one launch each; Q4_1 and F16 gate / up),
-    and against the per-token prefill of the same prompt."""
+    """Q4_0 / Q4_1 / F16 / F32 / Q6_K / Q8_0 layer matrices on the matrix cores against the
+    oracle (tiny_mixfmt: q, k and v in different formats, one launch each; Q4_1 and F16
+    gate / up; F32 q and ffn_down; a Q6_K attention output), and against the per-token
+    prefill of the same prompt."""
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"] + 3, n_prompt, info["n_vocab"])
     hip = pkg.HipModel(gguf(preset), max_seq=256)

@@ -122,15 +122,17 @@ PF_GEMM_SHAPES = [(2, 64, 16), (37, 2048, 256), (64, 896, 1152), (100, 8192, 128
 
 
 # the other formats the matrix cores take, read in their own layout: the register-streamed
-# tiles, the LDS-staged tiles (500 x 256 x 16384) and K split in slices (512 x 2048 x 2048)
-PF_GEMM_FMT_SHAPES = [(t, m, k, n) for t in (2, 3, 1)
+# tiles, the LDS-staged tiles (500 x 256 x 16384) and K split in slices (512 x 2048 x 2048);
+# F32 (0) and Q6_K (14, rows of a multiple of 256) always on their register-streamed tiles
+PF_GEMM_FMT_SHAPES = [(t, m, k, n) for t in (2, 3, 1, 0, 14)
                       for (m, k, n) in [(2, 64, 16), (37, 2048, 256), (130, 1536, 48), (7, 192, 320),
-                                        (500, 256, 16384), (512, 2048, 2048)]]
+                                        (500, 256, 16384), (512, 2048, 2048)]
+                      if t != 14 or k % 256 == 0]
 
 
 @pytest.mark.parametrize("t,m,k,n", [(8, m, k, n) for (m, k, n) in PF_GEMM_SHAPES] + PF_GEMM_FMT_SHAPES)
 def test_prefill_gemm_matches_oracle(pkg, t, m, k, n):
-    """Q8_0, Q4_0, Q4_1 or F16 rows x M activation rows on the matrix cores: |y - y_oracle|
+    """Q8_0, Q4_0, Q4_1, F16, F32 or Q6_K rows x M activation rows on the matrix cores: |y - y_oracle|
     <= 2e-5 * sum_k |x_k w_nk| per output. The fp16 pair of an activation keeps it to 2^-22
     of its row's largest element; the rest is fp32 reassociation, as for the GEMV."""
     rng = np.random.default_rng(2000 + m + k + n + t)
@@ -143,10 +145,11 @@ def test_prefill_gemm_matches_oracle(pkg, t, m, k, n):
     assert np.all(err <= 2e-5 * budget + 1e-30), f"max err/budget {np.max(err / (budget + 1e-30)):.3e}"
 
 
-@pytest.mark.parametrize("t", [8, 2, 3, 1])
+@pytest.mark.parametrize("t", [8, 2, 3, 1, 0, 14])
 def test_prefill_gemm_single_element_rows(pkg, t):
     """A row with one non-zero x_j gives x_j * w[:, j] (one product per output; Q4_1's
-    d n + m as d (x n) + m x, which the oracle's fp32 dequant rounds once: within 2 ulp)."""
+    d n + m as d (x n) + m x, which the oracle's fp32 dequant rounds once: within 2 ulp;
+    Q6_K's d (x sc q), where the dequant rounds d sc q: within 2 ulp)."""
     rng = np.random.default_rng(90 + t)
     k, n = 256, 4096  # 500 rows below: the LDS-staged kernel
     rows = random_rows(rng, t, k, n)
@@ -164,6 +167,8 @@ def test_prefill_gemm_single_element_rows(pkg, t):
         xa = np.abs(x[np.arange(500), js].astype(np.float64))[:, None]
         bound = 2.0**-22 * xa * (np.abs(deq[:, js].T - mj) + np.abs(mj))
         assert np.all(np.abs(got.astype(np.float64) - want) <= bound + 1e-30)
+    elif t == 14:
+        assert np.all(np.abs(got.astype(np.float64) - want) <= 2.0**-22 * np.abs(want) + 1e-30)
     else:
         assert np.array_equal(got, want)
 
