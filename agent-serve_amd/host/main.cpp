@@ -4,7 +4,8 @@
 // --prompt through the byte-level BPE tokenizer (BOS unless --no-bos), prefill, then up to
 // --n-predict tokens sampled on the GPU (greedy at --temp 0, else temperature / top-p with
 // the reference's std::mt19937 draws), stopping when the sampled id is eos after the first
-// (main.cpp:112-122); prefill/decode rates on stderr. Adds --device and --decode-path.
+// (main.cpp:112-122); prefill/decode rates on stderr. Adds --device and --decode-path, and
+// TF_HIP_MAPS_AT_EXIT (below).
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -172,6 +173,17 @@ int main(int argc, char** argv) {
         }
     } catch (const std::exception& e) {
         die(e.what());
+    }
+    // TF_HIP_MAPS_AT_EXIT=<file>: the process's memory map once the model is gone, for
+    // placing the addresses of a crash in library teardown after main returns
+    if (const char* maps_out = std::getenv("TF_HIP_MAPS_AT_EXIT")) {
+        FILE* in = std::fopen("/proc/self/maps", "r");
+        FILE* out = in ? std::fopen(maps_out, "w") : nullptr;
+        char buf[4096];
+        size_t n;
+        while (out && (n = std::fread(buf, 1, sizeof(buf), in)) > 0) std::fwrite(buf, 1, n, out);
+        if (out) std::fclose(out);
+        if (in) std::fclose(in);
     }
     return 0;
 }

@@ -3,6 +3,8 @@
     python3 agent-serve_amd/profsum.py trace <kernel_stats.csv> [--steps K]
     python3 agent-serve_amd/profsum.py steps <kernel_trace.csv>
     python3 agent-serve_amd/profsum.py stepcounters <fetch counter_collection.csv> <write counter_collection.csv>
+        --copy-fetch <csv> --copy-write <csv> [--copy-bytes N] [--kernel k_step|k_ring]
+    python3 agent-serve_amd/profsum.py digest
     python3 agent-serve_amd/profsum.py traffic <fetch counter_collection.csv> <write counter_collection.csv>
         --copy-bytes N
     python3 agent-serve_amd/profsum.py prefill <kernel_trace.csv> --tokens N --dims D,F,L,H,G
@@ -11,15 +13,48 @@
 run. `traffic` turns the FETCH_SIZE and WRITE_SIZE counters (KiB per dispatch, one
 --pmc run each) into HBM bytes per dispatch, each scaled by what the same counter reads
 for k_copy_stream, which reads N bytes and writes N bytes; the last line,
-`traffic_bytes_per_launch <kernel> <bytes>`, is what bench.py reads back.
+`traffic_bytes_per_launch <kernel> <bytes>`, is what bench.py reads back. `stepcounters`
+does the same for the persistent decode kernel (`traffic_bytes_per_token <kernel> <bytes>`)
+with the scale factors of a separate k_copy_stream run, and ends with the provenance lines
+bench.py checks: `commit <sha>` and `csrc_sha256 <digest of the kernel sources>`.
 """
 from __future__ import annotations
 
 import argparse
 import collections
 import csv
+import hashlib
+import pathlib
 import re
+import subprocess
 import sys
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def kernel_source_digest() -> str:
+    """sha256 (first 16 hex digits) of the kernel sources (agent-serve_amd/csrc/*) and the
+    ABI header: a counter summary records the digest of the build it measured, and bench.py
+    uses a summary's figures only while the digest is that of the sources it runs."""
+    h = hashlib.sha256()
+    files = sorted((ROOT / "agent-serve_amd" / "csrc").glob("*")) + [ROOT / "include" / "tf_hip.h"]
+    for f in files:
+        if f.is_file():
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def provenance(commit: str | None) -> None:
+    """The lines bench.py reads back: the commit measured and the kernel-source digest."""
+    if not commit:
+        try:
+            commit = subprocess.run(["git", "-C", str(ROOT), "rev-parse", "--short=12", "HEAD"], capture_output=True,
+                                    text=True, check=True).stdout.strip()
+        except (OSError, subprocess.CalledProcessError):
+            commit = "unknown"
+    print(f"commit {commit}")
+    print(f"csrc_sha256 {kernel_source_digest()}")
 
 
 def short(name: str) -> str:
@@ -52,20 +87,31 @@ def step_dispatches(trace_csv: str) -> list[float]:
     return out
 
 
-def step_counters(fetch_csv: str, write_csv: str) -> None:
-    """HBM bytes per decode token of the persistent step kernel from a run of the CLI
-    (the prompt on the matrix cores, then one step-kernel launch per decoded token): the
-    median over the launches after the first, FETCH_SIZE scaled by 2.0 and WRITE_SIZE by
-    1.0 (the factors k_copy_stream of a known size gives these counters on MI355X)."""
+def copy_scales(fetch_csv: str, write_csv: str, copy_bytes: int) -> tuple[float, float]:
+    """FETCH_SIZE and WRITE_SIZE scale factors: bytes over the counter's KiB for
+    k_copy_stream, which reads copy_bytes and writes copy_bytes per dispatch."""
+    f = counter_means(fetch_csv, "FETCH_SIZE")
+    w = counter_means(write_csv, "WRITE_SIZE")
+    fk = next(k for k in f if "k_copy_stream" in k)
+    wk = next(k for k in w if "k_copy_stream" in k)
+    return copy_bytes / (f[fk][1] * 1024.0), copy_bytes / (w[wk][1] * 1024.0)
+
+
+def step_counters(fetch_csv: str, write_csv: str, f_scale: float, w_scale: float, kernel: str = "k_step") -> None:
+    """HBM bytes per decode token of a persistent decode kernel (k_step or k_ring) from a
+    run of the CLI (the prompt, then one launch per decoded token): the median over the
+    launches after the first, FETCH_SIZE and WRITE_SIZE scaled by the copy kernel's
+    factors."""
     def vals(p, c):
         return [float(r["Counter_Value"]) for r in csv.DictReader(open(p))
-                if r["Counter_Name"] == c and "k_step" in r["Kernel_Name"]]
+                if r["Counter_Name"] == c and kernel in r["Kernel_Name"]]
     f, w = vals(fetch_csv, "FETCH_SIZE"), vals(write_csv, "WRITE_SIZE")
     fm, wm = sorted(f[1:])[len(f[1:]) // 2], sorted(w[1:])[len(w[1:]) // 2]
-    print(f"k_step dispatches: {len(f)} (one per decoded token; the first, a cold start, is left out of the medians)")
+    print(f"{kernel} dispatches: {len(f)} (one per decoded token; the first, a cold start, is left out of the medians)")
     print(f"decode dispatches: FETCH_SIZE median {fm:.0f} KiB (min {min(f[1:]):.0f}, max {max(f[1:]):.0f}), "
           f"WRITE_SIZE median {wm:.0f} KiB (min {min(w[1:]):.0f}, max {max(w[1:]):.0f})")
-    print(f"traffic_bytes_per_token k_step {fm * 1024 * 2.0 + wm * 1024 * 1.0:.0f}")
+    print(f"scale factors (k_copy_stream): FETCH_SIZE x {f_scale:.4f}, WRITE_SIZE x {w_scale:.4f}")
+    print(f"traffic_bytes_per_token {kernel} {fm * 1024 * f_scale + wm * 1024 * w_scale:.0f}")
 
 
 def pf_classifier():
@@ -197,8 +243,12 @@ def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> None:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["trace", "traffic", "steps", "stepcounters", "prefill", "mfma"])
-    ap.add_argument("files", nargs="+")
+    ap.add_argument("what", choices=["trace", "traffic", "steps", "stepcounters", "prefill", "mfma", "digest"])
+    ap.add_argument("files", nargs="*")
+    ap.add_argument("--copy-fetch", help="FETCH_SIZE counter csv of the k_copy_stream calibration run")
+    ap.add_argument("--copy-write", help="WRITE_SIZE counter csv of the k_copy_stream calibration run")
+    ap.add_argument("--kernel", default="k_step", help="stepcounters: the decode kernel (k_step or k_ring)")
+    ap.add_argument("--commit", default=None, help="commit measured (default: git HEAD)")
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--tokens", type=int, default=512)
@@ -210,10 +260,16 @@ def main() -> int:
         trace(a.files[0], a.steps)
     elif a.what == "prefill":
         prefill(a.files[0], a.tokens, a.dims)
+        provenance(a.commit)
     elif a.what == "mfma":
         mfma(a.files[0], a.simds, a.xcds)
+        provenance(a.commit)
     elif a.what == "stepcounters":
-        step_counters(a.files[0], a.files[1])
+        fs, ws = copy_scales(a.copy_fetch, a.copy_write, a.copy_bytes)
+        step_counters(a.files[0], a.files[1], fs, ws, a.kernel)
+        provenance(a.commit)
+    elif a.what == "digest":
+        provenance(a.commit)
     elif a.what == "steps":
         for i, d in enumerate(step_dispatches(a.files[0])):
             print(f"k_step dispatch {i}: {d:9.1f} us")

@@ -137,17 +137,13 @@ def ensure_model(pkg, preset: str, threads: int):
 
 
 def kernel_source_digest() -> str:
-    """sha256 (first 16 hex digits) of the kernel sources (agent-serve_amd/csrc/*) and the
-    ABI header: the counter summaries record the digest of the build they measured."""
-    import hashlib
+    """The kernel-source digest the counter summaries record (profsum.kernel_source_digest)."""
+    import importlib.util
 
-    h = hashlib.sha256()
-    files = sorted((ROOT / "agent-serve_amd" / "csrc").glob("*")) + [ROOT / "include" / "tf_hip.h"]
-    for f in files:
-        if f.is_file():
-            h.update(f.name.encode())
-            h.update(f.read_bytes())
-    return h.hexdigest()[:16]
+    spec = importlib.util.spec_from_file_location("profsum", ROOT / "agent-serve_amd" / "profsum.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.kernel_source_digest()
 
 
 def measured_traffic(key: str, tokens: int, kernel: str):
