@@ -53,8 +53,9 @@ void usage() {
                  "  --kv-layout seq|head override KV layout\n"
                  "  --no-bos             do not prepend BOS\n"
                  "  --device N           HIP device (default 0)\n"
-                 "  --decode-path P      step (persistent kernel, the default) | graph; a step kernel the\n"
-                 "                       GPU refuses (another process holds it) runs as graph\n"
+                 "  --decode-path P      step (persistent kernel, the default) | graph | ring (the\n"
+                 "                       LDS-ring kernel, Q8_0 models); a persistent kernel the GPU\n"
+                 "                       refuses (another process holds it) runs as graph\n"
                  "  --profile            print the per-kernel-class breakdown of one greedy pass\n");
 }
 
@@ -122,11 +123,13 @@ int main(int argc, char** argv) {
         Model model(model_path, cfg);
         const Tokenizer tok(model.gguf());
         // without the flag the library's choice stands (step, or TF_HIP_DECODE_PATH)
-        if (decode_path == "graph" || decode_path == "step") {
-            if (tf_hip_set_decode_path(model.ctx(), decode_path == "graph" ? TF_HIP_PATH_GRAPH : TF_HIP_PATH_STEP))
-                die("tf_hip_set_decode_path failed");
+        if (decode_path == "graph" || decode_path == "step" || decode_path == "ring") {
+            const int path = decode_path == "graph" ? TF_HIP_PATH_GRAPH
+                             : decode_path == "ring" ? TF_HIP_PATH_RING
+                                                     : TF_HIP_PATH_STEP;
+            if (tf_hip_set_decode_path(model.ctx(), path)) die("tf_hip_set_decode_path failed");
         } else if (!decode_path.empty()) {
-            die("--decode-path takes step or graph");
+            die("--decode-path takes step, graph or ring");
         }
         std::fprintf(stderr, "%s\n", model.describe().c_str());
         const std::vector<int> ids = !token_str.empty() ? parse_tokens(token_str) : tok.encode(prompt, add_bos);
@@ -174,6 +177,8 @@ int main(int argc, char** argv) {
     } catch (const std::exception& e) {
         die(e.what());
     }
+    // the process owns the device: release it before the runtime's own teardown at exit
+    (void)tf_hip_release_device(device);
     // TF_HIP_MAPS_AT_EXIT=<file>: the process's memory map once the model is gone, for
     // placing the addresses of a crash in library teardown after main returns
     if (const char* maps_out = std::getenv("TF_HIP_MAPS_AT_EXIT")) {
