@@ -1034,22 +1034,6 @@ int tf_hip_destroy(tf_hip_ctx* c) {
     return 0;
 }
 
-}  // extern "C"
-
-namespace {
-void forget_scratch(int device);  // the no-alloc entry point's cached array address
-}  // namespace
-
-extern "C" {
-
-int tf_hip_release_device(int device) {
-    int n = 0;
-    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return TF_HIP_EINVAL;
-    if (hipSetDevice(device) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return TF_HIP_EDEVICE;
-    forget_scratch(device);
-    return hipDeviceReset() == hipSuccess ? 0 : TF_HIP_EDEVICE;
-}
-
 int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne1, const void* host, size_t nbytes) {
     if (!c) return TF_HIP_EINVAL;
     const tf_hip_hparams& p = c->hp;
@@ -1698,13 +1682,6 @@ int scratch_on(int device, hipStream_t st, float** out) {
     }
     *out = g_scratch_ptr[device];
     return 0;
-}
-
-// After a device reset the array's address is stale: the next use looks it up again.
-void forget_scratch(int device) {
-    if (device < 0 || device >= kMaxDevices) return;
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    g_scratch_ptr[device] = nullptr;
 }
 
 }  // namespace

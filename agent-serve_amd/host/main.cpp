@@ -177,8 +177,6 @@ int main(int argc, char** argv) {
     } catch (const std::exception& e) {
         die(e.what());
     }
-    // the process owns the device: release it before the runtime's own teardown at exit
-    (void)tf_hip_release_device(device);
     // TF_HIP_MAPS_AT_EXIT=<file>: the process's memory map once the model is gone, for
     // placing the addresses of a crash in library teardown after main returns
     if (const char* maps_out = std::getenv("TF_HIP_MAPS_AT_EXIT")) {

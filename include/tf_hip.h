@@ -86,14 +86,6 @@ int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out);
 int tf_hip_destroy(tf_hip_ctx* ctx);
 const char* tf_hip_last_error(const tf_hip_ctx* ctx);
 
-/* Releases everything the process holds on `device` (hipDeviceReset). Every context on it
- * must be destroyed first, and nothing in the process may use the device afterwards: for a
- * program that owns the process, just before it exits (tinferno_hip calls it). The HIP
- * runtime's own teardown at exit then finds no device state to release; under rocprofv3
- * that teardown faulted inside the HSA runtime in processes that had made cooperative
- * launches. No counterpart in the reference (a CPU program). */
-int tf_hip_release_device(int device);
-
 /* Copies one GGUF tensor (raw GGUF row bytes, ne0 = row length, ne1 = rows) to HBM and
  * converts it to the backend's layout. Replaces the mmap binding of model.cpp:43-65. */
 int tf_hip_upload_tensor(tf_hip_ctx* ctx, int slot, int ggml_type, int64_t ne0, int64_t ne1, const void* host,
