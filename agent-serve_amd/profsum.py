@@ -5,8 +5,10 @@
     python3 agent-serve_amd/profsum.py stepcounters <fetch counter_collection.csv> <write counter_collection.csv>
         --copy-fetch <csv> --copy-write <csv> [--copy-bytes N] [--kernel k_step|k_ring]
     python3 agent-serve_amd/profsum.py digest
+    python3 agent-serve_amd/profsum.py decodetrace <kernel_stats.csv> <kernel_trace.csv> [--kernel k_step|k_ring]
+        [--algo-bytes B]
     python3 agent-serve_amd/profsum.py traffic <fetch counter_collection.csv> <write counter_collection.csv>
-        --copy-bytes N
+        --copy-bytes N [--copy-fetch <csv> --copy-write <csv>]
     python3 agent-serve_amd/profsum.py prefill <kernel_trace.csv> --tokens N --dims D,F,L,H,G
 
 `trace` lists each kernel's calls and average / min duration from a --kernel-trace --stats
@@ -209,6 +211,28 @@ def trace(path: str, steps: int | None) -> None:
               f"{float(r['MinNs']) / 1e3:9.2f} {float(r['TotalDurationNs']) / 1e6:9.3f}")
 
 
+def decode_trace(stats_csv: str, trace_csv: str, kernel: str, algo_bytes: float | None) -> None:
+    """A decode run of the CLI (one launch of the persistent kernel per decoded token): the
+    kernel table, every dispatch of `kernel` in launch order, their median after the first
+    (a cold start) and, given the algorithmic bytes per token, the rate and its share of
+    8 TB/s."""
+    trace(stats_csv, None)
+    d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in csv.DictReader(open(trace_csv))
+         if kernel in r["Kernel_Name"]]
+    print()
+    print(f"Per {kernel} dispatch (us), in launch order (one decoded token each):")
+    for i in range(0, len(d), 16):
+        print(" ".join(f"{v:.1f}" for v in d[i:i + 16]))
+    rest = sorted(d[1:])
+    med = rest[len(rest) // 2]
+    line = f"{kernel} dispatches after the first: median {med:.1f} us ({rest[0]:.1f}-{rest[-1]:.1f})"
+    if algo_bytes:
+        tbs = algo_bytes / (med * 1e-6) / 1e12
+        line += f"; algorithmic bytes per token {algo_bytes:,.0f}: {tbs:.2f} TB/s, {tbs / 8.0:.1%} of 8 TB/s"
+    print(line + ".")
+    print(f"median_us {kernel} {med:.1f}")
+
+
 def counter_means(path: str, counter: str) -> dict[str, tuple[int, float]]:
     """Mean counter value per kernel name; for k_step (one launch per call, calls of
     different token counts) the largest dispatch, which is the longest generate call."""
@@ -219,14 +243,20 @@ def counter_means(path: str, counter: str) -> dict[str, tuple[int, float]]:
     return {k: (len(v), max(v) if "k_step" in k else sum(v) / len(v)) for k, v in acc.items()}
 
 
-def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> None:
+def traffic(fetch_csv: str, write_csv: str, copy_bytes: int, scales: tuple[float, float] | None = None) -> None:
+    """Per kernel: HBM bytes per dispatch. The scale factors come from k_copy_stream in the
+    same files, or from a separate calibration run (scales)."""
     fetch = counter_means(fetch_csv, "FETCH_SIZE")
     write = counter_means(write_csv, "WRITE_SIZE")
-    copy_key = next(k for k in fetch if "k_copy_stream" in k)
-    f_scale = copy_bytes / (fetch[copy_key][1] * 1024.0)
-    w_scale = copy_bytes / (write[copy_key][1] * 1024.0)
-    print(f"k_copy_stream of {copy_bytes} bytes: FETCH_SIZE {fetch[copy_key][1]:.0f} KiB, "
-          f"WRITE_SIZE {write[copy_key][1]:.0f} KiB -> scale fetch {f_scale:.4f}, write {w_scale:.4f}")
+    copy_key = next((k for k in fetch if "k_copy_stream" in k), None)
+    if scales:
+        f_scale, w_scale = scales
+        print(f"scale factors (k_copy_stream of {copy_bytes} bytes, separate run): fetch {f_scale:.4f}, write {w_scale:.4f}")
+    else:
+        f_scale = copy_bytes / (fetch[copy_key][1] * 1024.0)
+        w_scale = copy_bytes / (write[copy_key][1] * 1024.0)
+        print(f"k_copy_stream of {copy_bytes} bytes: FETCH_SIZE {fetch[copy_key][1]:.0f} KiB, "
+              f"WRITE_SIZE {write[copy_key][1]:.0f} KiB -> scale fetch {f_scale:.4f}, write {w_scale:.4f}")
     print(f"{'kernel':60s} {'n':>5s} {'fetch_KiB':>11s} {'write_KiB':>10s} {'hbm_bytes':>12s}")
     for k, (n, f) in sorted(fetch.items(), key=lambda kv: -kv[1][1]):
         if k == copy_key:
@@ -243,11 +273,13 @@ def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> None:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["trace", "traffic", "steps", "stepcounters", "prefill", "mfma", "digest"])
+    ap.add_argument("what", choices=["trace", "traffic", "steps", "stepcounters", "prefill", "mfma", "digest",
+                                     "decodetrace"])
+    ap.add_argument("--algo-bytes", type=float, default=None, help="decodetrace: algorithmic bytes per token")
     ap.add_argument("files", nargs="*")
     ap.add_argument("--copy-fetch", help="FETCH_SIZE counter csv of the k_copy_stream calibration run")
     ap.add_argument("--copy-write", help="WRITE_SIZE counter csv of the k_copy_stream calibration run")
-    ap.add_argument("--kernel", default="k_step", help="stepcounters: the decode kernel (k_step or k_ring)")
+    ap.add_argument("--kernel", default="k_step", help="stepcounters, decodetrace: the decode kernel (k_step or k_ring)")
     ap.add_argument("--commit", default=None, help="commit measured (default: git HEAD)")
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
@@ -258,6 +290,10 @@ def main() -> int:
     a = ap.parse_args()
     if a.what == "trace":
         trace(a.files[0], a.steps)
+        provenance(a.commit)
+    elif a.what == "decodetrace":
+        decode_trace(a.files[0], a.files[1], a.kernel, a.algo_bytes)
+        provenance(a.commit)
     elif a.what == "prefill":
         prefill(a.files[0], a.tokens, a.dims)
         provenance(a.commit)
@@ -274,7 +310,9 @@ def main() -> int:
         for i, d in enumerate(step_dispatches(a.files[0])):
             print(f"k_step dispatch {i}: {d:9.1f} us")
     else:
-        traffic(a.files[0], a.files[1], a.copy_bytes)
+        scales = copy_scales(a.copy_fetch, a.copy_write, a.copy_bytes) if a.copy_fetch and a.copy_write else None
+        traffic(a.files[0], a.files[1], a.copy_bytes, scales)
+        provenance(a.commit)
     return 0
 
 
