@@ -4,8 +4,8 @@
 // --prompt through the byte-level BPE tokenizer (BOS unless --no-bos), prefill, then up to
 // --n-predict tokens sampled on the GPU (greedy at --temp 0, else temperature / top-p with
 // the reference's std::mt19937 draws), stopping when the sampled id is eos after the first
-// (main.cpp:112-122); prefill/decode rates on stderr. Adds --device and --decode-path, and
-// TF_HIP_MAPS_AT_EXIT (below).
+// (main.cpp:112-122); prefill/decode rates on stderr. Adds --device, --decode-path,
+// --device-loop and TF_HIP_MAPS_AT_EXIT (below).
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -56,6 +56,8 @@ void usage() {
                  "  --decode-path P      step (persistent kernel, the default) | graph | ring (the\n"
                  "                       LDS-ring kernel, Q8_0 models); a persistent kernel the GPU\n"
                  "                       refuses (another process holds it) runs as graph\n"
+                 "  --device-loop        greedy tokens from one tf_hip_generate call (one launch of the\n"
+                 "                       persistent kernel, as bench.py times it) instead of a decode per token\n"
                  "  --profile            print the per-kernel-class breakdown of one greedy pass\n");
 }
 
@@ -74,7 +76,7 @@ int main(int argc, char** argv) {
     std::string model_path, prompt, token_str, stage = "v2", kv_layout, decode_path;
     int n_predict = 64, seed = 42, max_seq = 4096, device = 0;
     float temp = 0, topp = 0.9f;
-    bool profile = false, add_bos = true;
+    bool profile = false, add_bos = true, device_loop = false;
     for (int i = 1; i < argc; ++i) {
         std::string a = argv[i];
         auto next = [&]() -> std::string {
@@ -94,6 +96,7 @@ int main(int argc, char** argv) {
         else if (a == "--kv-layout") kv_layout = next();
         else if (a == "--device") device = std::stoi(next());
         else if (a == "--decode-path") decode_path = next();
+        else if (a == "--device-loop") device_loop = true;
         else if (a == "--no-bos") add_bos = false;
         else if (a == "--pin") {
         } else if (a == "--profile") profile = true;
@@ -143,13 +146,27 @@ int main(int argc, char** argv) {
         std::mt19937 rng((unsigned)seed);
         std::vector<int> gen;
         t0 = now_s();
-        for (int i = 0; i < n_predict; ++i) {
-            const int id = model.sample(temp, topp, rng);
-            if (id == model.eos() && i > 0) break;
-            gen.push_back(id);
-            std::fputs(tok.decode_one(id).c_str(), stdout);
+        if (device_loop) {
+            // the greedy loop as one tf_hip_generate call (one launch of the persistent kernel),
+            // the tokens printed up to the first eos after the first token
+            if (temp > 0) die("--device-loop needs --temp 0");
+            std::vector<int32_t> out((size_t)std::max(n_predict, 0));
+            if (n_predict > 0) model.generate(n_predict, out.data());
+            for (int i = 0; i < n_predict; ++i) {
+                if (out[(size_t)i] == model.eos() && i > 0) break;
+                gen.push_back(out[(size_t)i]);
+                std::fputs(tok.decode_one(out[(size_t)i]).c_str(), stdout);
+            }
             std::fflush(stdout);
-            model.decode(id, nullptr);
+        } else {
+            for (int i = 0; i < n_predict; ++i) {
+                const int id = model.sample(temp, topp, rng);
+                if (id == model.eos() && i > 0) break;
+                gen.push_back(id);
+                std::fputs(tok.decode_one(id).c_str(), stdout);
+                std::fflush(stdout);
+                model.decode(id, nullptr);
+            }
         }
         const double t_decode = now_s() - t0;
         std::fputc('\n', stdout);

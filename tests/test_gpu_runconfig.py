@@ -76,6 +76,17 @@ def test_cli_stage_v5_runs_head_major(pkg, gguf):
     assert v5.stdout.strip() and v5.stdout == head.stdout == v2.stdout
 
 
+def test_cli_device_loop_prints_the_loop_tokens(pkg, gguf):
+    """tinferno_hip --device-loop (the greedy tokens from one tf_hip_generate call, as bench.py
+    runs them) prints the tokens of the reference's decode-per-token loop."""
+    path, toks, env = _cli_case(pkg, gguf)
+    exe = str(pkg.BIN_DIR / "tinferno_hip")
+    base = [exe, "--model", path, "--tokens", toks, "--n-predict", "24", "--max-seq", "64"]
+    loop = _run(base, env)
+    dev = _run(base + ["--device-loop"], env)
+    assert loop.stdout.strip() and dev.stdout == loop.stdout
+
+
 def test_patched_reference_stage_v5_runs_head_major(pkg, gguf):
     """The reference's own CLI with the backend switch (oracle/backend_patch.py): with
     --backend hip, --stage v5 hands the head-major layout to tf_hip_create, and the tokens
