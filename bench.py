@@ -162,7 +162,7 @@ def measured_traffic(key: str, tokens: int, kernel: str):
                 meta[f[0]] = f[1]
     except (OSError, AttributeError):
         return None, None
-    src = {"summary": str(path.relative_to(ROOT)), "commit": meta.get("commit"),
+    src = {"summary": os.path.relpath(path, ROOT), "commit": meta.get("commit"),
            "csrc_sha256": meta.get("csrc_sha256"),
            "current": meta.get("csrc_sha256") == kernel_source_digest()}
     if per_token is None or not src["current"]:

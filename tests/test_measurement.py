@@ -135,3 +135,40 @@ def test_stream_checksum_closed_form(pkg):
         n = nbytes // 16 * 4
         words = (np.arange(n, dtype=np.uint64) * np.uint64(0x9E3779B1)) % np.uint64(1 << 32)
         assert pkg.stream_checksum(nbytes) == int(words.sum() % np.uint64(1 << 32)), nbytes
+
+
+def _load(name, path):
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_traffic_summaries_are_of_these_sources(tmp_path, monkeypatch):
+    """bench.py takes a config's roofline.traffic from its counter summary only while the
+    summary's kernel-source digest is that of the sources it runs: the committed summaries
+    carry profsum's digest of this tree, a summary with another digest gives no traffic, and
+    the figure is the per-token bytes x tokens."""
+    import pathlib
+    import sys
+    root = pathlib.Path(__file__).resolve().parents[1]
+    monkeypatch.setattr(sys, "argv", ["bench.py"])
+    bench = _load("bench_for_test", root / "bench.py")
+    profsum = _load("profsum_for_test", root / "agent-serve_amd" / "profsum.py")
+    digest = profsum.kernel_source_digest()
+    assert bench.kernel_source_digest() == digest
+    for key in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5"):
+        traffic, src = bench.measured_traffic(key, 32, "k_step")
+        assert src["current"], (key, src)
+        assert src["csrc_sha256"] == digest and traffic > 0
+    stale = tmp_path / "stale.txt"
+    stale.write_text("traffic_bytes_per_token k_step 1000\ncommit abc\ncsrc_sha256 0000000000000000\n")
+    monkeypatch.setitem(bench.TRAFFIC_SUMMARIES, "cfg1", stale)
+    traffic, src = bench.measured_traffic("cfg1", 32, "k_step")
+    assert traffic is None and src["current"] is False and src["commit"] == "abc"
+    good = tmp_path / "good.txt"
+    good.write_text(f"traffic_bytes_per_token k_step 1000\ncommit abc\ncsrc_sha256 {digest}\n")
+    monkeypatch.setitem(bench.TRAFFIC_SUMMARIES, "cfg1", good)
+    traffic, src = bench.measured_traffic("cfg1", 32, "k_step")
+    assert traffic == 32000 and src["current"]
