@@ -318,13 +318,11 @@ class HipModel:
     def reset(self):
         self._check(self._L.tfh_reset(self._h))
 
-    PATH_GRAPH, PATH_STEP, PATH_RING = 0, 1, 2
+    PATH_GRAPH, PATH_STEP = 0, 1
 
     def set_decode_path(self, path: int):
         """PATH_STEP: one persistent kernel per call where the model allows it (default);
-        PATH_RING: the persistent kernel with each CU's weights streamed through an LDS ring
-        by a loader wave (Q8_0 models; others take PATH_STEP's choice); PATH_GRAPH: the
-        captured per-layer graph, replayed per token."""
+        PATH_GRAPH: the captured per-layer graph, replayed per token."""
         H = hip_lib()
         rc = H.tf_hip_set_decode_path(self._L.tfh_ctx(self._h), int(path))
         if rc != 0:

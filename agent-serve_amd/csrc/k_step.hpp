@@ -76,7 +76,7 @@ __device__ __forceinline__ void set_err(Ctl* c, int v) {
 // words tid + i*kT. Every load of the first pass is issued before any is checked; a word
 // that does not carry its epoch yet is read again (bit i of `pend`) until it does.
 // Needs na <= NA * kT, nb <= NB * kT, NA + NB <= 32.
-template <int NA, int NB, int SLEEP = 1>
+template <int NA, int NB>
 __device__ __forceinline__ void gather(u64* pa, int na, uint32_t ea, float* da, u64* pb, int nb, uint32_t eb,
                                        Ctl* ctl) {
     const int tid = threadIdx.x;
@@ -106,7 +106,7 @@ __device__ __forceinline__ void gather(u64* pa, int na, uint32_t ea, float* da, 
             if (!get_err(ctl)) set_err(ctl, kErrTimeout);  // the first failure's code stays
             break;
         }
-        __builtin_amdgcn_s_sleep(SLEEP);
+        __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             if (pend & (1u << i)) {
@@ -129,7 +129,7 @@ __device__ __forceinline__ void gather(u64* pa, int na, uint32_t ea, float* da, 
 }
 
 // gather() of words base[idx(j)], j < n, of epoch e into d[j] (LDS).
-template <int NA, class Idx, int SLEEP = 1>
+template <int NA, class Idx>
 __device__ __forceinline__ void gather_idx(u64* base, Idx&& idx, int n, uint32_t e, float* d, Ctl* ctl) {
     const int tid = threadIdx.x;
     u64 w[NA];
@@ -152,7 +152,7 @@ __device__ __forceinline__ void gather_idx(u64* base, Idx&& idx, int n, uint32_t
             if (!get_err(ctl)) set_err(ctl, kErrTimeout);  // the first failure's code stays
             break;
         }
-        __builtin_amdgcn_s_sleep(SLEEP);
+        __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             if (pend & (1u << i)) {

@@ -82,10 +82,6 @@ struct tf_hip_ctx {
     int split_all_from = -1;                  // tf_hip_set_split_all_from (< 0: step_split_all_from)
     int split_from = kSplitFromDefault;       // tf_hip_set_split_from: spans up to this attend unsplit
     StepLayer* d_layers = nullptr;
-    // ring step kernel (k_ring.hpp)
-    int ring_state = -1;              // -1 undecided, 0 not used, 1 ready
-    RingArgs ring{};                  // its plan (phases, ring size) and table
-    RingLayer* d_rlayers = nullptr;
     bool coop_refused = false;  // the GPU refused the step kernel's cooperative launch: graph path from then on
     int refuse_coop = 0;        // test hook: this many more step launches report a refusal
     unsigned long long* ex = nullptr;
@@ -611,130 +607,12 @@ int set_ctl(tf_hip_ctx* c, int att_start, int mode) {
     return 0;
 }
 
-// Decides once, after the step kernel's set-up, whether the ring kernel runs this model
-// (TF_HIP_PATH_RING requested, Q8_0 layer matrices and lm_head, and a plan that fits its
-// LDS: ring_plan); it shares the step kernel's exchange words and attention splits.
-// Returns 1 (ring kernel), 0 or < 0.
-int ensure_ring(tf_hip_ctx* c) {
-    if (c->path_opt != TF_HIP_PATH_RING) return 0;
-    if (c->ring_state >= 0) return c->ring_state;
-    const int s = ensure_step(c);
-    if (s <= 0) return s;
-    c->ring_state = 0;
-    const tf_hip_hparams& p = c->hp;
-    if (c->step_tl != TF_HIP_TYPE_Q8_0 || c->step_to != TF_HIP_TYPE_Q8_0 || c->step_split_all <= 0) return 0;
-    const bool bias = vec(c, TF_HIP_SLOT_LAYER(0, TF_HIP_LAYER_BQ)) != nullptr;
-    for (int l = 0; l < p.n_layer; ++l) {
-        const bool lb = vec(c, TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_BQ)) != nullptr &&
-                        vec(c, TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_BK)) != nullptr &&
-                        vec(c, TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_BV)) != nullptr;
-        const bool none = vec(c, TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_BQ)) == nullptr &&
-                          vec(c, TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_BK)) == nullptr &&
-                          vec(c, TF_HIP_SLOT_LAYER(l, TF_HIP_LAYER_BV)) == nullptr;
-        if (bias ? !lb : !none) return 0;  // all three biases in every layer, or none
-    }
-    RingArgs a{};
-    if (!ring_plan(p.n_layer, p.n_embd, p.n_ff, p.n_head, p.n_kv_head, p.head_dim, (int)output_mat(c).N, c->n_wg,
-                   p.max_seq, c->step_split_all, c->split_from, bias, &a))
-        return 0;
-    std::vector<RingLayer> tab((size_t)p.n_layer);
-    const int kinds[7] = {TF_HIP_LAYER_Q,    TF_HIP_LAYER_K,  TF_HIP_LAYER_V,   TF_HIP_LAYER_O,
-                          TF_HIP_LAYER_GATE, TF_HIP_LAYER_UP, TF_HIP_LAYER_DOWN};
-    for (int l = 0; l < p.n_layer; ++l) {
-        RingLayer& t = tab[(size_t)l];
-        for (int k = 0; k < 7; ++k) {
-            const DevMat& m = mat(c, TF_HIP_SLOT_LAYER(l, kinds[k]));
-            t.q[k] = m.q;
-            t.s[k] = m.s;
-        }
-        auto V = [&](int k) { return vec(c, TF_HIP_SLOT_LAYER(l, k)); };
-        t.attn_norm = V(TF_HIP_LAYER_ATTN_NORM);
-        t.ffn_norm = V(TF_HIP_LAYER_FFN_NORM);
-        t.bq = V(TF_HIP_LAYER_BQ);
-        t.bk = V(TF_HIP_LAYER_BK);
-        t.bv = V(TF_HIP_LAYER_BV);
-        t.kc = c->kc + (size_t)l * c->kv_layer;
-        t.vc = c->vc + (size_t)l * c->kv_layer;
-    }
-    int rc = dalloc(c, &c->d_rlayers, tab.size() * sizeof(RingLayer));
-    if (rc) return rc;
-    HIPCHK(c, hipMemcpy(c->d_rlayers, tab.data(), tab.size() * sizeof(RingLayer), hipMemcpyHostToDevice));
-    // TF_HIP_RING_CAP: the loader's loads in flight (a tuning override, 1..48)
-    if (const char* e = std::getenv("TF_HIP_RING_CAP")) {
-        const int v = std::atoi(e);
-        if (v >= 1 && v <= 48) a.cap = v;
-    }
-    c->ring = a;
-    c->ring_state = 1;
-    return 1;
-}
-
-// n tokens through the ring kernel, from position c->pos; results as run_step.
-int run_ring(tf_hip_ctx* c, int n, int greedy, int lm_every, int att_start) {
-    const tf_hip_hparams& p = c->hp;
-    RingArgs a = c->ring;
-    a.layers = c->d_rlayers;
-    a.embd = mat(c, TF_HIP_SLOT_TOKEN_EMBD);
-    a.out = output_mat(c);
-    a.out_norm = vec(c, TF_HIP_SLOT_OUTPUT_NORM);
-    a.rope_cos = c->rope_cos;
-    a.rope_sin = c->rope_sin;
-    a.ex = c->ex;
-    a.ctl = c->ctl;
-    a.hist = c->hist;
-    a.logits = c->logits;
-    a.taps = c->taps;
-    a.n_layer = p.n_layer;
-    a.D = p.n_embd;
-    a.F = p.n_ff;
-    a.H = p.n_head;
-    a.G = p.n_kv_head;
-    a.hd = p.head_dim;
-    a.max_seq = p.max_seq;
-    a.layout = p.kv_layout;
-    a.eps = p.rms_eps;
-    a.n_tokens = n;
-    a.greedy = greedy;
-    a.lm_every = lm_every;
-    a.att_start = att_start;
-    a.split_all = c->step_split_all;
-    a.split_from = c->split_from;
-    int rc = epoch_guard(c, n);
-    if (rc) return rc;
-    hipError_t e;
-    if (c->refuse_coop > 0) {
-        --c->refuse_coop;
-        e = hipErrorCooperativeLaunchTooLarge;
-    } else {
-        e = launch_ring(a, c->n_wg, c->st);
-    }
-    if (coop_refusal(e)) {
-        (void)hipGetLastError();
-        c->coop_refused = true;
-        c->step_state = 0;
-        c->ring_state = 0;
-        return kStepRefused;
-    }
-    if (e != hipSuccess) return fail(c, TF_HIP_EDEVICE, std::string("ring kernel launch: ") + hipGetErrorString(e));
-    c->epoch += (uint32_t)((uint64_t)n * (6ull * (uint64_t)p.n_layer + 8ull));
-    return 0;
-}
-
-// The persistent kernel of this context: 2 ring kernel, 1 step kernel, 0 none (graph path), < 0 error.
-int ensure_persistent(tf_hip_ctx* c) {
-    const int r = ensure_ring(c);
-    if (r < 0) return r;
-    if (r == 1) return 2;
-    return ensure_step(c);
-}
-
-// n tokens on the context's decode path, from position c->pos: the ring (*use_step 2) or
-// step kernel (1), else n replays of the captured graph. A refused cooperative launch switches
+// n tokens on the context's decode path, from position c->pos: the step kernel when
+// *use_step, else n replays of the captured graph. A refused cooperative launch switches
 // the context to the graph path and runs the tokens there (*use_step then reads 0).
 int run_tokens(tf_hip_ctx* c, int* use_step, int n, int greedy, int lm_every, int att_start) {
     if (*use_step) {
-        const int rc = *use_step == 2 ? run_ring(c, n, greedy, lm_every, att_start)
-                                      : run_step(c, n, greedy, lm_every, att_start);
+        const int rc = run_step(c, n, greedy, lm_every, att_start);
         if (rc != kStepRefused) return rc;
         *use_step = 0;
         const int g = ensure_graph(c);
@@ -927,8 +805,6 @@ int finish_step_outputs(tf_hip_ctx* c, float* logits, int32_t* argmax) {
     HIPCHK(c, hipMemcpyAsync(c->ctl_host, c->ctl, sizeof(Ctl), hipMemcpyDeviceToHost, c->st));
     HIPCHK(c, hipStreamSynchronize(c->st));
     if (c->ctl_host->err == 2) return fail(c, TF_HIP_EDEVICE, "step kernel: an exchange wait timed out");
-    if (c->ctl_host->err == 3) return fail(c, TF_HIP_EDEVICE, "ring kernel: a wait for streamed weights timed out");
-    if (c->ctl_host->err == 4) return fail(c, TF_HIP_EDEVICE, "ring kernel: the loader's wait for ring space timed out");
     if (c->ctl_host->err) return fail(c, TF_HIP_EDEVICE, "device reported an invalid token");
     if (c->ctl_host->pos != c->pos) return fail(c, TF_HIP_EDEVICE, "device position out of step");
     if (argmax) *argmax = key_to_index(c->ctl_host->key);
@@ -962,13 +838,12 @@ int tf_hip_create(int device, const tf_hip_hparams* hp, tf_hip_ctx** out) {
         const long v = std::strtol(sf, &end, 10);
         if (end != sf && *end == 0 && v >= 0 && v <= kSplitFromMax) c->split_from = (int)v;
     }
-    // TF_HIP_DECODE_PATH=ring|step|graph: the initial decode path, for callers that do not
+    // TF_HIP_DECODE_PATH=step|graph: the initial decode path, for callers that do not
     // call tf_hip_set_decode_path (other values are ignored)
     if (const char* dp = std::getenv("TF_HIP_DECODE_PATH")) {
         const std::string v(dp);
         if (v == "step") c->path_opt = TF_HIP_PATH_STEP;
         if (v == "graph") c->path_opt = TF_HIP_PATH_GRAPH;
-        if (v == "ring") c->path_opt = TF_HIP_PATH_RING;
     }
     c->hp = p;
     c->H = p.n_head * p.head_dim;
@@ -1068,7 +943,6 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
             if (rc) return rc;
             c->vecs[(size_t)slot] = d;
             c->step_state = -1;
-            c->ring_state = -1;
             c->pf_state = -1;
         }
         c->vec_len[(size_t)slot] = want;
@@ -1117,7 +991,6 @@ int tf_hip_upload_tensor(tf_hip_ctx* c, int slot, int t, int64_t ne0, int64_t ne
     c->allocs.insert(c->allocs.end(), owned.begin(), owned.end());
     c->mats[(size_t)slot] = m;  // a re-upload leaves the old streams allocated until destroy
     c->step_state = -1;         // the step kernel's layer table is rebuilt
-    c->ring_state = -1;         // and the ring kernel's
     c->pf_state = -1;
     return 0;
 }
@@ -1157,7 +1030,7 @@ int tf_hip_decode(tf_hip_ctx* c, int32_t token, float* logits, int32_t* argmax) 
     if (c->pos >= c->hp.max_seq) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
     if (token < 0 || token >= mat(c, TF_HIP_SLOT_TOKEN_EMBD).N)
         return fail(c, TF_HIP_ERANGE, "token " + std::to_string(token) + " out of range");
-    int use_step = ensure_persistent(c);
+    int use_step = ensure_step(c);
     if (use_step < 0) return use_step;
     int rc = use_step ? 0 : ensure_graph(c);
     if (rc) return rc;
@@ -1183,7 +1056,7 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
             return fail(c, TF_HIP_ERANGE, "token " + std::to_string(tokens[i]) + " out of range");
     const int use_pf = n >= 2 ? ensure_pf(c) : 0;
     if (use_pf < 0) return use_pf;
-    int use_step = use_pf ? 0 : ensure_persistent(c);
+    int use_step = use_pf ? 0 : ensure_step(c);
     if (use_step < 0) return use_step;
     int rc = (use_pf || use_step) ? 0 : ensure_graph(c);
     if (rc) return rc;
@@ -1202,7 +1075,7 @@ int tf_hip_prefill(tf_hip_ctx* c, const int32_t* tokens, int32_t n, float* logit
     if (rc) return rc;
     HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
     c->last_steps = use_pf ? 1 : (use_step ? 1 : n);
-    c->last_name = use_pf ? "prefill_mfma" : (use_step == 2 ? "k_ring" : (use_step ? "k_step" : "decode_graph"));
+    c->last_name = use_pf ? "prefill_mfma" : (use_step ? "k_step" : "decode_graph");
     c->have_logits = true;
     return 0;
 }
@@ -1213,7 +1086,7 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     HIPCHK(c, hipSetDevice(c->device));
     if (!c->have_logits) return fail(c, TF_HIP_ESTATE, "generate needs a prior prefill or decode");
     if (n > c->hp.max_seq - c->pos) return fail(c, TF_HIP_ERANGE, "decode exceeds max_seq");
-    int use_step = ensure_persistent(c);
+    int use_step = ensure_step(c);
     if (use_step < 0) return use_step;
     int rc = use_step ? 0 : ensure_graph(c);
     if (rc) return rc;
@@ -1229,16 +1102,15 @@ int tf_hip_generate(tf_hip_ctx* c, int32_t n, int32_t* out) {
     std::memcpy(out, c->tok_host, (size_t)n * 4);
     HIPCHK(c, hipEventElapsedTime(&c->last_ms, c->ev0, c->ev1));
     c->last_steps = use_step ? 1 : n;
-    c->last_name = use_step == 2 ? "k_ring" : (use_step ? "k_step" : "decode_graph");
+    c->last_name = use_step ? "k_step" : "decode_graph";
     return 0;
 }
 
 int tf_hip_set_decode_path(tf_hip_ctx* c, int32_t path) {
-    if (!c || (path != TF_HIP_PATH_GRAPH && path != TF_HIP_PATH_STEP && path != TF_HIP_PATH_RING))
+    if (!c || (path != TF_HIP_PATH_GRAPH && path != TF_HIP_PATH_STEP))
         return TF_HIP_EINVAL;
     c->path_opt = path;
     if (path != TF_HIP_PATH_GRAPH && c->step_state == 0) c->step_state = -1;  // decide again
-    if (path == TF_HIP_PATH_RING && c->ring_state == 0) c->ring_state = -1;
     return 0;
 }
 
@@ -1316,8 +1188,8 @@ int tf_hip_get_prefill_path(tf_hip_ctx* c) {
 int tf_hip_get_decode_path(tf_hip_ctx* c) {
     if (!c) return TF_HIP_EINVAL;
     HIPCHK(c, hipSetDevice(c->device));
-    const int s = ensure_persistent(c);
-    return s < 0 ? s : (s == 2 ? TF_HIP_PATH_RING : (s ? TF_HIP_PATH_STEP : TF_HIP_PATH_GRAPH));
+    const int s = ensure_step(c);
+    return s < 0 ? s : (s ? TF_HIP_PATH_STEP : TF_HIP_PATH_GRAPH);
 }
 
 int tf_hip_get_layer_act(tf_hip_ctx* c, int32_t layer, float* out) {

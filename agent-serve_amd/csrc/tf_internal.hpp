@@ -150,65 +150,6 @@ struct StepArgs {
     int split_from;            // spans (positions attended) up to this attend on one workgroup per kv head
 };
 
-// ---------------------------------------------------------------- ring step kernel (k_ring.hpp)
-// One GEMV phase of the ring kernel, planned on the host: the phase's N rows of K elements
-// are split over the participating workgroups in contiguous runs; a workgroup's rows are
-// cut into items of P = K / sk consecutive elements (sk parts per row), and items go out in
-// batches of 8, one per compute wave. A batch occupies ub ring units of 256 bytes: the
-// items' quants as 1 KiB lines (lpi per item and matrix; mats matrices per item: 2 for the
-// paired gate and up rows), then their fp16 scales (spi dwords per item and matrix) in su
-// units. Before the batches come nu units of norm weights (0: none) and bu units holding
-// the rows' biases (0: none).
-struct RingPhase {
-    int N, K, sk, lsk, P, lpi, spi, mats;  // lsk = log2(sk)
-    int qu, su, ub, nu, bu;
-};
-enum RingPhaseId : int { RP_QKV = 0, RP_WO, RP_GU, RP_DOWN, RP_LM, RP_COUNT };
-
-// One layer of the ring kernel: the Q8_0 matrices' quants and scales (wq, wk, wv, wo, wg,
-// wu, wd), norms, biases and the layer's K/V cache.
-struct RingLayer {
-    const uint8_t* q[7];
-    const uint8_t* s[7];
-    const float* attn_norm;
-    const float* ffn_norm;
-    const float* bq;
-    const float* bk;
-    const float* bv;
-    float* kc;
-    float* vc;
-};
-
-struct RingArgs {
-    const RingLayer* layers;
-    DevMat embd, out;          // token embedding, lm_head (Q8_0)
-    const float* out_norm;
-    const float* rope_cos;     // [max_seq][hd/2]
-    const float* rope_sin;
-    unsigned long long* ex;    // exchange words, the step kernel's (step_exchange_words)
-    Ctl* ctl;
-    int32_t* hist;
-    float* logits;
-    float* taps;
-    int n_layer, D, F, H, G, hd, max_seq, layout;
-    float eps;
-    int n_tokens, greedy, lm_every, att_start;
-    int split_all;             // > 0: splits per kv head when every workgroup splits
-    int split_from;            // spans up to this attend on one workgroup per kv head
-    int ring_units;            // ring size in 256-byte units (a multiple of 4)
-    int cap;                   // the loader's loads in flight at most (1..48)
-    int part_floats;           // LDS floats for the items' partial sums
-    RingPhase ph[RP_COUNT];
-};
-
-// The ring kernel's plan for a model (phases, ring size), or false when it does not run it:
-// Q8_0 layer matrices and lm_head, head size <= 128, at most 8 query heads per kv head, row
-// lengths divisible by 64, and an LDS ring of at least two of the largest batches.
-bool ring_plan(int n_layer, int D, int F, int H, int G, int hd, int V, int n_wg, int max_seq, int split_all,
-               int split_from, bool has_bias, RingArgs* a);
-size_t ring_lds_bytes(const RingArgs& a, int n_wg);
-hipError_t launch_ring(const RingArgs& a, int n_wg, hipStream_t st);
-
 // ---------------------------------------------------------------- prefill on the matrix cores
 // Rows (tokens) of a prefill GEMM workgroup tile; activation buffers are padded to it.
 constexpr int kPfTileM = 64;

@@ -53,9 +53,8 @@ void usage() {
                  "  --kv-layout seq|head override KV layout\n"
                  "  --no-bos             do not prepend BOS\n"
                  "  --device N           HIP device (default 0)\n"
-                 "  --decode-path P      step (persistent kernel, the default) | graph | ring (the\n"
-                 "                       LDS-ring kernel, Q8_0 models); a persistent kernel the GPU\n"
-                 "                       refuses (another process holds it) runs as graph\n"
+                 "  --decode-path P      step (persistent kernel, the default) | graph; a step kernel the\n"
+                 "                       GPU refuses (another process holds it) runs as graph\n"
                  "  --device-loop        greedy tokens from one tf_hip_generate call (one launch of the\n"
                  "                       persistent kernel, as bench.py times it) instead of a decode per token\n"
                  "  --profile            print the per-kernel-class breakdown of one greedy pass\n");
@@ -126,13 +125,11 @@ int main(int argc, char** argv) {
         Model model(model_path, cfg);
         const Tokenizer tok(model.gguf());
         // without the flag the library's choice stands (step, or TF_HIP_DECODE_PATH)
-        if (decode_path == "graph" || decode_path == "step" || decode_path == "ring") {
-            const int path = decode_path == "graph" ? TF_HIP_PATH_GRAPH
-                             : decode_path == "ring" ? TF_HIP_PATH_RING
-                                                     : TF_HIP_PATH_STEP;
-            if (tf_hip_set_decode_path(model.ctx(), path)) die("tf_hip_set_decode_path failed");
+        if (decode_path == "graph" || decode_path == "step") {
+            if (tf_hip_set_decode_path(model.ctx(), decode_path == "graph" ? TF_HIP_PATH_GRAPH : TF_HIP_PATH_STEP))
+                die("tf_hip_set_decode_path failed");
         } else if (!decode_path.empty()) {
-            die("--decode-path takes step, graph or ring");
+            die("--decode-path takes step or graph");
         }
         std::fprintf(stderr, "%s\n", model.describe().c_str());
         const std::vector<int> ids = !token_str.empty() ? parse_tokens(token_str) : tok.encode(prompt, add_bos);

@@ -3,9 +3,9 @@
     python3 agent-serve_amd/profsum.py trace <kernel_stats.csv> [--steps K]
     python3 agent-serve_amd/profsum.py steps <kernel_trace.csv>
     python3 agent-serve_amd/profsum.py stepcounters <fetch counter_collection.csv> <write counter_collection.csv>
-        --copy-fetch <csv> --copy-write <csv> [--copy-bytes N] [--kernel k_step|k_ring]
+        --copy-fetch <csv> --copy-write <csv> [--copy-bytes N] [--kernel <name>]
     python3 agent-serve_amd/profsum.py digest
-    python3 agent-serve_amd/profsum.py decodetrace <kernel_stats.csv> <kernel_trace.csv> [--kernel k_step|k_ring]
+    python3 agent-serve_amd/profsum.py decodetrace <kernel_stats.csv> <kernel_trace.csv> [--kernel <name>]
         [--algo-bytes B]
     python3 agent-serve_amd/profsum.py traffic <fetch counter_collection.csv> <write counter_collection.csv>
         --copy-bytes N [--copy-fetch <csv> --copy-write <csv>]
@@ -100,7 +100,7 @@ def copy_scales(fetch_csv: str, write_csv: str, copy_bytes: int) -> tuple[float,
 
 
 def step_counters(fetch_csv: str, write_csv: str, f_scale: float, w_scale: float, kernel: str = "k_step") -> None:
-    """HBM bytes per decode token of a persistent decode kernel (k_step or k_ring) from a
+    """HBM bytes per decode token of the persistent decode kernel (k_step) from a
     run of the CLI (the prompt, then one launch per decoded token): the median over the
     launches after the first, FETCH_SIZE and WRITE_SIZE scaled by the copy kernel's
     factors."""
@@ -279,7 +279,7 @@ def main() -> int:
     ap.add_argument("files", nargs="*")
     ap.add_argument("--copy-fetch", help="FETCH_SIZE counter csv of the k_copy_stream calibration run")
     ap.add_argument("--copy-write", help="WRITE_SIZE counter csv of the k_copy_stream calibration run")
-    ap.add_argument("--kernel", default="k_step", help="stepcounters, decodetrace: the decode kernel (k_step or k_ring)")
+    ap.add_argument("--kernel", default="k_step", help="stepcounters, decodetrace: the persistent decode kernel's name")
     ap.add_argument("--commit", default=None, help="commit measured (default: git HEAD)")
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)

@@ -120,18 +120,13 @@ int tf_hip_generate(tf_hip_ctx* ctx, int32_t n, int32_t* out_tokens);
  * per-layer kernels replayed per token. Both compute the same function; neither has a
  * counterpart in the reference (a backend choice below Model::decode, model.cpp:197-208).
  * tf_hip_get_decode_path returns the path the next call will take (needs every tensor
- * uploaded). The environment variable TF_HIP_DECODE_PATH (ring, step or graph), read by
+ * uploaded). The environment variable TF_HIP_DECODE_PATH (step or graph), read by
  * tf_hip_create, sets the initial path for callers that never call the setter. The step
  * path launches cooperatively; when the GPU refuses the cooperative launch (another
  * process holds that resource, or the grid does not fit), the context switches itself to
  * the graph path for the rest of its life and tf_hip_get_decode_path reports that. */
 #define TF_HIP_PATH_GRAPH 0
 #define TF_HIP_PATH_STEP 1
-/* TF_HIP_PATH_RING: the persistent kernel with a loader wave per CU streaming that CU's
- * weight rows through an LDS ring (Q8_0 layer matrices and lm_head, head size <= 128);
- * models it does not cover take TF_HIP_PATH_STEP's choice. Same function as the others.
- * Never chosen by default: it is selected only through the setter or the environment. */
-#define TF_HIP_PATH_RING 2
 int tf_hip_set_decode_path(tf_hip_ctx* ctx, int32_t path);
 int tf_hip_get_decode_path(tf_hip_ctx* ctx);
 

@@ -13,21 +13,13 @@ from gpu_util import REGRESS, model_parity
 pytestmark = pytest.mark.gpu
 
 SMALL = ["tiny_f32", "tiny_q8", "tiny_mixq4", "tiny_qwen", "tiny_hd128", "small_q8"]
-GRAPH, STEP, RING = 0, 1, 2  # HipModel.PATH_GRAPH, PATH_STEP, PATH_RING
-Q8 = ["tiny_q8", "tiny_qwen", "tiny_hd128", "small_q8"]  # presets the ring kernel runs (others: step kernel)
+GRAPH, STEP = 0, 1  # HipModel.PATH_GRAPH, PATH_STEP
 
 
-@pytest.mark.parametrize("path", [GRAPH, STEP, RING], ids=["graph", "step", "ring"])
+@pytest.mark.parametrize("path", [GRAPH, STEP], ids=["graph", "step"])
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("preset", SMALL)
 def test_small_models(pkg, gguf, preset, layout, path):
-    if path == RING:
-        m = pkg.HipModel(gguf(preset), max_seq=64)
-        m.set_decode_path(RING)
-        try:
-            assert m.decode_path() == (RING if preset in Q8 else STEP)
-        finally:
-            m.close()
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"], 6, info["n_vocab"])
     ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 16, 64, layout, decode_path=path)
@@ -52,14 +44,14 @@ def test_decode_path_selection(pkg, gguf, preset, want):
     big.close()
 
 
-@pytest.mark.parametrize("path", [GRAPH, STEP, RING], ids=["graph", "step", "ring"])
+@pytest.mark.parametrize("path", [GRAPH, STEP], ids=["graph", "step"])
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("preset", ["tiny_q8", "tiny_f32", "tiny_qwen", "small_q8", "tiny_mixq4", "tiny_hd128"])
 def test_long_cache_split_attention(pkg, gguf, preset, layout, path):
     """A 600-token prompt in a 1024-position cache: the step kernel's attention splits the
-    positions over its trailing workgroups and merges the splits there, the ring kernel's
-    over every workgroup, the graph path's over split workgroups and a combine launch; each
-    against the oracle while decoding past it."""
+    positions over its trailing workgroups and merges the splits there, the graph path's
+    over split workgroups and a combine launch; each against the oracle while decoding
+    past it."""
     info = pkg.synth_preset_info(preset)
     prompt = pkg.synth_prompt(info["seed"] + 7, 600, info["n_vocab"])
     ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, 12, 1024, layout, decode_path=path)
@@ -357,21 +349,6 @@ def test_full_size(pkg, gguf, preset, n_prompt, n_gen, max_seq, layout):
     prompt = pkg.synth_prompt(info["seed"], n_prompt, info["n_vocab"])
     ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, n_gen, max_seq, layout)
     print(f"{preset}: {len(ids)} tokens identical; logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
-
-
-@pytest.mark.parametrize("preset,n_prompt,n_gen,max_seq,layout", [
-    ("llama1b_q8", 6, 32, 512, 0),
-    ("qwen05b_q8", 16, 64, 512, 0),
-    ("qwen15b_q8", 64, 16, 8192, 1),
-    ("llama1b_q8", 512, 16, 1024, 0),
-])
-def test_full_size_ring(pkg, gguf, preset, n_prompt, n_gen, max_seq, layout):
-    """The Q8_0 workloads at full size through the ring kernel, against the oracle."""
-    info = pkg.synth_preset_info(preset)
-    prompt = pkg.synth_prompt(info["seed"], n_prompt, info["n_vocab"])
-    ids, worst, worst_tap, margin = model_parity(pkg, gguf(preset), prompt, n_gen, max_seq, layout,
-                                                 decode_path=RING)
-    print(f"{preset} ring: {len(ids)} tokens identical; logits {worst:.2e} taps {worst_tap:.2e} margin {margin:.3e}")
 
 
 GOLDEN =__import__("pathlib").Path(__file__).resolve().parent / "golden"
