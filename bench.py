@@ -18,7 +18,8 @@ of once() -- reset, prefill (TTFT), n_predict x (greedy argmax on the device + d
 token one call -- reported as medians with IQR and per-token p50/p95/p99; next to it the
 one-launch greedy loop over the same tokens gives the config's roofline object, and the
 reference --stage v2 path (compiled from its own sources, oracle/_ref) on the host's cores
-gives its cpu_baseline on a bounded sample. `prefill` is the 512-token prompt on the matrix
+gives its cpu_baseline on the same workload (whole prompt, every token). `prefill` is the
+512-token prompt on the matrix
 cores (MFMA utilisation), `context_sweep` the decode rate after 512..4000-token prompts.
 """
 from __future__ import annotations
@@ -353,23 +354,20 @@ def context_sweep(pkg, threads):
 
 # ---------------------------------------------------------------- the CPU baselines
 
-# bounded samples of the reference --stage v2 path per config: (prompt tokens, decode
-# tokens, runs); the full workload where it takes seconds
-CPU_SAMPLES = {"cfg1": (6, 32, 3), "cfg2": (16, 128, 3), "cfg3": (6, 16, 3), "cfg4": (512, 4, 2), "cfg5": (256, 8, 1)}
+# the reference --stage v2 path per config: (prompt tokens, decode tokens, runs) — every
+# workload whole; the Qwen2.5-1.5B shape's 4096-token prompt takes ≈ 85 s on 16 host threads
+# (its prefill attention is single-threaded), so it runs once
+CPU_SAMPLES = {"cfg1": (6, 32, 3), "cfg2": (16, 128, 3), "cfg3": (6, 64, 3), "cfg4": (512, 16, 2), "cfg5": (4096, 256, 1)}
 
 
-def cpu_config(pkg, key, preset, n_prompt, n_dec, max_seq, layout, cpus, want_ids, full_prompt=False):
+def cpu_config(pkg, key, preset, n_prompt, n_dec, max_seq, layout, cpus, want_ids):
     """The reference --stage v2 Model (oracle/_ref) on this host: bench_e2e's once()
-    (reset, prefill, n x (sample_greedy + decode)) after one warm-up, median over runs.
-    full_prompt (--cpu-full): the whole prompt and up to 16 decode tokens, one run (the
-    Qwen2.5-1.5B shape's 4096-token prompt then takes minutes on the CPU)."""
+    (reset, prefill, n x (sample_greedy + decode)) after one warm-up, median over runs."""
     from oracle.bind import RefModel, ref_available
 
     if not ref_available():
         return None
     s_prompt, s_dec, runs = CPU_SAMPLES[key]
-    if full_prompt:
-        s_prompt, s_dec, runs = n_prompt, max(s_dec, min(n_dec, 16)), 1
     s_prompt = min(s_prompt, n_prompt)
     s_dec = min(s_dec, n_dec)
     path, info = ensure_model(pkg, preset, cpus["threads"])
@@ -410,8 +408,6 @@ def main() -> int:
     ap.add_argument("--runs", type=int, default=5, help="bench_e2e runs per config")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--quick", action="store_true", help="headline only (no config list, sweep or prefill leg)")
-    ap.add_argument("--cpu-full", action="store_true",
-                    help="CPU baselines on every workload's whole prompt (minutes for the 4096-token one)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: the token loop runs on one GPU; --gpus {args.gpus} is not supported "
@@ -469,7 +465,7 @@ def main() -> int:
             if args.quick and key != HEADLINE:
                 continue
             want = configs[key]["ids"] if key in configs else list(ids)
-            c = cpu_config(pkg, key, preset, n_prompt, n_dec, max_seq, layout, cpus, want, args.cpu_full)
+            c = cpu_config(pkg, key, preset, n_prompt, n_dec, max_seq, layout, cpus, want)
             if key in configs:
                 configs[key]["cpu_baseline"] = c
             if key == HEADLINE:
