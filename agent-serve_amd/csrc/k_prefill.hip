@@ -1183,6 +1183,7 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
     const int q_base = (blk * QG + w / n_rep) * 16 * QS;
     const int wg_last = min(n - 1, (blk + 1) * QG * 16 * QS - 1);
     const int n_tiles = (pos0 + wg_last - att_start) / kAttnTile + 1;
+    const int q_first = __builtin_amdgcn_readfirstlane(pos0 + min(q_base, n - 1));  // the wave's first query
     const int l16 = lane & 15, gq = lane >> 4;
     const float scale = 1.0f / sqrtf((float)HD);
 
@@ -1208,7 +1209,7 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
         amax = quad_max(amax);
         const int e = pow2_exp(amax, 0);
         const float sc = ldexpf(1.0f, e);
-        fq[qs] = ldexpf(scale, -e);
+        fq[qs] = ldexpf(scale, -e) * 1.44269504088896341f;  // the scores in units of log2
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -1276,6 +1277,8 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
         const float fkj[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
         const float fvj[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         const int kpos = att_start + kAttnTile * t + 4 * gq;  // key j of the lane: kpos + 16 (j / 4) + j % 4
+        // keys past a query only where the tile reaches past the wave's first query
+        const bool masked = att_start + kAttnTile * t + kAttnTile - 1 > q_first;
         h8_t ph[QS], pl[QS];
         float resc[QS];
         int unit_new[QS];
@@ -1284,18 +1287,24 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
             float p[8];
             float mt = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int key = kpos + 16 * (j >> 2) + (j & 3);
-                p[j] = key <= qpos[qs] ? s[qs][j >> 2][j & 3] * fq[qs] * fkj[j] : -INFINITY;
-                mt = fmaxf(mt, p[j]);
+            for (int j = 0; j < 8; ++j) p[j] = s[qs][j >> 2][j & 3] * fq[qs] * fkj[j];
+            if (masked) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (kpos + 16 * (j >> 2) + (j & 3) > qpos[qs]) p[j] = -INFINITY;
             }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) mt = fmaxf(mt, p[j]);
             mt = quad_max(mt);
+            // scores are in units of log2 (fq carries log2 e): 2^(x - m) is exp of the score
+            // difference; every query has a key in tile 0 (att_start <= its position), so
+            // m_new is finite from the first tile on
             const float m_new = fmaxf(m_run[qs], mt);
-            const float alpha = expf(m_run[qs] - m_new);  // 0 on the first tile
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - m_new);  // 0 on the first tile
             float ls = 0.0f, x[8], mx = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                p[j] = p[j] == -INFINITY ? 0.0f : expf(p[j] - m_new);
+                p[j] = __builtin_amdgcn_exp2f(p[j] - m_new);  // 0 for a masked key
                 ls += p[j];
                 x[j] = p[j] * fvj[j];
                 mx = fmaxf(mx, x[j]);
@@ -1304,13 +1313,18 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
             mx = quad_max(mx);
             l_run[qs] = fmaf(l_run[qs], alpha, ls);
             m_run[qs] = m_new;
-            // the tile's unit: its largest term in [2^14, 2^15); no change when it adds
-            // nothing, and never so far above the running unit that the rescaled output
-            // (below 2^43 in its unit, times alpha) could leave fp32's range
+            // the tile's unit: the running one while it keeps the tile's largest term in
+            // [2^7, 2^15) (so the output needs no rescaling when the max holds), else the one
+            // putting it in [2^14, 2^15); no change when the tile adds nothing, and never so
+            // far above the running unit that the rescaled output (below 2^43 in its unit,
+            // times alpha) could leave fp32's range
             int e = unit[qs];
             if (mx > 0.0f) {
-                e = 15 - __builtin_amdgcn_frexp_expf(mx);
-                if (alpha > 0.0f) e = min(e, unit[qs] + 76 - __builtin_amdgcn_frexp_expf(alpha));
+                const int fit = 15 - __builtin_amdgcn_frexp_expf(mx);
+                if (fit < unit[qs] || fit > unit[qs] + 7) {
+                    e = fit;
+                    if (alpha > 0.0f) e = min(e, unit[qs] + 76 - __builtin_amdgcn_frexp_expf(alpha));
+                }
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -1321,15 +1335,23 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
             resc[qs] = ldexpf(alpha, e - unit[qs]);
             unit_new[qs] = e;
         }
+        bool scaled = false;  // some lane's output changes scale (max or unit): rescale all
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs) unit[qs] = unit_new[qs];
+        for (int qs = 0; qs < QS; ++qs) {
+            unit[qs] = unit_new[qs];
+            scaled = scaled || resc[qs] != 1.0f;
+        }
+        if (__builtin_amdgcn_ballot_w64(scaled) != 0)
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+                for (int d = 0; d < NT; ++d) acc[qs][d] = acc[qs][d] * resc[qs];
 #pragma unroll
         for (int d = 0; d < NT; ++d) {
             const h8_t vh = vf[d * 128 + lane], vl = vf[d * 128 + 64 + lane];
 #pragma unroll
             for (int qs = 0; qs < QS; ++qs) {
-                f4_t x = acc[qs][d] * resc[qs];
-                x = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[qs], x, 0, 0, 0);
+                f4_t x = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[qs], acc[qs][d], 0, 0, 0);
                 x = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl[qs], x, 0, 0, 0);
                 acc[qs][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[qs], x, 0, 0, 0);
             }
@@ -1392,7 +1414,7 @@ hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, flo
                            uint16_t* xa, float* rs, hipStream_t st) {
     if (K % 32 != 0 || K > kBlock * 8 * kSplitGroups || ldx % 4 != 0 || Mpad % kPfTileM != 0 || M > Mpad)
         return hipErrorInvalidValue;
-    // a wave per row while a lane holds at most 16 groups (rows up to 8192), else a workgroup
+    // a wave per row while a lane holds at most 20 groups (rows up to 10240), else a workgroup
     const int per1 = (K / 8 + 63) / 64;
 #define TF_SPLIT(NG, WPR, rows)                                                                              \
     hipLaunchKernelGGL((k_pf_split<NG, WPR>), dim3((unsigned)(Mpad / (rows))), dim3(kBlock), 0, st, x, ldx, \
@@ -1405,6 +1427,8 @@ hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, flo
         TF_SPLIT(8, 1, kWavesPerBlock);
     else if (per1 <= 16)
         TF_SPLIT(16, 1, kWavesPerBlock);
+    else if (per1 <= 20)
+        TF_SPLIT(20, 1, kWavesPerBlock);
     else
         TF_SPLIT(kSplitGroups, 4, 1);  // per4 <= 8: K was checked above
 #undef TF_SPLIT
@@ -1422,23 +1446,30 @@ hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
         const int n_big = (a.n_sub + per_big - 1) / per_big * (a.Mpad / kBigRows);
         const int cus = device_cu_count();
         int ks = 1;
-        if (n_big < cus && a.mode != GEMV_SILU && a.part) {
-            // the fewest slices that fill the CUs, each at least 8 stages long (shorter
-            // slices spend more on filling their pipeline and on the partial rows they
-            // write than they save), or 4 when that fills the CUs with one workgroup each;
-            // worth it from half the CUs on
+        bool big = n_big >= cus;
+        if (!big && a.mode != GEMV_SILU && a.part) {
+            // K slices by the span they give: rounds of workgroups over the CUs times
+            // stages per slice; the fewest slices with the shortest span (each split adds
+            // its reduce), each slice at least 8 stages long (shorter slices spend more on
+            // filling their pipeline and on the partial rows they write than they save), or
+            // 4 when that fits the CUs in one round. Big tiles when at least half the CUs
+            // get one.
             const int S = a.K / 64;
             const size_t per_slice = (size_t)a.Mpad * a.n_sub * 16;
+            int64_t best = (int64_t)((n_big + cus - 1) / cus) * S;
             for (int k = 2; k <= 16; k *= 2) {
                 if (S % k != 0 || S / k < 4 || (S / k < 8 && n_big * k > cus) ||
                     (size_t)k * per_slice > a.part_floats)
                     break;
-                ks = k;
-                if (n_big * k >= cus) break;
+                const int64_t span = (int64_t)((n_big * k + cus - 1) / cus) * (S / k);
+                if (span < best) {
+                    best = span;
+                    ks = k;
+                }
             }
-            if (2 * n_big * ks < cus) ks = 1;
+            big = 2 * n_big * ks >= cus;
         }
-        if (n_big >= cus || ks > 1) {
+        if (big) {
             static bool attr_set[6] = {false, false, false, false, false, false};
             const void* fns[6] = {(const void*)k_pf_gemm_big<GEMV_STORE, false, T>,
                                   (const void*)k_pf_gemm_big<GEMV_RESID, false, T>,
