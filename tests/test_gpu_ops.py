@@ -174,6 +174,28 @@ def test_prefill_gemm_single_element_rows(pkg, t):
         assert np.array_equal(got, want)
 
 
+def test_prefill_gemm_seeded_shapes(pkg):
+    """Twenty shapes drawn from a fixed seed (rows 1..700, K a multiple of 64 up to 10,240, N a
+    multiple of 16 up to 4,096; Q8_0, Q4_0 and Q4_1): whatever tile kernel and K split the
+    launch picks for them, each output within 2e-5 * sum_k |x_k w_nk| of the oracle."""
+    rng = np.random.default_rng(4242)
+    for _ in range(20):
+        t = int(rng.choice([8, 2, 3]))
+        m = int(rng.integers(1, 701))
+        k = 64 * int(rng.integers(1, 161))
+        n = 16 * int(rng.integers(1, 257))
+        while m * k * n > 1.5e9:
+            n = max(16, n // 32 * 16)
+            m = max(1, m // 2)
+        rows = random_rows(rng, t, k, n)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        got = pkg.matmul(t, rows, k, n, x)
+        want = oracle_matmul(t, rows, k, x)
+        budget = np.abs(x).astype(np.float64) @ np.abs(oracle_dequant(t, rows, k)).astype(np.float64).T
+        err = np.abs(got.astype(np.float64) - want)
+        assert np.all(err <= 2e-5 * budget + 1e-30), f"type {t} {m}x{k}x{n}: max err/budget {np.max(err / (budget + 1e-30)):.3e}"
+
+
 def test_prefill_gemm_row_scales(pkg):
     """Rows of very different magnitude keep their relative precision (each row has its own
     power-of-two scale); a zero row gives zeros; a row with one non-zero x_j gives
