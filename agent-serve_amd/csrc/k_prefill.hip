@@ -290,13 +290,14 @@ template <int MODE, int NI>
 struct TileCtx {
     static constexpr int NO = MODE == GEMV_SILU ? NI / 2 : NI;  // output subtiles per wave
     int lane, l16, lc, m0;
-    int seg[NI], c[NI];
+    int kslice = 0;  // K slice of a split launch (ks slices, workgroups slice-fastest)
+    int seg[NI], c[NI], gcol[NI];
     bool ok[NI];
     float* y[NI];
     const float* bias[NI];
     int64_t ldy[NI];
     const uint8_t *wq[NI], *wq2[NI], *ws[NI], *ws2[NI];  // the subtile's matrix streams
-    __device__ __forceinline__ TileCtx(const PfGemmArgs& a) {
+    __device__ __forceinline__ TileCtx(const PfGemmArgs& a, int ks = 1) {
         lane = threadIdx.x & 63;
         l16 = lane & 15;
         lc = lane >> 4;
@@ -308,6 +309,8 @@ struct TileCtx {
             const int q = (int)gridDim.x / 8;
             if (b < 8 * q) b = (b % 8) * q + b / 8;
         }
+        kslice = b % ks;
+        b /= ks;
         const int MT = a.Mpad / kPfTileM;
         const int mt = b % MT, nt = b / MT;
         m0 = mt * kPfTileM + (wave & 1) * 32;
@@ -319,6 +322,7 @@ struct TileCtx {
             u = u < a.n_sub ? u : a.n_sub - 1;
             seg[ni] = (a.n_seg > 2 && u >= a.seg[2].sub0) ? 2 : ((a.n_seg > 1 && u >= a.seg[1].sub0) ? 1 : 0);
             c[ni] = (u - PF_SEL(seg[ni], sub0)) * 16 + l16;
+            gcol[ni] = u * 16 + l16;
             const bool u2 = up(ni);
             const int sg = seg[ni];
             wq[ni] = u2 ? PF_SEL(sg, w2.q) : PF_SEL(sg, w.q);
@@ -370,6 +374,27 @@ struct TileCtx {
             }
         }
     }
+    // a K slice's row-scaled partial sums: part[kslice][row][output column] (the big tiles'
+    // layout, read by the same reduces)
+    // (GEMV_SILU: the gate columns, then the up columns)
+    __device__ __forceinline__ void epilogue_part(const PfGemmArgs& a, const f4_t (&acc)[2][NI]) const {
+        const int nout = a.n_sub * 16;
+        const int ntot = MODE == GEMV_SILU ? 2 * nout : nout;
+        float* part = a.part + (int64_t)kslice * a.Mpad * ntot;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+            const int r0 = m0 + 16 * mi + 4 * (lane >> 4);
+            const float4 rsv = *(const float4*)(a.rs + r0);
+            const float rsa[4] = {rsv.x, rsv.y, rsv.z, rsv.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (r0 + r >= a.M) continue;
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni)
+                    if (ok[ni]) part[(int64_t)(r0 + r) * ntot + gcol[ni] + (up(ni) ? nout : 0)] = acc[mi][ni][r] * rsa[r];
+            }
+        }
+    }
 };
 
 // Per 32-element block: for each (row subtile, column subtile) an MFMA of the hi part from
@@ -378,10 +403,10 @@ struct TileCtx {
 // same two MFMAs against a fragment of ones). Weight bytes and activation fragments stream
 // from L2 into registers, one stage of two blocks ahead; every load is unconditional
 // (indices clamped) so the compiler waits only for the stage it consumes.
-template <int MODE, int NI, int T>
+template <int MODE, int NI, int T, bool SPLIT>
 __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
     using W = PfW<T>;
-    const TileCtx<MODE, NI> t(a);
+    const TileCtx<MODE, NI> t(a, SPLIT ? a.ks : 1);
     const int K = a.K, nblk = K / 32;
     constexpr int SW = W::kScale == 4 ? 2 : 1;  // scale words per stage and column
     const TF_GLOBAL uint8_t* bp[NI];
@@ -405,9 +430,10 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
         typename W::Raw bw[NI][2];  // [column subtile][block]: the lane's weight bytes
         uint32_t d[NI][SW];         // the scale words of the stage's two blocks
     };
-    const int S = K / 64;
+    const int S = SPLIT ? K / 64 / a.ks : K / 64;  // stages (two blocks) of this K slice
+    const int sb = SPLIT ? t.kslice * S : 0;       // its first stage
     auto load = [&](int s, Stage& g) {
-        s = s < S ? s : S - 1;
+        s = sb + (s < S ? s : S - 1);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int blk = 2 * s + j;
@@ -473,7 +499,10 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
         compute(s1);
     }
     if (s < S) compute(s0);
-    t.epilogue(a, acc);
+    if (SPLIT)
+        t.epilogue_part(a, acc);
+    else
+        t.epilogue(a, acc);
 }
 
 // F32 weights on v_mfma_f32_16x16x4_f32. The activations come from the same hi + lo
@@ -860,8 +889,10 @@ template <int MODE, int KS>
 __global__ __launch_bounds__(kBlock) void k_pf_reduce(const PfGemmArgs a) {
     const int row = blockIdx.y;
     const int col0 = (blockIdx.x * kBlock + threadIdx.x) * 4;
-    const int ntot = a.n_sub * 16;
-    if (col0 >= ntot) return;
+    const int nout = a.n_sub * 16;
+    // GEMV_SILU: the gate columns, then the up columns
+    const int ntot = MODE == GEMV_SILU ? 2 * nout : nout;
+    if (col0 >= nout) return;
     const float* p = a.part + (int64_t)row * ntot + col0;
     float4 pv[KS];
 #pragma unroll
@@ -873,6 +904,22 @@ __global__ __launch_bounds__(kBlock) void k_pf_reduce(const PfGemmArgs a) {
         v[1] += pv[k].y;
         v[2] += pv[k].z;
         v[3] += pv[k].w;
+    }
+    if (MODE == GEMV_SILU) {
+#pragma unroll
+        for (int k = 0; k < KS; ++k) pv[k] = *(const float4*)(p + nout + (int64_t)k * a.Mpad * ntot);
+        float w[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            w[0] += pv[k].x;
+            w[1] += pv[k].y;
+            w[2] += pv[k].z;
+            w[3] += pv[k].w;
+        }
+        float* y = a.seg[0].y + (int64_t)row * a.seg[0].ldy + col0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (v[e] / (1.0f + expf(-v[e]))) * w[e];
+        return;
     }
     // a 16-column subtile never straddles two segments, so neither do the 4 columns
     const int u = col0 / 16;
@@ -1437,6 +1484,75 @@ hipError_t launch_pf_split(const float* x, int64_t ldx, const float* norm_w, flo
 
 namespace {
 
+// The reduce of a GEMM whose K ran in ks slices (2, 4, 8 or 16; partial sums in b.part): the
+// QKV reduce fused with RoPE and the cache store, the residual reduce fused with the next
+// GEMM's activation split, or the plain reduce; *fused says whether the fused work ran.
+hipError_t launch_split_reduce(const PfGemmArgs& a, int ks, hipStream_t st, bool* fused) {
+    hipError_t e = hipSuccess;
+    if (a.mode == GEMV_STORE && a.rope_cos && a.rope_sin && a.kc && a.vc && a.n_seg == 3 && a.hd % 2 == 0 &&
+        a.seg[0].w.N == (int64_t)a.n_head * a.hd && a.seg[1].w.N == (int64_t)a.n_kv * a.hd &&
+        a.seg[2].w.N == (int64_t)a.n_kv * a.hd) {
+        const int items = (a.n_head + a.n_kv) * (a.hd / 2) + a.n_kv * a.hd;
+        const dim3 qgrid((unsigned)((items + kBlock - 1) / kBlock), (unsigned)a.M);
+#define PF_RROPE(KS) hipLaunchKernelGGL((k_pf_reduce_rope<KS>), qgrid, dim3(kBlock), 0, st, a)
+        switch (ks) {
+            case 2: PF_RROPE(2); break;
+            case 4: PF_RROPE(4); break;
+            case 8: PF_RROPE(8); break;
+            case 16: PF_RROPE(16); break;
+            default: return hipErrorInvalidValue;
+        }
+#undef PF_RROPE
+        e = hipGetLastError();
+        if (e == hipSuccess && fused) *fused = true;
+        return e;
+    }
+    const int ngr = a.n_sub * 2;  // 8-column groups of an output row
+    if (a.mode == GEMV_RESID && a.split_xa && a.split_rs && a.n_seg == 1 && a.seg[0].ldy % 4 == 0 && a.seg[0].ldy >= ngr * 8 &&
+        ((uintptr_t)a.seg[0].y & 15) == 0 && ngr <= 4 * kBlock) {
+        const int ng = ngr <= kBlock ? 1 : (ngr <= 2 * kBlock ? 2 : 4);
+#define PF_RSPLIT(KS, NG) hipLaunchKernelGGL((k_pf_reduce_split<KS, NG>), dim3((unsigned)a.Mpad), dim3(kBlock), 0, st, a)
+        switch (ks * 8 + ng) {  // ks is 2, 4, 8 or 16 here
+            case 17: PF_RSPLIT(2, 1); break;
+            case 18: PF_RSPLIT(2, 2); break;
+            case 20: PF_RSPLIT(2, 4); break;
+            case 33: PF_RSPLIT(4, 1); break;
+            case 34: PF_RSPLIT(4, 2); break;
+            case 36: PF_RSPLIT(4, 4); break;
+            case 65: PF_RSPLIT(8, 1); break;
+            case 66: PF_RSPLIT(8, 2); break;
+            case 68: PF_RSPLIT(8, 4); break;
+            case 129: PF_RSPLIT(16, 1); break;
+            case 130: PF_RSPLIT(16, 2); break;
+            case 132: PF_RSPLIT(16, 4); break;
+            default: return hipErrorInvalidValue;
+        }
+#undef PF_RSPLIT
+        e = hipGetLastError();
+        if (e == hipSuccess && fused) *fused = true;
+        return e;
+    }
+    const dim3 rgrid((unsigned)((a.n_sub * 4 + kBlock - 1) / kBlock), (unsigned)a.M);
+#define PF_REDUCE(MODE, KS) hipLaunchKernelGGL((k_pf_reduce<MODE, KS>), rgrid, dim3(kBlock), 0, st, a)
+    switch (a.mode * 32 + ks) {  // ks is 2, 4, 8 or 16 here
+        case 2: PF_REDUCE(GEMV_STORE, 2); break;
+        case 4: PF_REDUCE(GEMV_STORE, 4); break;
+        case 8: PF_REDUCE(GEMV_STORE, 8); break;
+        case 16: PF_REDUCE(GEMV_STORE, 16); break;
+        case 34: PF_REDUCE(GEMV_RESID, 2); break;
+        case 36: PF_REDUCE(GEMV_RESID, 4); break;
+        case 40: PF_REDUCE(GEMV_RESID, 8); break;
+        case 48: PF_REDUCE(GEMV_RESID, 16); break;
+        case 66: PF_REDUCE(GEMV_SILU, 2); break;
+        case 68: PF_REDUCE(GEMV_SILU, 4); break;
+        case 72: PF_REDUCE(GEMV_SILU, 8); break;
+        case 80: PF_REDUCE(GEMV_SILU, 16); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef PF_REDUCE
+    return hipGetLastError();
+}
+
 // The launch of launch_pf_gemm for weights of format T (arguments checked).
 template <int T>
 hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
@@ -1496,85 +1612,57 @@ hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
             }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess || ks == 1) return e;
-            if (a.mode == GEMV_STORE && a.rope_cos && a.rope_sin && a.kc && a.vc && a.n_seg == 3 && a.hd % 2 == 0 &&
-                a.seg[0].w.N == (int64_t)a.n_head * a.hd && a.seg[1].w.N == (int64_t)a.n_kv * a.hd &&
-                a.seg[2].w.N == (int64_t)a.n_kv * a.hd) {
-                const int items = (a.n_head + a.n_kv) * (a.hd / 2) + a.n_kv * a.hd;
-                const dim3 qgrid((unsigned)((items + kBlock - 1) / kBlock), (unsigned)a.M);
-#define PF_RROPE(KS) hipLaunchKernelGGL((k_pf_reduce_rope<KS>), qgrid, dim3(kBlock), 0, st, b)
-                switch (ks) {
-                    case 2: PF_RROPE(2); break;
-                    case 4: PF_RROPE(4); break;
-                    case 8: PF_RROPE(8); break;
-                    case 16: PF_RROPE(16); break;
-                    default: return hipErrorInvalidValue;
-                }
-#undef PF_RROPE
-                e = hipGetLastError();
-                if (e == hipSuccess && fused) *fused = true;
-                return e;
-            }
-            const int ngr = a.n_sub * 2;  // 8-column groups of an output row
-            if (a.mode == GEMV_RESID && a.split_xa && a.split_rs && a.n_seg == 1 && a.seg[0].ldy % 4 == 0 && a.seg[0].ldy >= ngr * 8 &&
-                ((uintptr_t)a.seg[0].y & 15) == 0 && ngr <= 4 * kBlock) {
-                const int ng = ngr <= kBlock ? 1 : (ngr <= 2 * kBlock ? 2 : 4);
-#define PF_RSPLIT(KS, NG) hipLaunchKernelGGL((k_pf_reduce_split<KS, NG>), dim3((unsigned)a.Mpad), dim3(kBlock), 0, st, b)
-                switch (ks * 8 + ng) {  // ks is 2, 4, 8 or 16 here
-                    case 17: PF_RSPLIT(2, 1); break;
-                    case 18: PF_RSPLIT(2, 2); break;
-                    case 20: PF_RSPLIT(2, 4); break;
-                    case 33: PF_RSPLIT(4, 1); break;
-                    case 34: PF_RSPLIT(4, 2); break;
-                    case 36: PF_RSPLIT(4, 4); break;
-                    case 65: PF_RSPLIT(8, 1); break;
-                    case 66: PF_RSPLIT(8, 2); break;
-                    case 68: PF_RSPLIT(8, 4); break;
-                    case 129: PF_RSPLIT(16, 1); break;
-                    case 130: PF_RSPLIT(16, 2); break;
-                    case 132: PF_RSPLIT(16, 4); break;
-                    default: return hipErrorInvalidValue;
-                }
-#undef PF_RSPLIT
-                e = hipGetLastError();
-                if (e == hipSuccess && fused) *fused = true;
-                return e;
-            }
-            const dim3 rgrid((unsigned)((a.n_sub * 4 + kBlock - 1) / kBlock), (unsigned)a.M);
-#define PF_REDUCE(MODE, KS) hipLaunchKernelGGL((k_pf_reduce<MODE, KS>), rgrid, dim3(kBlock), 0, st, b)
-            switch ((a.mode == GEMV_STORE ? 0 : 32) + ks) {  // ks is 2, 4, 8 or 16 here
-                case 2: PF_REDUCE(GEMV_STORE, 2); break;
-                case 4: PF_REDUCE(GEMV_STORE, 4); break;
-                case 8: PF_REDUCE(GEMV_STORE, 8); break;
-                case 16: PF_REDUCE(GEMV_STORE, 16); break;
-                case 34: PF_REDUCE(GEMV_RESID, 2); break;
-                case 36: PF_REDUCE(GEMV_RESID, 4); break;
-                case 40: PF_REDUCE(GEMV_RESID, 8); break;
-                case 48: PF_REDUCE(GEMV_RESID, 16); break;
-                default: return hipErrorInvalidValue;
-            }
-#undef PF_REDUCE
-            return hipGetLastError();
+            return launch_split_reduce(b, ks, st, fused);
         }
     }
     // 4 column subtiles per wave; 2 when that leaves fewer than two workgroups per CU
+    const int cus = device_cu_count();
     const int mt = a.Mpad / kPfTileM;
     const int out4 = a.mode == GEMV_SILU ? 2 : 4;
     const int wg4 = (a.n_sub + 2 * out4 - 1) / (2 * out4) * mt;
-    const int ni = wg4 >= 2 * device_cu_count() ? 4 : 2;
+    const int ni = wg4 >= 2 * cus ? 4 : 2;
     const int per_wg = 2 * (a.mode == GEMV_SILU ? ni / 2 : ni);  // output subtiles per workgroup column
-    const dim3 grid((unsigned)((a.n_sub + per_wg - 1) / per_wg * mt));
-#define PF_LAUNCH(MODE, NI) hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T>), grid, dim3(256), 0, st, a)
-    switch (a.mode * 8 + ni) {
-        case GEMV_STORE * 8 + 4: PF_LAUNCH(GEMV_STORE, 4); break;
-        case GEMV_STORE * 8 + 2: PF_LAUNCH(GEMV_STORE, 2); break;
-        case GEMV_RESID * 8 + 4: PF_LAUNCH(GEMV_RESID, 4); break;
-        case GEMV_RESID * 8 + 2: PF_LAUNCH(GEMV_RESID, 2); break;
-        case GEMV_SILU * 8 + 4: PF_LAUNCH(GEMV_SILU, 4); break;
-        case GEMV_SILU * 8 + 2: PF_LAUNCH(GEMV_SILU, 2); break;
+    const int n_wg = (a.n_sub + per_wg - 1) / per_wg * mt;
+    // Few tiles (a short prompt: every weight byte is read once whatever the row count, so
+    // the time is the weight stream's): K in slices too, by the same span rule with two
+    // workgroups per CU, slices of at least 2 stages (4 blocks)
+    int ks = 1;
+    if (n_wg < 2 * cus && a.part) {
+        const int S = a.K / 64, slots = 2 * cus;
+        const size_t per_slice = (size_t)a.Mpad * a.n_sub * 16 * (a.mode == GEMV_SILU ? 2 : 1);
+        int64_t best = (int64_t)((n_wg + slots - 1) / slots) * S;
+        for (int k = 2; k <= 16; k *= 2) {
+            if (S % k != 0 || S / k < 2 || (size_t)k * per_slice > a.part_floats) break;
+            const int64_t span = (int64_t)((n_wg * k + slots - 1) / slots) * (S / k);
+            if (span < best) {
+                best = span;
+                ks = k;
+            }
+        }
+    }
+    PfGemmArgs b = a;
+    b.ks = ks;
+    const dim3 grid((unsigned)(n_wg * ks));
+#define PF_LAUNCH(MODE, NI, SP) hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T, SP>), grid, dim3(256), 0, st, b)
+    switch (a.mode * 16 + ni * 2 + (ks > 1 ? 1 : 0)) {
+        case GEMV_STORE * 16 + 8: PF_LAUNCH(GEMV_STORE, 4, false); break;
+        case GEMV_STORE * 16 + 4: PF_LAUNCH(GEMV_STORE, 2, false); break;
+        case GEMV_STORE * 16 + 9: PF_LAUNCH(GEMV_STORE, 4, true); break;
+        case GEMV_STORE * 16 + 5: PF_LAUNCH(GEMV_STORE, 2, true); break;
+        case GEMV_RESID * 16 + 8: PF_LAUNCH(GEMV_RESID, 4, false); break;
+        case GEMV_RESID * 16 + 4: PF_LAUNCH(GEMV_RESID, 2, false); break;
+        case GEMV_RESID * 16 + 9: PF_LAUNCH(GEMV_RESID, 4, true); break;
+        case GEMV_RESID * 16 + 5: PF_LAUNCH(GEMV_RESID, 2, true); break;
+        case GEMV_SILU * 16 + 8: PF_LAUNCH(GEMV_SILU, 4, false); break;
+        case GEMV_SILU * 16 + 4: PF_LAUNCH(GEMV_SILU, 2, false); break;
+        case GEMV_SILU * 16 + 9: PF_LAUNCH(GEMV_SILU, 4, true); break;
+        case GEMV_SILU * 16 + 5: PF_LAUNCH(GEMV_SILU, 2, true); break;
         default: return hipErrorInvalidValue;
     }
 #undef PF_LAUNCH
-    return hipGetLastError();
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || ks == 1) return e;
+    return launch_split_reduce(b, ks, st, fused);
 }
 
 }  // namespace

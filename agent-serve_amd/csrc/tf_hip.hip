@@ -1362,10 +1362,9 @@ int tf_hip_matmul(int device, int t, const void* w, int64_t ne0, int64_t ne1, co
         PfGemmArgs a;
         a.xa = xa;
         a.rs = rs;
-        if (Mpad % 128 == 0) {  // workspace for K slices of the large-tile kernel
-            a.part_floats = (size_t)8 * Mpad * ne1;
-            OPCHK(s.alloc(&a.part, a.part_floats * 4));
-        }
+        // workspace for K slices (up to 8 of them, as a model context's chunk buffers hold)
+        a.part_floats = (size_t)8 * Mpad * ne1;
+        OPCHK(s.alloc(&a.part, a.part_floats * 4));
         a.K = (int)ne0;
         a.M = n_rows_x;
         a.Mpad = Mpad;
