@@ -286,7 +286,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
 // of 16 (GEMV_SILU: NI / 2 output subtiles, each a gate and an up subtile). Per subtile: its
 // segment, the weight row c this lane reads (the output column), whether it is past the
 // last subtile (computed on a clamped one, not written).
-template <int MODE, int NI>
+template <int MODE, int NI, int MI = 2>
 struct TileCtx {
     static constexpr int NO = MODE == GEMV_SILU ? NI / 2 : NI;  // output subtiles per wave
     int lane, l16, lc, m0;
@@ -311,10 +311,12 @@ struct TileCtx {
         }
         kslice = b % ks;
         b /= ks;
-        const int MT = a.Mpad / kPfTileM;
+        // MI == 2: 64-row tiles, waves 2 (rows, 2 subtiles each) x 2 (columns); MI == 1 (at
+        // most 16 rows): one 16-row subtile, all 4 waves along the columns
+        const int MT = MI == 2 ? a.Mpad / kPfTileM : (a.M + 15) / 16;
         const int mt = b % MT, nt = b / MT;
-        m0 = mt * kPfTileM + (wave & 1) * 32;
-        const int wid = nt * 2 + (wave >> 1);
+        m0 = MI == 2 ? mt * kPfTileM + (wave & 1) * 32 : mt * 16;
+        const int wid = MI == 2 ? nt * 2 + (wave >> 1) : nt * 4 + wave;
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
             int u = wid * NO + ni % NO;
@@ -336,17 +338,17 @@ struct TileCtx {
     }
     __device__ __forceinline__ static bool up(int ni) { return MODE == GEMV_SILU && ni >= NO; }
     // fragment pointers of the wave's two 16-row activation subtiles (lane's 8 halves)
-    __device__ __forceinline__ void act(const PfGemmArgs& a, const TF_GLOBAL h8_t* (&ap)[2]) const {
+    __device__ __forceinline__ void act(const PfGemmArgs& a, const TF_GLOBAL h8_t* (&ap)[MI]) const {
         const int nblk = a.K / 32;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < MI; ++mi)
             ap[mi] = (const TF_GLOBAL h8_t*)a.xa + (int64_t)(m0 / 16 + mi) * nblk * 128 + lane;
     }
     // lane holds rows m0 + 16 mi + 4 (lane / 16) + r of output column c[ni], scaled back by
     // the row scales: store (+ bias), residual add (+ the tap row) or silu(gate) * up
-    __device__ __forceinline__ void epilogue(const PfGemmArgs& a, const f4_t (&acc)[2][NI]) const {
+    __device__ __forceinline__ void epilogue(const PfGemmArgs& a, const f4_t (&acc)[MI][NI]) const {
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
+        for (int mi = 0; mi < MI; ++mi) {
             const int r0 = m0 + 16 * mi + 4 * (lane >> 4);
             const float4 rsv = *(const float4*)(a.rs + r0);
             const float rsa[4] = {rsv.x, rsv.y, rsv.z, rsv.w};
@@ -377,12 +379,12 @@ struct TileCtx {
     // a K slice's row-scaled partial sums: part[kslice][row][output column] (the big tiles'
     // layout, read by the same reduces)
     // (GEMV_SILU: the gate columns, then the up columns)
-    __device__ __forceinline__ void epilogue_part(const PfGemmArgs& a, const f4_t (&acc)[2][NI]) const {
+    __device__ __forceinline__ void epilogue_part(const PfGemmArgs& a, const f4_t (&acc)[MI][NI]) const {
         const int nout = a.n_sub * 16;
         const int ntot = MODE == GEMV_SILU ? 2 * nout : nout;
         float* part = a.part + (int64_t)kslice * a.Mpad * ntot;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
+        for (int mi = 0; mi < MI; ++mi) {
             const int r0 = m0 + 16 * mi + 4 * (lane >> 4);
             const float4 rsv = *(const float4*)(a.rs + r0);
             const float rsa[4] = {rsv.x, rsv.y, rsv.z, rsv.w};
@@ -403,10 +405,10 @@ struct TileCtx {
 // same two MFMAs against a fragment of ones). Weight bytes and activation fragments stream
 // from L2 into registers, one stage of two blocks ahead; every load is unconditional
 // (indices clamped) so the compiler waits only for the stage it consumes.
-template <int MODE, int NI, int T, bool SPLIT>
+template <int MODE, int NI, int T, bool SPLIT, int MI>
 __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
     using W = PfW<T>;
-    const TileCtx<MODE, NI> t(a, SPLIT ? a.ks : 1);
+    const TileCtx<MODE, NI, MI> t(a, SPLIT ? a.ks : 1);
     const int K = a.K, nblk = K / 32;
     constexpr int SW = W::kScale == 4 ? 2 : 1;  // scale words per stage and column
     const TF_GLOBAL uint8_t* bp[NI];
@@ -416,17 +418,17 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
         bp[ni] = (const TF_GLOBAL uint8_t*)t.wq[ni] + (int64_t)t.c[ni] * nblk * W::kBytes + W::off(t.lc);
         sp[ni] = (const TF_GLOBAL uint32_t*)(t.ws[ni] + (int64_t)t.c[ni] * nblk * W::kScale);
     }
-    const TF_GLOBAL h8_t* ap[2];
+    const TF_GLOBAL h8_t* ap[MI];
     t.act(a, ap);
 
-    f4_t acc[2][NI];
+    f4_t acc[MI][NI];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
 
     struct Stage {
-        h8_t ah[2][2], al[2][2];    // [row subtile][block]
+        h8_t ah[MI][2], al[MI][2];  // [row subtile][block]
         typename W::Raw bw[NI][2];  // [column subtile][block]: the lane's weight bytes
         uint32_t d[NI][SW];         // the scale words of the stage's two blocks
     };
@@ -438,7 +440,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
         for (int j = 0; j < 2; ++j) {
             const int blk = 2 * s + j;
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
+            for (int mi = 0; mi < MI; ++mi) {
                 g.ah[mi][j] = ap[mi][blk * 128];
                 g.al[mi][j] = ap[mi][blk * 128 + 64];
             }
@@ -458,9 +460,9 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
             h8_t bh[NI];
 #pragma unroll
             for (int ni = 0; ni < NI; ++ni) bh[ni] = W::cvt(g.bw[ni][j], t.lc);
-            f4_t tb[2][NI], ts[2];
+            f4_t tb[MI][NI], ts[MI];
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
+            for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni)
                     tb[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.ah[mi][j], bh[ni],
@@ -470,7 +472,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
                                                                     0, 0, 0);
             }
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
+            for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
                 for (int ni = 0; ni < NI; ++ni)
                     tb[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.al[mi][j], bh[ni], tb[mi][ni], 0, 0, 0);
@@ -481,7 +483,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
                 float dv, mv;
                 pf_scale<W::kScale>(g.d[ni][SW == 2 ? j : 0], j, dv, mv);
 #pragma unroll
-                for (int mi = 0; mi < 2; ++mi)
+                for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                         acc[mi][ni][r] = W::kMin ? fmaf(dv, tb[mi][ni][r], fmaf(mv, ts[mi][r], acc[mi][ni][r]))
@@ -1615,13 +1617,17 @@ hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
             return launch_split_reduce(b, ks, st, fused);
         }
     }
-    // 4 column subtiles per wave; 2 when that leaves fewer than two workgroups per CU
+    // 64-row tiles with two waves along the rows, or, for at most 16 rows, 16-row tiles with
+    // all four waves along the columns (a quarter of the activation reads per weight byte);
+    // 4 column subtiles per wave, 2 when that leaves fewer than two workgroups per CU
     const int cus = device_cu_count();
-    const int mt = a.Mpad / kPfTileM;
+    const bool rows16 = a.M <= 16;
+    const int mt = rows16 ? (a.M + 15) / 16 : a.Mpad / kPfTileM;
+    const int wcols = rows16 ? 4 : 2;  // waves along the columns
     const int out4 = a.mode == GEMV_SILU ? 2 : 4;
-    const int wg4 = (a.n_sub + 2 * out4 - 1) / (2 * out4) * mt;
+    const int wg4 = (a.n_sub + wcols * out4 - 1) / (wcols * out4) * mt;
     const int ni = wg4 >= 2 * cus ? 4 : 2;
-    const int per_wg = 2 * (a.mode == GEMV_SILU ? ni / 2 : ni);  // output subtiles per workgroup column
+    const int per_wg = wcols * (a.mode == GEMV_SILU ? ni / 2 : ni);  // output subtiles per workgroup column
     const int n_wg = (a.n_sub + per_wg - 1) / per_wg * mt;
     // Few tiles (a short prompt: every weight byte is read once whatever the row count, so
     // the time is the weight stream's): K in slices too, by the same span rule with two
@@ -1643,7 +1649,13 @@ hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
     PfGemmArgs b = a;
     b.ks = ks;
     const dim3 grid((unsigned)(n_wg * ks));
-#define PF_LAUNCH(MODE, NI, SP) hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T, SP>), grid, dim3(256), 0, st, b)
+#define PF_LAUNCH(MODE, NI, SP)                                                                      \
+    do {                                                                                           \
+        if (rows16)                                                                                \
+            hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T, SP, 1>), grid, dim3(256), 0, st, b);   \
+        else                                                                                       \
+            hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T, SP, 2>), grid, dim3(256), 0, st, b);   \
+    } while (0)
     switch (a.mode * 16 + ni * 2 + (ks > 1 ? 1 : 0)) {
         case GEMV_STORE * 16 + 8: PF_LAUNCH(GEMV_STORE, 4, false); break;
         case GEMV_STORE * 16 + 4: PF_LAUNCH(GEMV_STORE, 2, false); break;
