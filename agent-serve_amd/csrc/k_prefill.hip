@@ -286,7 +286,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_split(const float* x, int64_t ldx
 // of 16 (GEMV_SILU: NI / 2 output subtiles, each a gate and an up subtile). Per subtile: its
 // segment, the weight row c this lane reads (the output column), whether it is past the
 // last subtile (computed on a clamped one, not written).
-template <int MODE, int NI, int MI = 2>
+template <int MODE, int NI, int MI = 2, int WM = 2>
 struct TileCtx {
     static constexpr int NO = MODE == GEMV_SILU ? NI / 2 : NI;  // output subtiles per wave
     int lane, l16, lc, m0;
@@ -311,12 +311,12 @@ struct TileCtx {
         }
         kslice = b % ks;
         b /= ks;
-        // MI == 2: 64-row tiles, waves 2 (rows, 2 subtiles each) x 2 (columns); MI == 1 (at
-        // most 16 rows): one 16-row subtile, all 4 waves along the columns
-        const int MT = MI == 2 ? a.Mpad / kPfTileM : (a.M + 15) / 16;
+        // WM == 2: 64-row tiles, waves 2 (rows, MI = 2 subtiles each) x 2 (columns); WM == 1:
+        // tiles of MI 16-row subtiles, all 4 waves along the columns
+        const int MT = WM == 2 ? a.Mpad / kPfTileM : (a.M + 16 * MI - 1) / (16 * MI);
         const int mt = b % MT, nt = b / MT;
-        m0 = MI == 2 ? mt * kPfTileM + (wave & 1) * 32 : mt * 16;
-        const int wid = MI == 2 ? nt * 2 + (wave >> 1) : nt * 4 + wave;
+        m0 = WM == 2 ? mt * kPfTileM + (wave & 1) * 32 : mt * 16 * MI;
+        const int wid = WM == 2 ? nt * 2 + (wave >> 1) : nt * 4 + wave;
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
             int u = wid * NO + ni % NO;
@@ -405,10 +405,10 @@ struct TileCtx {
 // same two MFMAs against a fragment of ones). Weight bytes and activation fragments stream
 // from L2 into registers, one stage of two blocks ahead; every load is unconditional
 // (indices clamped) so the compiler waits only for the stage it consumes.
-template <int MODE, int NI, int T, bool SPLIT, int MI>
+template <int MODE, int NI, int T, bool SPLIT, int MI, int WM>
 __global__ __launch_bounds__(256) void k_pf_gemm_tile(const PfGemmArgs a) {
     using W = PfW<T>;
-    const TileCtx<MODE, NI, MI> t(a, SPLIT ? a.ks : 1);
+    const TileCtx<MODE, NI, MI, WM> t(a, SPLIT ? a.ks : 1);
     const int K = a.K, nblk = K / 32;
     constexpr int SW = W::kScale == 4 ? 2 : 1;  // scale words per stage and column
     const TF_GLOBAL uint8_t* bp[NI];
@@ -1555,6 +1555,10 @@ hipError_t launch_split_reduce(const PfGemmArgs& a, int ks, hipStream_t st, bool
     return hipGetLastError();
 }
 
+// Row counts up to which the register-streamed tiles put all four waves along the columns
+// (33-64 rows as two 32-row tiles measured the same as one 64-row tile).
+constexpr int kSmallRows = 32;
+
 // The launch of launch_pf_gemm for weights of format T (arguments checked).
 template <int T>
 hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
@@ -1617,13 +1621,14 @@ hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
             return launch_split_reduce(b, ks, st, fused);
         }
     }
-    // 64-row tiles with two waves along the rows, or, for at most 16 rows, 16-row tiles with
-    // all four waves along the columns (a quarter of the activation reads per weight byte);
-    // 4 column subtiles per wave, 2 when that leaves fewer than two workgroups per CU
+    // 64-row tiles with two waves along the rows, or, for at most 32 rows, tiles of 16 rows
+    // (at most 16) or 32 with all four waves along the columns (fewer activation reads per
+    // weight byte); 4 column subtiles per wave, 2 when that leaves fewer than two workgroups
+    // per CU
     const int cus = device_cu_count();
-    const bool rows16 = a.M <= 16;
-    const int mt = rows16 ? (a.M + 15) / 16 : a.Mpad / kPfTileM;
-    const int wcols = rows16 ? 4 : 2;  // waves along the columns
+    const int shape = a.M <= 16 ? 1 : (a.M <= kSmallRows ? 2 : 0);  // 16-row, 32-row or 64-row tiles
+    const int mt = shape == 0 ? a.Mpad / kPfTileM : (a.M + 16 * shape - 1) / (16 * shape);
+    const int wcols = shape ? 4 : 2;  // waves along the columns
     const int out4 = a.mode == GEMV_SILU ? 2 : 4;
     const int wg4 = (a.n_sub + wcols * out4 - 1) / (wcols * out4) * mt;
     const int ni = wg4 >= 2 * cus ? 4 : 2;
@@ -1651,10 +1656,12 @@ hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
     const dim3 grid((unsigned)(n_wg * ks));
 #define PF_LAUNCH(MODE, NI, SP)                                                                      \
     do {                                                                                           \
-        if (rows16)                                                                                \
-            hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T, SP, 1>), grid, dim3(256), 0, st, b);   \
+        if (shape == 1)                                                                            \
+            hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T, SP, 1, 1>), grid, dim3(256), 0, st, b); \
+        else if (shape == 2)                                                                       \
+            hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T, SP, 2, 1>), grid, dim3(256), 0, st, b); \
         else                                                                                       \
-            hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T, SP, 2>), grid, dim3(256), 0, st, b);   \
+            hipLaunchKernelGGL((k_pf_gemm_tile<MODE, NI, T, SP, 2, 2>), grid, dim3(256), 0, st, b); \
     } while (0)
     switch (a.mode * 16 + ni * 2 + (ks > 1 ? 1 : 0)) {
         case GEMV_STORE * 16 + 8: PF_LAUNCH(GEMV_STORE, 4, false); break;
