@@ -116,7 +116,7 @@ def test_matmul_several_rows(pkg):
 
 # (M, K, N) of the prefill GEMM: row counts around the 64-row tile, the workloads' K
 PF_GEMM_SHAPES = [(2, 64, 16), (37, 2048, 256), (64, 896, 1152), (100, 8192, 128), (130, 1536, 48),
-                  (512, 2048, 64), (65, 8960, 32), (7, 192, 320),
+                  (512, 2048, 64), (65, 8960, 32), (7, 192, 320), (24, 2048, 512), (11, 8192, 2048),
                   (500, 256, 16384),  # enough 128 x 256 tiles for every CU: the LDS-staged kernel
                   (512, 2048, 2048),  # 32 such tiles, K split in 8 slices and reduced
                   (512, 512, 12288)]  # 192 such tiles, unsplit (slices would not shorten the span)
