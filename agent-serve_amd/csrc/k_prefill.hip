@@ -1049,6 +1049,57 @@ __global__ __launch_bounds__(kBlock) void k_pf_reduce_split(const PfGemmArgs a) 
 }
 
 
+// k_pf_reduce of a GEMV_SILU GEMM (gate columns, then up columns, K split) fused with the
+// split of its rows (k_pf_split without a norm, a workgroup per row): thread t owns the
+// 8-column groups t, t + 256, ...; each gate and up sum adds the slices in slice order as
+// k_pf_reduce does, silu(gate) * up as the GEMM's epilogue computes it, then the row's
+// power-of-two scale and its hi + lo fragments. The rows themselves are not stored: only
+// the next GEMM reads them, from the fragments. Rows M.. get the padding zeros.
+template <int KS, int NG>
+__global__ __launch_bounds__(kBlock) void k_pf_reduce_silu_split(const PfGemmArgs a) {
+    __shared__ double red_d[kWavesPerBlock];
+    __shared__ float red_f[kWavesPerBlock];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const int F = a.n_sub * 16, ng = F / 8;
+    if (m >= a.M) {
+        split_zero<kBlock>(tid, m, F, (h8_t*)a.split_xa, a.split_rs);
+        return;
+    }
+    const float* p = a.part + (int64_t)m * 2 * F;
+    const int64_t sstride = (int64_t)a.Mpad * 2 * F;
+    float v[NG][8];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const int j = tid + i * kBlock;
+        const int jj = j < ng ? j : ng - 1;  // a clamped re-read, masked in the split
+        float g[8] = {0, 0, 0, 0, 0, 0, 0, 0}, u[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float4 pv[KS][2];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            pv[k][0] = *(const float4*)(p + k * sstride + 8 * jj);
+            pv[k][1] = *(const float4*)(p + k * sstride + 8 * jj + 4);
+        }
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            g[0] += pv[k][0].x; g[1] += pv[k][0].y; g[2] += pv[k][0].z; g[3] += pv[k][0].w;
+            g[4] += pv[k][1].x; g[5] += pv[k][1].y; g[6] += pv[k][1].z; g[7] += pv[k][1].w;
+        }
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            pv[k][0] = *(const float4*)(p + F + k * sstride + 8 * jj);
+            pv[k][1] = *(const float4*)(p + F + k * sstride + 8 * jj + 4);
+        }
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            u[0] += pv[k][0].x; u[1] += pv[k][0].y; u[2] += pv[k][0].z; u[3] += pv[k][0].w;
+            u[4] += pv[k][1].x; u[5] += pv[k][1].y; u[6] += pv[k][1].z; u[7] += pv[k][1].w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = (g[e] / (1.0f + expf(-g[e]))) * u[e];
+    }
+    split_emit<NG, 4>(v, tid, m, F, nullptr, 0.0f, (h8_t*)a.split_xa, a.split_rs, red_d, red_f);
+}
+
 // ---------------------------------------------------------------- RoPE and KV store
 
 // Row i is position pos0 + i: q heads rotated in place, k heads rotated into the cache,
@@ -1531,6 +1582,29 @@ hipError_t launch_split_reduce(const PfGemmArgs& a, int ks, hipStream_t st, bool
         }
 #undef PF_RSPLIT
         e = hipGetLastError();
+        if (e == hipSuccess && fused) *fused = true;
+        return e;
+    }
+    const int ngs = a.n_sub * 2 <= kBlock ? 1 : (a.n_sub * 2 <= 2 * kBlock ? 2 : (a.n_sub * 2 <= 4 * kBlock ? 4 : 8));
+    // (a thread's partial loads, ks x groups, kept to 16 so that they stay in registers)
+    if (a.mode == GEMV_SILU && a.split_xa && a.split_rs && a.n_sub * 2 <= 8 * kBlock && ks * ngs <= 16) {
+        const int ng = ngs;  // 8-column groups of an output row per thread
+#define PF_RSS(KS, NG) hipLaunchKernelGGL((k_pf_reduce_silu_split<KS, NG>), dim3((unsigned)a.Mpad), dim3(kBlock), 0, st, a)
+        switch (ks * 16 + ng) {  // ks is 2, 4, 8 or 16 here
+            case 33: PF_RSS(2, 1); break;
+            case 34: PF_RSS(2, 2); break;
+            case 36: PF_RSS(2, 4); break;
+            case 40: PF_RSS(2, 8); break;
+            case 65: PF_RSS(4, 1); break;
+            case 66: PF_RSS(4, 2); break;
+            case 68: PF_RSS(4, 4); break;
+            case 129: PF_RSS(8, 1); break;
+            case 130: PF_RSS(8, 2); break;
+            case 257: PF_RSS(16, 1); break;
+            default: return hipErrorInvalidValue;
+        }
+#undef PF_RSS
+        const hipError_t e = hipGetLastError();
         if (e == hipSuccess && fused) *fused = true;
         return e;
     }

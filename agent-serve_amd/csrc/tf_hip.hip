@@ -777,9 +777,12 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                 a.mode = GEMV_SILU;
                 seg(a, M(TF_HIP_LAYER_GATE), c->ph, F, nullptr);
                 a.seg[0].w2 = mat(c, M(TF_HIP_LAYER_UP));
-                chk(launch_pf_gemm(a, c->st));
+                a.split_xa = c->pxa;  // a K-split reduce also splits the hidden rows
+                a.split_rs = c->prs;
+                bool done = false;
+                chk(launch_pf_gemm(a, c->st, &done));
+                if (!done) chk(launch_pf_split(c->ph, F, nullptr, 0.0f, F, nc, Mpad, c->pxa, c->prs, c->st));
             }
-            chk(launch_pf_split(c->ph, F, nullptr, 0.0f, F, nc, Mpad, c->pxa, c->prs, c->st));
             {
                 PfGemmArgs a = base(F);
                 a.mode = GEMV_RESID;

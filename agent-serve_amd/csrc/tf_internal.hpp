@@ -191,7 +191,8 @@ struct PfGemmArgs {
     // Work the split-K reduce can take over from the kernel that follows the GEMM
     // (launch_pf_gemm reports through *fused whether it did):
     // GEMV_RESID over one segment, split_xa set: the split of every updated row
-    // (launch_pf_split of the output rows, rmsnorm with split_w when given)
+    // (launch_pf_split of the output rows, rmsnorm with split_w when given); GEMV_SILU with
+    // K split, split_xa set: the split of the silu * up rows, which are then not stored
     uint16_t* split_xa = nullptr;
     float* split_rs = nullptr;
     const float* split_w = nullptr;
