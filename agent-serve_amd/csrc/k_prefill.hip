@@ -851,11 +851,15 @@ __global__ __launch_bounds__(kBigThreads) void k_pf_gemm_big(const PfGemmArgs a)
             resolve(qb[ni], u, seg, up);
             if (uraw >= a.n_sub) continue;
             if (SPLIT) {
-                const int ntot = a.n_sub * 16;
+                // GEMV_SILU: the gate columns, then the up columns
+                const int nout = a.n_sub * 16, ntot = SILU ? 2 * nout : nout;
                 float* part = a.part + ((int64_t)kslice * a.Mpad) * ntot + u * 16 + l16;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    if (r0 + r < a.M) part[(int64_t)(r0 + r) * ntot] = acc[mi][ni][r] * rsa[r];
+                    if (r0 + r < a.M) {
+                        part[(int64_t)(r0 + r) * ntot] = acc[mi][ni][r] * rsa[r];
+                        if (SILU) part[(int64_t)(r0 + r) * ntot + nout] = acc[mi][ni + 2][r] * rsa[r];
+                    }
                 continue;
             }
             const int c = (u - PF_SEL(seg, sub0)) * 16 + l16;
@@ -1643,7 +1647,7 @@ hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
         const int cus = device_cu_count();
         int ks = 1;
         bool big = n_big >= cus;
-        if (!big && a.mode != GEMV_SILU && a.part) {
+        if (!big && a.part) {
             // K slices by the span they give: rounds of workgroups over the CUs times
             // stages per slice; the fewest slices with the shortest span (each split adds
             // its reduce), each slice at least 8 stages long (shorter slices spend more on
@@ -1651,7 +1655,7 @@ hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
             // 4 when that fits the CUs in one round. Big tiles when at least half the CUs
             // get one.
             const int S = a.K / 64;
-            const size_t per_slice = (size_t)a.Mpad * a.n_sub * 16;
+            const size_t per_slice = (size_t)a.Mpad * a.n_sub * 16 * (a.mode == GEMV_SILU ? 2 : 1);
             int64_t best = (int64_t)((n_big + cus - 1) / cus) * S;
             for (int k = 2; k <= 16; k *= 2) {
                 if (S % k != 0 || S / k < 4 || (S / k < 8 && n_big * k > cus) ||
@@ -1688,7 +1692,8 @@ hipError_t launch_gemm_t(const PfGemmArgs& a, hipStream_t st, bool* fused) {
                 case 1: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_RESID, false, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
                 case 2: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_SILU, false, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
                 case 3: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_STORE, true, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
-                default: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_RESID, true, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                case 4: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_RESID, true, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
+                default: hipLaunchKernelGGL((k_pf_gemm_big<GEMV_SILU, true, T>), grid, dim3(kBigThreads), kBigLdsBytes, st, b); break;
             }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess || ks == 1) return e;

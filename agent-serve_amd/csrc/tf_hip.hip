@@ -644,7 +644,8 @@ int ensure_pf(tf_hip_ctx* c) {
     }
     if (!pf_attn_supported(p.head_dim, p.n_head / p.n_kv_head)) return 0;
     if (!c->px) {
-        const int cap = std::min((p.max_seq + kPfTileM - 1) / kPfTileM * kPfTileM, kPfChunk);
+        // rows of a chunk, padded to the large GEMM tiles' 128 (kPfChunk is a multiple)
+        const int cap = std::min((p.max_seq + 127) / 128 * 128, kPfChunk);
         const size_t D = (size_t)p.n_embd, F = (size_t)p.n_ff, NQ = (size_t)c->H + 2 * (size_t)c->KVd;
         const size_t kmax = std::max({D, F, (size_t)c->H});
         if ((rc = dalloc(c, &c->px, cap * D * 4)) || (rc = dalloc(c, &c->pqkv, cap * NQ * 4)) ||
@@ -679,7 +680,8 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
     int nc = 0;
     for (int c0 = 0; c0 < n && e == hipSuccess; c0 += nc) {
         nc = std::min(c->pf_cap, n - c0);
-        const int Mpad = (nc + kPfTileM - 1) / kPfTileM * kPfTileM;
+        // beyond one 64-row tile, whole 128-row tiles: the large-tile GEMMs take any row count
+        const int Mpad = nc <= kPfTileM ? kPfTileM : (nc + 127) / 128 * 128;
         const int pos0 = start + c0;
         const bool last = c0 + nc == n;
         chk(launch_embed_rows(mat(c, TF_HIP_SLOT_TOKEN_EMBD), c->hist + pos0, nc, c->px, D, c->st));
