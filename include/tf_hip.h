@@ -172,10 +172,12 @@ int tf_hip_test_refuse_cooperative(tf_hip_ctx* ctx, int32_t n);
 /* Prefill path (no counterpart in the reference, whose layer_prefill is the one
  * path, model.cpp:144-195): TF_HIP_PREFILL_MFMA runs a prompt of two or more tokens
  * through the matrix-core GEMMs and the causal chunk attention when every layer
- * matrix is Q8_0 with row lengths divisible by 64 (at most 16384) and output lengths by 16 and the head
- * size is 32, 64 or 128 (the default); otherwise, and under TF_HIP_PREFILL_TOKENS,
- * prompt tokens run one at a time through the decode path with attention limited to
- * the prompt. get returns the path a prompt would take (or < 0 on error). */
+ * matrix is Q8_0, Q4_0, Q4_1, F16, F32 or Q6_K with row lengths divisible by 64 (256 for
+ * Q6_K; at most 16384) and output lengths by 16, ffn_gate and ffn_up share a format, the
+ * head size is 32, 64 or 128 and a kv head has at most 8 query heads (the default);
+ * otherwise, and under TF_HIP_PREFILL_TOKENS, prompt tokens run one at a time through the
+ * decode path with attention limited to the prompt. get returns the path a prompt would
+ * take (or < 0 on error). */
 #define TF_HIP_PREFILL_TOKENS 0
 #define TF_HIP_PREFILL_MFMA 1
 int tf_hip_set_prefill_path(tf_hip_ctx* ctx, int32_t path);
@@ -222,9 +224,9 @@ int tf_hip_dequant_rows(int device, int ggml_type, const void* w, int64_t ne0, i
                         int64_t nrows, float* out);
 
 /* matmul (matmul.cpp:64-73): y[m][n] = sum_k x[m][k] * W[n][k] for m < n_rows_x.
- * One row runs the decode GEMV. Two or more rows of a Q8_0 matrix with ne0 % 64 == 0,
- * ne0 <= 16384 and ne1 % 16 == 0 run the prefill GEMM on the matrix cores; other shapes
- * and formats run the GEMV once per row. */
+ * One row runs the decode GEMV. Two or more rows of a Q8_0, Q4_0, Q4_1, F16, F32 or Q6_K
+ * matrix with ne0 % 64 == 0 (Q6_K: % 256), ne0 <= 16384 and ne1 % 16 == 0 run the prefill
+ * GEMM on the matrix cores; other shapes run the GEMV once per row. */
 int tf_hip_matmul(int device, int ggml_type, const void* w, int64_t ne0, int64_t ne1, const float* x,
                   int32_t n_rows_x, float* y);
 
