@@ -20,7 +20,8 @@ one-launch greedy loop over the same tokens gives the config's roofline object, 
 reference --stage v2 path (compiled from its own sources, oracle/_ref) on the host's cores
 gives its cpu_baseline on the same workload (whole prompt, every token). `prefill` is the
 512-token prompt on the matrix
-cores (MFMA utilisation), `context_sweep` the decode rate after 512..4000-token prompts.
+cores (MFMA utilisation) and the prefill time by prompt length (2..1024 tokens),
+`context_sweep` the decode rate after 512..4000-token prompts.
 """
 from __future__ import annotations
 
@@ -302,6 +303,30 @@ def prefill_run(pkg, preset, threads, n, reps):
     return info, name, statistics.median(dev), statistics.median(wall), first_wall * 1e3 - statistics.median(wall)
 
 
+PF_LENGTHS = (2, 6, 16, 32, 64, 128, 256, 513, 1024)
+
+
+def prefill_lengths(pkg, threads, reps=3):
+    """Prefill time by prompt length on the Llama-3.2-1B shape (Q8_0, max-seq 2048): median
+    device ms (HIP events) of `reps` prefills from a reset, after one of the same prompt."""
+    path, info = ensure_model(pkg, "llama1b_q8", threads)
+    m = pkg.HipModel(path, max_seq=2048, kv_layout=0)
+    out = []
+    for n in PF_LENGTHS:
+        prompt = pkg.synth_prompt(info["seed"] + n, n, info["n_vocab"])
+        m.reset()
+        m.prefill(prompt, want_logits=False)
+        dev = []
+        for _ in range(reps):
+            m.reset()
+            m.prefill(prompt, want_logits=False)
+            dev.append(m.last_timing()[0])
+        d = statistics.median(dev)
+        out.append({"tokens": n, "device_ms": round(d, 3), "tok_s": round(n / (d * 1e-3), 1)})
+    m.close()
+    return out
+
+
 def prefill_leg(pkg, threads, reps=5):
     """The 512-token prompt of the Llama-3.2-1B shape on the matrix cores (Q8_0, and the
     Q4_0 / Q4_1 mix of the same shape), the layer matrices read in their HBM layout."""
@@ -323,6 +348,7 @@ def prefill_leg(pkg, threads, reps=5):
         "mixq4": {"path": name4, "device_ms": round(d4_ms, 3), "wall_ms": round(w4_ms, 3),
                   "tok_s": round(n / (d4_ms * 1e-3), 1),
                   "note": "the same prompt on the Q4_0 layer matrices (Q4_1 ffn_down in layers 0 and 15)"},
+        "by_length": prefill_lengths(pkg, threads),
     }
 
 
