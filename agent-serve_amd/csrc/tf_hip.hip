@@ -665,6 +665,27 @@ int ensure_pf(tf_hip_ctx* c) {
     return 1;
 }
 
+// Rows [r0, r0 + n) of a layer matrix as a matrix of its own: its streams advanced by r0
+// rows (the per-row strides of the DevMat layout of each format, as Fmt<T>::row reads them).
+DevMat devmat_rows(const DevMat& m, int64_t r0, int64_t n) {
+    DevMat d = m;
+    int64_t q = 0, q2 = 0, sc = 0, s2 = 0;  // bytes per row of the q, q2, s and s2 streams
+    switch (m.type) {
+        case TF_HIP_TYPE_Q8_0: q = m.K; sc = m.K / 32 * 2; break;
+        case TF_HIP_TYPE_Q4_0: q = m.K / 2; sc = m.K / 32 * 2; break;
+        case TF_HIP_TYPE_Q4_1: q = m.K / 2; sc = m.K / 32 * 4; break;
+        case TF_HIP_TYPE_Q6_K: q = m.K / 2; q2 = m.K / 4; sc = m.K / 16; s2 = m.K / 256 * 2; break;
+        case TF_HIP_TYPE_F16: q = m.K * 2; break;
+        default: q = m.K * 4; break;  // F32
+    }
+    d.q = m.q ? m.q + r0 * q : nullptr;
+    d.q2 = m.q2 ? m.q2 + r0 * q2 : nullptr;
+    d.s = m.s ? m.s + r0 * sc : nullptr;
+    d.s2 = m.s2 ? m.s2 + r0 * s2 : nullptr;
+    d.N = n;
+    return d;
+}
+
 // n prompt tokens, staged at hist[c->pos ..], through the matrix-core layers in chunks
 // of pf_cap rows; attention of every chunk covers the prompt from c->pos (the reference
 // attends within the prefill call only, attention.cpp:82-111). Ends with the lm_head of
@@ -775,14 +796,41 @@ int prefill_mfma(tf_hip_ctx* c, int n) {
                                         c->prs, c->st));
             }
             {
-                PfGemmArgs a = base(D);
-                a.mode = GEMV_SILU;
-                seg(a, M(TF_HIP_LAYER_GATE), c->ph, F, nullptr);
-                a.seg[0].w2 = mat(c, M(TF_HIP_LAYER_UP));
-                a.split_xa = c->pxa;  // a K-split reduce also splits the hidden rows
-                a.split_rs = c->prs;
+                // gate/up's large tiles (128 output columns) past whole rounds over the CUs: the
+                // columns of the whole rounds in one launch, the rest in a second, which splits
+                // its K to fill the CUs — when the rest is at most half a round (a 640-row chunk:
+                // 255 + 65 tiles instead of two rounds; with more, its slices take a round too)
+                const int cus = device_cu_count(), MT = Mpad % 128 == 0 ? Mpad / 128 : 0;
+                const int ncol = F % 128 == 0 ? F / 128 : 0, n_big = ncol * MT;
+                int ncA = ncol;
+                if (n_big > cus && n_big % cus != 0) {
+                    const int a_cols = n_big / cus * cus / MT;
+                    if ((ncol - a_cols) * MT <= cus / 2) ncA = a_cols;
+                }
+                auto gateup = [&](int c0, int c1, bool fuse, bool* done) {
+                    PfGemmArgs a = base(D);
+                    a.mode = GEMV_SILU;
+                    PfSeg& sg = a.seg[a.n_seg++];
+                    sg.w = devmat_rows(mat(c, M(TF_HIP_LAYER_GATE)), c0, c1 - c0);
+                    sg.w2 = devmat_rows(mat(c, M(TF_HIP_LAYER_UP)), c0, c1 - c0);
+                    sg.y = c->ph + c0;
+                    sg.ldy = F;
+                    sg.bias = nullptr;
+                    sg.sub0 = 0;
+                    a.n_sub = (c1 - c0) / 16;
+                    if (fuse) {  // a K-split reduce also splits the hidden rows
+                        a.split_xa = c->pxa;
+                        a.split_rs = c->prs;
+                    }
+                    chk(launch_pf_gemm(a, c->st, done));
+                };
                 bool done = false;
-                chk(launch_pf_gemm(a, c->st, &done));
+                if (ncA > 0 && ncA < ncol) {
+                    gateup(0, ncA * 128, false, nullptr);
+                    gateup(ncA * 128, F, false, nullptr);
+                } else {
+                    gateup(0, F, true, &done);
+                }
                 if (!done) chk(launch_pf_split(c->ph, F, nullptr, 0.0f, F, nc, Mpad, c->pxa, c->prs, c->st));
             }
             {

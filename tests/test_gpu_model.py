@@ -233,14 +233,16 @@ def test_prefill_paths_agree(pkg, gguf):
         assert rel_err(a, b) <= 1e-4
 
 
-@pytest.mark.parametrize("n_prompt", [2, 16, 17, 32, 33, 64, 65, 129, 257])
+@pytest.mark.parametrize("n_prompt", [2, 16, 17, 32, 33, 64, 65, 129, 257, 2700])
 def test_prefill_prompt_lengths(pkg, gguf, n_prompt):
     """Prompt lengths on either side of every tile shape the matrix-core prefill picks by
     row count (16-, 32- and 64-row register-streamed tiles, chunks padded to 128-row tiles,
-    K split or not): logits, per-layer activations and the greedy stream against the oracle."""
+    K split or not; at 2700 rows gate/up's 264 large tiles run as 242 + 22 in two launches):
+    logits, per-layer activations and the greedy stream against the oracle."""
     info = pkg.synth_preset_info("small_q8")
     prompt = pkg.synth_prompt(info["seed"] + n_prompt, n_prompt, info["n_vocab"])
-    ids, worst, worst_tap, margin = model_parity(pkg, gguf("small_q8"), prompt, 2, 512, 0)
+    max_seq = max(512, n_prompt + 64)
+    ids, worst, worst_tap, margin = model_parity(pkg, gguf("small_q8"), prompt, 2, max_seq, 0)
     print(f"small_q8 {n_prompt}-token prompt: ids {ids} logits {worst:.2e} taps {worst_tap:.2e}")
 
 
