@@ -1186,6 +1186,12 @@ __device__ __forceinline__ float quad_sum(float v) {
 // A V^T fragment's lane l holds dim l % 16 and the 8 keys of P^T's lane l: keys
 // 4 (l / 16) + 0..3 and 16 + 4 (l / 16) + 0..3, the keys whose scores S^T leaves there.
 __host__ __device__ constexpr int attn_rec_bytes(int hd) { return 256 * hd + 512; }
+// A record's LDS buffer in k_pf_attn: whole 1 KiB slots (the DMA granule of a wave)
+__host__ __device__ constexpr int attn_buf_bytes(int hd) { return (attn_rec_bytes(hd) + 1023) / 1024 * 1024; }
+// LDS record buffers of k_pf_attn: one in use, one loading. With two (66 KiB for head size
+// 128) two workgroups share a CU, which measured faster than three or four buffers (loads
+// two or three tiles ahead) with one workgroup per CU.
+constexpr int kAttnBufs = 2;
 
 constexpr int kZeroRow = 1000;  // row exponent of an all-zero row
 
@@ -1267,7 +1273,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_pack_kv(const float* kc, const fl
 
 // Workgroup: QG query blocks of 16 QS queries of one kv head, times its n_rep query
 // heads: wave w takes head w % n_rep of block w / n_rep (4 to 8 waves). Per tile record
-// (staged through LDS, the next one loaded into registers meanwhile) a wave computes, for
+// (loaded into LDS ahead of its use) a wave computes, for
 // each of its 16-query subtiles, S^T of 32 keys (lane l: query l % 16, keys 4 (l / 16) + r
 // and 16 + 4 (l / 16) + r), the online softmax of those scores, and O^T += V^T P^T with
 // P^T straight from the same lanes. Keys run from att_start to the workgroup's last query;
@@ -1278,8 +1284,7 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
                                                  int64_t ldo) {
     extern __shared__ uint4 lds_rec[];
     constexpr int NC = HD / 32, NT = HD / 16;
-    constexpr int RU = attn_rec_bytes(HD) / 16;  // uint4 per record
-    constexpr int PF = (RU + 255) / 256;         // per thread, at least 256 threads
+    constexpr int kSlots = attn_buf_bytes(HD) / 1024, RB = attn_buf_bytes(HD), RBYTES = attn_rec_bytes(HD);
     const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
     const int w = tid >> 6;
     const int g = blockIdx.y, h = g * n_rep + w % n_rep;
@@ -1290,6 +1295,26 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
     const int q_first = __builtin_amdgcn_readfirstlane(pos0 + min(q_base, n - 1));  // the wave's first query
     const int l16 = lane & 15, gq = lane >> 4;
     const float scale = 1.0f / sqrtf((float)HD);
+
+    // Records go straight from global memory into the kAttnBufs LDS buffers
+    // (global_load_lds, 1 KiB per wave instruction), one tile ahead, so no registers hold
+    // records in flight. Wave w loads the record's 1 KiB slots w + nw i, i < dpw: slot
+    // indices past the last re-load it, lanes past the record's end re-read its last 16
+    // bytes into the buffer's padding, and the load past the last tile re-loads it. Load i
+    // (tile min(i, n_tiles - 1)) goes to buffer i % kAttnBufs.
+    const int nw = nthr >> 6, dpw = (kSlots + nw - 1) / nw;
+    const unsigned char* src = recs + (int64_t)g * T * RBYTES;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds_rec;
+    auto issue = [&](int i) {
+        const unsigned char* rec = src + (int64_t)(i < n_tiles ? i : n_tiles - 1) * RBYTES;
+        const uint32_t base = lds0 + (uint32_t)((i % kAttnBufs) * RB);
+        for (int k = 0; k < dpw; ++k) {
+            const int j = min(w + nw * k, kSlots - 1);
+            const int off = min(j * 1024 + lane * 16, RBYTES - 16);
+            lds_dma16((const TF_GLOBAL unsigned char*)rec + off, __builtin_amdgcn_readfirstlane(base + (uint32_t)(j * 1024)));
+        }
+    };
+    for (int i = 0; i < kAttnBufs - 1; ++i) issue(i);
 
     h8_t qh[QS][NC], ql[QS][NC];
     float fq[QS];
@@ -1336,31 +1361,26 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) unit[qs] = 0;
 
-    // two records in flight in registers: a record is loaded two tiles before its use
-    uint4 pa[PF], pb[PF];
-    const uint4* src = (const uint4*)(recs + (int64_t)g * T * attn_rec_bytes(HD));
-    // unconditional loads (tile and index clamped; the stores skip the copies): a load
-    // behind a branch makes the compiler's next wait drain every load in flight, the other
-    // record's included
-    auto gload = [&](uint4 (&pf)[PF], int t) {
-        t = t < n_tiles ? t : n_tiles - 1;  // past the last tile: a re-read, never stored
-#pragma unroll
-        for (int i = 0; i < PF; ++i) {
-            const int idx = tid + i * nthr;
-            pf[i] = gload_u4(src + (int64_t)t * RU + (idx < RU ? idx : RU - 1));
-        }
-    };
-    auto lstore = [&](const uint4 (&pf)[PF], int buf) {
-#pragma unroll
-        for (int i = 0; i < PF; ++i) {
-            const int idx = tid + i * nthr;
-            if (idx < RU) lds_rec[buf * RU + idx] = pf[i];
-        }
-    };
     auto tile = [&](const unsigned char* rec, int t) {
         const h8_t* kf = (const h8_t*)rec;
         const h8_t* vf = (const h8_t*)(rec + 128 * HD);
         const float* fk = (const float*)(rec + 256 * HD);
+        // every K and V fragment of the tile is read up front: the V reads complete under
+        // the q.k MFMAs (the softmax's branches would otherwise leave each pair of them to
+        // be read, and waited for, right before its MFMAs)
+        h8_t kr[NC][2][2], vr[NT][2];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                kr[c][half][0] = kf[(half * NC + c) * 128 + lane];
+                kr[c][half][1] = kf[(half * NC + c) * 128 + 64 + lane];
+            }
+#pragma unroll
+        for (int d = 0; d < NT; ++d) {
+            vr[d][0] = vf[d * 128 + lane];
+            vr[d][1] = vf[d * 128 + 64 + lane];
+        }
         f4_t s[QS][2];
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs) s[qs][0] = s[qs][1] = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
@@ -1368,7 +1388,7 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
         for (int c = 0; c < NC; ++c)
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
-                const h8_t kh = kf[(half * NC + c) * 128 + lane], kl = kf[(half * NC + c) * 128 + 64 + lane];
+                const h8_t kh = kr[c][half][0], kl = kr[c][half][1];
 #pragma unroll
                 for (int qs = 0; qs < QS; ++qs) {
                     f4_t x = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[qs][c], s[qs][half], 0, 0, 0);
@@ -1376,6 +1396,8 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
                     s[qs][half] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[qs][c], x, 0, 0, 0);
                 }
             }
+#pragma unroll
+        for (int d = 0; d < NT; ++d) asm volatile("" : "+v"(vr[d][0]), "+v"(vr[d][1]));
         const float4 k0 = *(const float4*)(fk + 4 * gq), k1 = *(const float4*)(fk + 16 + 4 * gq);
         const float4 v0 = *(const float4*)(fk + kAttnTile + 4 * gq), v1 = *(const float4*)(fk + kAttnTile + 16 + 4 * gq);
         const float fkj[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
@@ -1452,7 +1474,7 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
                 for (int d = 0; d < NT; ++d) acc[qs][d] = acc[qs][d] * resc[qs];
 #pragma unroll
         for (int d = 0; d < NT; ++d) {
-            const h8_t vh = vf[d * 128 + lane], vl = vf[d * 128 + 64 + lane];
+            const h8_t vh = vr[d][0], vl = vr[d][1];
 #pragma unroll
             for (int qs = 0; qs < QS; ++qs) {
                 f4_t x = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[qs], acc[qs][d], 0, 0, 0);
@@ -1462,23 +1484,16 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
         }
     };
 
-    gload(pa, 0);
-    gload(pb, 1);
-    lstore(pa, 0);
-    __syncthreads();
-    for (int t = 0; t < n_tiles; t += 2) {
-        // tile t in buffer 0; pa is free, pb holds tile t + 1
-        gload(pa, t + 2);
-        tile((const unsigned char*)lds_rec, t);
-        if (t + 1 < n_tiles) lstore(pb, 1);
-        __syncthreads();
-        if (t + 1 >= n_tiles) break;
-        // tile t + 1 in buffer 1; pb is free, pa holds tile t + 2
-        gload(pb, t + 3);
-        tile((const unsigned char*)(lds_rec + RU), t + 1);
-        if (t + 2 < n_tiles) lstore(pa, 0);
-        __syncthreads();
+    for (int t = 0; t < n_tiles; ++t) {
+        // this wave's loads of tile t are done (the only ones in flight); the barrier then
+        // makes every wave's done, and every wave has left tile t - 1, whose buffer load
+        // t + 1 takes
+        static_assert(kAttnBufs == 2, "the wait counts no loads issued after tile t's");
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(t + kAttnBufs - 1);
+        tile((const unsigned char*)lds_rec + (t % kAttnBufs) * RB, t);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-loads past the last tile
     // lane holds O[query l16][dims 16 d + 4 gq + 0..3] times 2^unit l_run
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) {
@@ -1842,7 +1857,7 @@ namespace {
 template <int HD, int QS>
 hipError_t launch_attn_t(const float* q, int64_t ldq, const unsigned char* recs, int T, int G, int n_rep, int QG,
                          int n, int pos0, int att_start, float* out, int64_t ldo, hipStream_t st) {
-    const size_t lds = 2 * (size_t)attn_rec_bytes(HD);
+    const size_t lds = kAttnBufs * (size_t)attn_buf_bytes(HD);
     static hipError_t attr = hipFuncSetAttribute((const void*)k_pf_attn<HD, QS>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
