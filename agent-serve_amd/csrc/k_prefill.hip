@@ -1188,9 +1188,9 @@ __device__ __forceinline__ float quad_sum(float v) {
 __host__ __device__ constexpr int attn_rec_bytes(int hd) { return 256 * hd + 512; }
 // A record's LDS buffer in k_pf_attn: whole 1 KiB slots (the DMA granule of a wave)
 __host__ __device__ constexpr int attn_buf_bytes(int hd) { return (attn_rec_bytes(hd) + 1023) / 1024 * 1024; }
-// LDS record buffers of k_pf_attn: one in use, one loading. With two (66 KiB for head size
-// 128) two workgroups share a CU, which measured faster than three or four buffers (loads
-// two or three tiles ahead) with one workgroup per CU.
+// LDS record buffers of k_pf_attn per key-tile stream: one in use, one loading. With two
+// (66 KiB for head size 128) two workgroups share a CU, which measured faster than three or
+// four buffers (loads two or three tiles ahead) with one workgroup per CU.
 constexpr int kAttnBufs = 2;
 
 constexpr int kZeroRow = 1000;  // row exponent of an all-zero row
@@ -1272,13 +1272,16 @@ __global__ __launch_bounds__(kBlock) void k_pf_pack_kv(const float* kc, const fl
 }
 
 // Workgroup: QG query blocks of 16 QS queries of one kv head, times its n_rep query
-// heads: wave w takes head w % n_rep of block w / n_rep (4 to 8 waves). Per tile record
+// heads, times KS key streams: wave w takes head w' % n_rep of block w' / n_rep and the key
+// tiles t = KS i + w / (n_rep QG), w' = w % (n_rep QG) (4 to 8 waves). With KS = 2 the two
+// waves of a head and block each run an online softmax over alternate tiles, which halves
+// the longest block's chain of tiles, and merge through LDS at the end. Per tile record
 // (loaded into LDS ahead of its use) a wave computes, for
 // each of its 16-query subtiles, S^T of 32 keys (lane l: query l % 16, keys 4 (l / 16) + r
 // and 16 + 4 (l / 16) + r), the online softmax of those scores, and O^T += V^T P^T with
 // P^T straight from the same lanes. Keys run from att_start to the workgroup's last query;
 // keys past a query's position score -inf.
-template <int HD, int QS>
+template <int HD, int QS, int KS>
 __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, const unsigned char* recs, int T,
                                                  int n_rep, int QG, int n, int pos0, int att_start, float* out,
                                                  int64_t ldo) {
@@ -1287,34 +1290,37 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
     constexpr int kSlots = attn_buf_bytes(HD) / 1024, RB = attn_buf_bytes(HD), RBYTES = attn_rec_bytes(HD);
     const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
     const int w = tid >> 6;
-    const int g = blockIdx.y, h = g * n_rep + w % n_rep;
+    // waves per key stream, this wave's stream and its place in it
+    const int nhw = n_rep * QG, khalf = KS > 1 ? w / nhw : 0, wq = KS > 1 ? w % nhw : w;
+    const int g = blockIdx.y, h = g * n_rep + wq % n_rep;
     const int blk = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
-    const int q_base = (blk * QG + w / n_rep) * 16 * QS;
+    const int q_base = (blk * QG + wq / n_rep) * 16 * QS;
     const int wg_last = min(n - 1, (blk + 1) * QG * 16 * QS - 1);
     const int n_tiles = (pos0 + wg_last - att_start) / kAttnTile + 1;
     const int q_first = __builtin_amdgcn_readfirstlane(pos0 + min(q_base, n - 1));  // the wave's first query
     const int l16 = lane & 15, gq = lane >> 4;
     const float scale = 1.0f / sqrtf((float)HD);
 
-    // Records go straight from global memory into the kAttnBufs LDS buffers
-    // (global_load_lds, 1 KiB per wave instruction), one tile ahead, so no registers hold
-    // records in flight. Wave w loads the record's 1 KiB slots w + nw i, i < dpw: slot
-    // indices past the last re-load it, lanes past the record's end re-read its last 16
-    // bytes into the buffer's padding, and the load past the last tile re-loads it. Load i
-    // (tile min(i, n_tiles - 1)) goes to buffer i % kAttnBufs.
+    // Records go straight from global memory into the kAttnBufs KS LDS buffers
+    // (global_load_lds, 1 KiB per wave instruction), one step of KS tiles ahead, so no
+    // registers hold records in flight. Wave w loads the record's 1 KiB slots w + nw i,
+    // i < dpw: slot indices past the last re-load it, lanes past the record's end re-read its
+    // last 16 bytes into the buffer's padding, and loads past the last tile re-load it. Load
+    // i (tile min(i, n_tiles - 1)) goes to buffer i % nbuf.
+    const int nbuf = kAttnBufs * KS;
     const int nw = nthr >> 6, dpw = (kSlots + nw - 1) / nw;
     const unsigned char* src = recs + (int64_t)g * T * RBYTES;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds_rec;
     auto issue = [&](int i) {
         const unsigned char* rec = src + (int64_t)(i < n_tiles ? i : n_tiles - 1) * RBYTES;
-        const uint32_t base = lds0 + (uint32_t)((i % kAttnBufs) * RB);
+        const uint32_t base = lds0 + (uint32_t)((i % nbuf) * RB);
         for (int k = 0; k < dpw; ++k) {
             const int j = min(w + nw * k, kSlots - 1);
             const int off = min(j * 1024 + lane * 16, RBYTES - 16);
             lds_dma16((const TF_GLOBAL unsigned char*)rec + off, __builtin_amdgcn_readfirstlane(base + (uint32_t)(j * 1024)));
         }
     };
-    for (int i = 0; i < kAttnBufs - 1; ++i) issue(i);
+    for (int i = 0; i < KS; ++i) issue(i);
 
     h8_t qh[QS][NC], ql[QS][NC];
     float fq[QS];
@@ -1425,12 +1431,15 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
             // scores are in units of log2 (fq carries log2 e): 2^(x - m) is exp of the score
             // difference; every query has a key in tile 0 (att_start <= its position), so
             // m_new is finite from the first tile on
+            // (a second key stream's first tiles can hold no key of a query: m_new stays -inf
+            // and the exps take 0 as the reference, so that alpha and p are 0, not NaN)
             const float m_new = fmaxf(m_run[qs], mt);
-            const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - m_new);  // 0 on the first tile
+            const float m_ref = KS > 1 && m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - m_ref);  // 0 on the first tile
             float ls = 0.0f, x[8], mx = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                p[j] = __builtin_amdgcn_exp2f(p[j] - m_new);  // 0 for a masked key
+                p[j] = __builtin_amdgcn_exp2f(p[j] - m_ref);  // 0 for a masked key
                 ls += p[j];
                 x[j] = p[j] * fvj[j];
                 mx = fmaxf(mx, x[j]);
@@ -1484,16 +1493,65 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
         }
     };
 
-    for (int t = 0; t < n_tiles; ++t) {
-        // this wave's loads of tile t are done (the only ones in flight); the barrier then
-        // makes every wave's done, and every wave has left tile t - 1, whose buffer load
-        // t + 1 takes
-        static_assert(kAttnBufs == 2, "the wait counts no loads issued after tile t's");
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        issue(t + kAttnBufs - 1);
-        tile((const unsigned char*)lds_rec + (t % kAttnBufs) * RB, t);
+    // this wave's loads of a step's tiles are done (the only ones in flight); the barrier
+    // then makes every wave's done, and every wave has left the step before, whose buffers
+    // the loads of the next step take
+    static_assert(kAttnBufs == 2, "the wait counts no loads issued after a step's own");
+    if constexpr (KS == 1) {
+        for (int t = 0; t < n_tiles; ++t) {
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue(t + 1);
+            tile((const unsigned char*)lds_rec + (t % nbuf) * RB, t);
+        }
+    } else {
+        for (int it = 0; it * KS < n_tiles; ++it) {
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+            for (int k = 0; k < KS; ++k) issue(KS * (it + 1) + k);
+            const int t = KS * it + khalf;
+            if (t < n_tiles) tile((const unsigned char*)lds_rec + (t % nbuf) * RB, t);
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-loads past the last tile
+    if constexpr (KS > 1) {
+        // the second stream's waves hand their state (O times 2^unit l, m, l, unit) to the
+        // first's through LDS; O = (A0 2^(m0 - M) + A1 2^(m1 - M)) / (l0 2^(m0 - M) + l1 2^(m1 - M))
+        // with A = acc 2^-unit and M = max(m0, m1) (m0 is finite: tile 0 is the first stream's)
+        constexpr int MW = (4 * NT + 3) * QS;
+        float* mg = (float*)lds_rec;  // [wave of the first stream][lane][MW]
+        __syncthreads();
+        if (khalf == 1) {
+            float* d = mg + ((int64_t)wq * 64 + lane) * MW;
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) {
+#pragma unroll
+                for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) d[(qs * NT + dt) * 4 + r] = acc[qs][dt][r];
+                d[4 * NT * QS + 3 * qs] = m_run[qs];
+                d[4 * NT * QS + 3 * qs + 1] = l_run[qs];
+                d[4 * NT * QS + 3 * qs + 2] = (float)unit[qs];
+            }
+        }
+        __syncthreads();
+        if (khalf == 1) return;
+        const float* sp = mg + ((int64_t)wq * 64 + lane) * MW;
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) {
+            const float m1 = sp[4 * NT * QS + 3 * qs], l1 = sp[4 * NT * QS + 3 * qs + 1];
+            const int u1 = (int)sp[4 * NT * QS + 3 * qs + 2];
+            const float M = fmaxf(m_run[qs], m1);
+            const float f0 = __builtin_amdgcn_exp2f(m_run[qs] - M), f1 = __builtin_amdgcn_exp2f(m1 - M);
+            const float L = fmaf(l_run[qs], f0, l1 * f1);
+            const float c0 = ldexpf(f0 / L, -unit[qs]), c1 = ldexpf(f1 / L, -u1);
+#pragma unroll
+            for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[qs][dt][r] = fmaf(acc[qs][dt][r], c0, sp[(qs * NT + dt) * 4 + r] * c1);
+            l_run[qs] = 1.0f;  // acc now holds the normalised output
+            unit[qs] = 0;
+        }
+    }
     // lane holds O[query l16][dims 16 d + 4 gq + 0..3] times 2^unit l_run
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) {
@@ -1854,16 +1912,16 @@ size_t pf_attn_ws_bytes(int hd, int G, int n_keys) {
 
 namespace {
 
-template <int HD, int QS>
+template <int HD, int QS, int KS>
 hipError_t launch_attn_t(const float* q, int64_t ldq, const unsigned char* recs, int T, int G, int n_rep, int QG,
                          int n, int pos0, int att_start, float* out, int64_t ldo, hipStream_t st) {
-    const size_t lds = kAttnBufs * (size_t)attn_buf_bytes(HD);
-    static hipError_t attr = hipFuncSetAttribute((const void*)k_pf_attn<HD, QS>,
+    const size_t lds = (size_t)kAttnBufs * KS * attn_buf_bytes(HD);
+    static hipError_t attr = hipFuncSetAttribute((const void*)k_pf_attn<HD, QS, KS>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
     const int per_blk = 16 * QS * QG;
-    const dim3 grid((unsigned)((n + per_blk - 1) / per_blk), (unsigned)G), block((unsigned)(64 * n_rep * QG));
-    hipLaunchKernelGGL((k_pf_attn<HD, QS>), grid, block, lds, st, q, ldq, recs, T, n_rep, QG, n, pos0, att_start,
+    const dim3 grid((unsigned)((n + per_blk - 1) / per_blk), (unsigned)G), block((unsigned)(64 * n_rep * QG * KS));
+    hipLaunchKernelGGL((k_pf_attn<HD, QS, KS>), grid, block, lds, st, q, ldq, recs, T, n_rep, QG, n, pos0, att_start,
                        out, ldo);
     return hipGetLastError();
 }
@@ -1880,7 +1938,9 @@ hipError_t launch_attn_hd(const float* q, int64_t ldq, const float* kc, const fl
     // 4 to 8 waves per workgroup, one 16-query subtile per wave (a prompt chunk of 4096
     // rows gives 256 query blocks per kv head)
     const int QG = (4 + n_rep - 1) / n_rep;
-    return launch_attn_t<HD, 1>(q, ldq, recs, T, G, n_rep, QG, n, pos0, att_start, out, ldo, st);
+    // two key streams where the waves of one stream leave room for a second
+    if (2 * n_rep * QG <= 8) return launch_attn_t<HD, 1, 2>(q, ldq, recs, T, G, n_rep, QG, n, pos0, att_start, out, ldo, st);
+    return launch_attn_t<HD, 1, 1>(q, ldq, recs, T, G, n_rep, QG, n, pos0, att_start, out, ldo, st);
 }
 
 }  // namespace
