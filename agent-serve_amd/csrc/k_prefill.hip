@@ -1518,6 +1518,7 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
         // first's through LDS; O = (A0 2^(m0 - M) + A1 2^(m1 - M)) / (l0 2^(m0 - M) + l1 2^(m1 - M))
         // with A = acc 2^-unit and M = max(m0, m1) (m0 is finite: tile 0 is the first stream's)
         constexpr int MW = (4 * NT + 3) * QS;
+        static_assert(4 * 64 * MW * 4 <= 2 * kAttnBufs * attn_buf_bytes(HD), "at most 4 waves per stream");
         float* mg = (float*)lds_rec;  // [wave of the first stream][lane][MW]
         __syncthreads();
         if (khalf == 1) {
