@@ -355,6 +355,7 @@ def test_errors_and_reset(pkg, gguf):
     ("llama1b_mixq4", 6, 64, 512, 0),   # Q4_0 / Q4_1 / Q6_K mix
     ("qwen15b_q8", 64, 16, 8192, 1),    # Qwen2.5-1.5B shape, head-major cache (short prompt)
     ("llama1b_q8", 512, 16, 1024, 0),   # 512-token prompt on the matrix cores, then 16 decode tokens
+    ("llama1b_q8", 513, 8, 1024, 0),    # 513 rows: gate/up's 320 large tiles run as 256 + 64 (K split)
     ("llama1b_mixq4", 512, 16, 1024, 0),  # the same on Q4_0 / Q4_1 layer matrices
 ])
 def test_full_size(pkg, gguf, preset, n_prompt, n_gen, max_seq, layout):
