@@ -1284,7 +1284,7 @@ __global__ __launch_bounds__(kBlock) void k_pf_pack_kv(const float* kc, const fl
 template <int HD, int QS, int KS>
 __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, const unsigned char* recs, int T,
                                                  int n_rep, int QG, int n, int pos0, int att_start, float* out,
-                                                 int64_t ldo) {
+                                                 int64_t ldo, int G) {
     extern __shared__ uint4 lds_rec[];
     constexpr int NC = HD / 32, NT = HD / 16;
     constexpr int kSlots = attn_buf_bytes(HD) / 1024, RB = attn_buf_bytes(HD), RBYTES = attn_rec_bytes(HD);
@@ -1292,8 +1292,11 @@ __global__ __launch_bounds__(512) void k_pf_attn(const float* q, int64_t ldq, co
     const int w = tid >> 6;
     // waves per key stream, this wave's stream and its place in it
     const int nhw = n_rep * QG, khalf = KS > 1 ? w / nhw : 0, wq = KS > 1 ? w % nhw : w;
-    const int g = blockIdx.y, h = g * n_rep + wq % n_rep;
-    const int blk = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
+    // query blocks in order of decreasing length over all kv heads (the kv head fastest), so
+    // the longest start first: 4096-token prompt 38.64 -> 38.34 ms against the heads one
+    // after the other
+    const int g = (int)blockIdx.x % G, h = g * n_rep + wq % n_rep;
+    const int blk = (int)gridDim.x / G - 1 - (int)blockIdx.x / G;
     const int q_base = (blk * QG + wq / n_rep) * 16 * QS;
     const int wg_last = min(n - 1, (blk + 1) * QG * 16 * QS - 1);
     const int n_tiles = (pos0 + wg_last - att_start) / kAttnTile + 1;
@@ -1921,9 +1924,9 @@ hipError_t launch_attn_t(const float* q, int64_t ldq, const unsigned char* recs,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
     const int per_blk = 16 * QS * QG;
-    const dim3 grid((unsigned)((n + per_blk - 1) / per_blk), (unsigned)G), block((unsigned)(64 * n_rep * QG * KS));
+    const dim3 grid((unsigned)((n + per_blk - 1) / per_blk * G)), block((unsigned)(64 * n_rep * QG * KS));
     hipLaunchKernelGGL((k_pf_attn<HD, QS, KS>), grid, block, lds, st, q, ldq, recs, T, n_rep, QG, n, pos0, att_start,
-                       out, ldo);
+                       out, ldo, G);
     return hipGetLastError();
 }
 
