@@ -274,13 +274,15 @@ def test_mixed_format_prefill(pkg, gguf, preset, n_prompt):
         assert rel_err(a, b) <= 1e-4
 
 
-def test_long_prompt_runs_in_chunks(pkg, gguf):
+@pytest.mark.parametrize("n_prompt", [4200, 4097])
+def test_long_prompt_runs_in_chunks(pkg, gguf, n_prompt):
     """A prompt longer than one prefill chunk (4096 rows): later chunks attend to the earlier
-    ones through the cache, as one attn_prefill over the whole prompt does."""
+    ones through the cache, as one attn_prefill over the whole prompt does; 4097 tokens leave
+    a last chunk of one row."""
     info = pkg.synth_preset_info("tiny_q8")
-    prompt = pkg.synth_prompt(info["seed"] + 2, 4200, info["n_vocab"])
+    prompt = pkg.synth_prompt(info["seed"] + 2, n_prompt, info["n_vocab"])
     ids, worst, worst_tap, margin = model_parity(pkg, gguf("tiny_q8"), prompt, 4, 4352, 1)
-    print(f"tiny_q8 4200-token prompt: ids {ids} logits {worst:.2e} taps {worst_tap:.2e}")
+    print(f"tiny_q8 {n_prompt}-token prompt: ids {ids} logits {worst:.2e} taps {worst_tap:.2e}")
 
 
 def test_step_and_graph_agree(pkg, gguf):
